@@ -1,0 +1,136 @@
+/* xdna_hip.h -- C ABI of the MI355X (gfx950) int8 hot path of torch_xdna.
+ *
+ * The reference (AyaSakura-comp/torch-xdna) reaches its device through Python launchers:
+ * `kernels.mm_i8` (torch_xdna/kernels.py:172-192) for the int8 GEMM and Triton-XDNA's
+ * `tl.extra.npu.conv3x3` op (called at torch_xdna/conv.py:78-84, :94-96) for the conv, with the
+ * quantize / dequantize around them done as torch CPU ops (torch_xdna/runtime.py:145-148,
+ * :350-353, :366-374; torch_xdna/conv.py:45-51). This library replaces all of them with HIP
+ * kernels behind plain C entry points: every pointer is device memory the caller owns (torch's
+ * caching allocator in torch_xdna), every size is an element count, every function enqueues on
+ * the given hipStream_t (passed as void*) and returns an int status without synchronizing.
+ *
+ * Status: 0 = success; > 0 = a hipError_t from the launch; < 0 = an XDNA_E* code below. The
+ * message of the last failure on the calling thread is xdna_last_error().
+ *
+ * Layout conventions: matrices are row-major with an explicit leading dimension (elements
+ * between rows). int8 GEMM operands are "K-contiguous": A is [M, K], the weight is [N, K]
+ * (one row per output channel). Operand rows must start on 16-byte boundaries and K must be a
+ * multiple of 16 (the quantize entry points zero-pad K for this). Conv activations are NHWC with
+ * the channel count padded to a multiple of 16 (`c_pad`), conv weights are [Co][9][ci_pad] with
+ * taps in (ky, kx) order.
+ */
+#ifndef XDNA_HIP_H
+#define XDNA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XDNA_ABI_VERSION 1
+
+/* dtype codes */
+#define XDNA_F32 0
+#define XDNA_BF16 1
+#define XDNA_F16 2
+#define XDNA_I8 3
+#define XDNA_U8 4
+#define XDNA_I32 5
+
+/* status codes (negative; positive values are hipError_t) */
+#define XDNA_OK 0
+#define XDNA_EINVAL (-1)
+#define XDNA_EUNSUPPORTED (-2)
+#define XDNA_ENODEV (-3)
+
+/* Library version (XDNA_ABI_VERSION). Replaces the import probe of kernels.available()
+ * (torch_xdna/kernels.py:43-56): a loader checks it before trusting the other symbols. */
+int xdna_abi_version(void);
+
+/* Message of the last non-zero status returned on this thread ("" if none). The reference
+ * surfaces launcher failures as Python exceptions caught at torch_xdna/runtime.py:294-295. */
+const char* xdna_last_error(void);
+
+/* Number of compute units and the gfx architecture of the current device, for launch shaping
+ * and for reports (replaces kernels.unavailable_reason(), torch_xdna/kernels.py:59-60). */
+int xdna_device_info(int* num_cus, int* gfx_major, int* gfx_minor);
+
+/* Per-row symmetric int8 quantization of activations or weights:
+ *   s[r] = max(amax_k |x[r,k]|, 1e-8f) / 127  (IEEE float32 division),
+ *   q[r,k] = clamp(round_half_even(x[r,k] / s[r]), -127, 127),
+ * bit-exact with torch_xdna/runtime.py:145-148 (`_quant_rows`), :366-368 (`linear_int8`) and
+ * :64-65 (`QWeight`). x is [rows, k] of x_dtype (XDNA_F32/BF16/F16) with row stride ld_x; q is
+ * written as [rows, k_pad] with row stride ld_q, columns [k, k_pad) set to 0; s is [rows]. */
+int xdna_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ld_x, int8_t* q,
+                    int64_t ld_q, int64_t k_pad, float* s, void* stream);
+
+/* c[m, n] = sum_k a[m, k] * w[n, k] in exact int32 (int8 x int8 -> int32).
+ * Replaces kernels.mm_i8 + matmul_i8_k (torch_xdna/kernels.py:172-192,
+ * torch_xdna/_triton_kernels.py:6-23) behind runtime._npu_acc (torch_xdna/runtime.py:191-209);
+ * bit-exact with torch._int_mm(xq, w_kn) (torch_xdna/runtime.py:162-163). No padding of M or N
+ * is needed; k % 16 == 0, lda and ldw multiples of 16, ldc >= n. */
+int xdna_gemm_i8_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int32_t* c,
+                     int64_t ldc, int64_t m, int64_t n, int64_t k, void* stream);
+
+/* The W8A8 linear with its dequantize fused into the GEMM epilogue:
+ *   y[m, n] = ((float)acc[m, n] * sx[m]) * sw[n] (+ bias[n]) in float32, each step rounded
+ *   once, then converted to y_dtype (XDNA_F32/BF16/F16, round to nearest even),
+ * the arithmetic of torch_xdna/runtime.py:350-353 / :429-432 (`linear`, `linear_cat`) and
+ * :370-374 (`linear_int8`). bias may be NULL. Same operand rules as xdna_gemm_i8_i32. */
+int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const int8_t* w, int64_t ldw,
+                         const float* sw, const float* bias, void* y, int y_dtype, int64_t ldy,
+                         int64_t m, int64_t n, int64_t k, void* stream);
+
+/* dst[r, :cols] = src[r, :cols], dst[r, cols:cols_pad] = 0 for int8 rows (aligning an int8
+ * activation handed to xdna::linear_i8, torch_xdna/ops.py:49-55, to the 16-byte K rule). */
+int xdna_pad_rows_i8(const int8_t* src, int64_t rows, int64_t cols, int64_t ld_src, int8_t* dst,
+                     int64_t ld_dst, int64_t cols_pad, void* stream);
+
+/* Per-image quantization of an NCHW activation into the conv's NHWC int8 layout:
+ *   sx[b] = max(amax |x[b]|, 1e-8f) / 127 over the whole image (C*H*W values),
+ *   q[b, p, c] = clamp(round_half_even(x[b, c, p] / sx[b]), -127, 127) for c < ch, 0 for
+ *   ch <= c < c_pad, p = y * w + x,
+ * bit-exact with torch_xdna/conv.py:45-46 (`conv3x3_int8`). amax_ws is caller scratch of nb
+ * floats (overwritten). */
+int xdna_conv_quant_nhwc(const void* x, int x_dtype, int64_t nb, int64_t ch, int64_t h, int64_t w,
+                         int8_t* q, int64_t c_pad, float* sx, float* amax_ws, void* stream);
+
+/* Conv weight quantize-once (torch_xdna/conv.py:58-60, `ConvLayer.__init__`):
+ *   sw[o] = max(amax |w[o]|, 1e-8f) / 127 over (Ci, 3, 3); wq = clamp(round(w / sw), +-127),
+ * written in the kernel's layout wq[o][ky*3+kx][c] with ci_pad channels (zeros past ci).
+ * w is [co][ci][3][3] of w_dtype. */
+int xdna_conv_weight_pack(const void* w, int w_dtype, int64_t co, int64_t ci, int8_t* wq, int64_t ci_pad,
+                          float* sw, void* stream);
+
+/* int8 3x3 / stride 1 / padding 1 convolution as an implicit GEMM on MFMA, with the requantize of
+ * torch_xdna/conv.py:89-92 fused: q = sat((acc + (1 << (shift-1))) >> shift) to [0, 255] (uint8)
+ * when relu, else [-128, 127] (int8). Replaces Triton-XDNA's Conv3x3 launch
+ * (torch_xdna/conv.py:78-84, :94-96; kernel math npu_kernels/conv3x3_cascade.cc:24-131).
+ * x: NHWC [nb, h, w, c_pad] int8; wq: [co][9][c_pad]; y: NHWC [nb, h, w, co] (int8 or uint8).
+ * If acc_max is not NULL the launch is a calibration pass (torch_xdna/conv.py:71-75): nothing is
+ * written to y (which may be NULL), shift is ignored, and acc_max[0] receives max(acc, 0) when
+ * relu else max |acc| over all outputs. c_pad % 16 == 0, 1 <= shift <= 31. */
+int xdna_conv3x3_i8(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad, const int8_t* wq,
+                    int64_t co, int shift, int relu, void* y, int32_t* acc_max, void* stream);
+
+/* Conv dequantize back to NCHW (torch_xdna/conv.py:48-51):
+ *   y[b, o, p] = (float)q[b, p, o] * (scale[o] * sx[b]) (+ bias[o]) -> y_dtype,
+ * q NHWC [nb, h*w, co] int8 (uint8 when relu). bias may be NULL. */
+int xdna_conv_dequant(const void* q, int relu, int64_t nb, int64_t h, int64_t w, int64_t co,
+                      const float* scale, const float* sx, const float* bias, void* y, int y_dtype,
+                      void* stream);
+
+/* int8 layout changes for the reference op's NCHW int8 contract (torch_xdna/ops.py:64-76):
+ * NCHW [nb, ch, h, w] -> NHWC [nb, h, w, c_pad] (zero channels past ch), and
+ * NHWC [nb, h, w, ch] -> NCHW [nb, ch, h, w] (one byte per element, int8 or uint8). */
+int xdna_nchw_to_nhwc_i8(const int8_t* src, int64_t nb, int64_t ch, int64_t h, int64_t w, int8_t* dst,
+                         int64_t c_pad, void* stream);
+int xdna_nhwc_to_nchw_i8(const void* src, int64_t nb, int64_t ch, int64_t h, int64_t w, void* dst,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XDNA_HIP_H */

@@ -1,0 +1,183 @@
+"""GPU parity of every C-ABI entry point against the CPU oracle (bit-exact).
+
+Each test calls the HIP library through its ctypes binding (torch_xdna.kernels) on seeded inputs and
+compares with oracle/ (numpy restatement; the C restatement for the larger integer sums):
+  * integers (quantized activations and weights, int32 sums, int8/uint8 conv outputs) bit for bit;
+  * float32 scales and dequantized outputs bit for bit in float32, and bf16 / fp16 outputs bit
+    for bit after the round-to-nearest-even cast (the 1e-6 relative / 1 ulp bound of the contract
+    is not needed: the fused epilogue rounds exactly like the reference's CPU ops).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import c_oracle
+from oracle import xdna_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _f32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _rand(shape, dtype, seed, scale=1.0, outliers=0.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=g) * scale
+    if outliers:
+        x = torch.where(torch.rand(*shape, generator=g) < outliers, x * 20, x)
+    return x.to(dtype)
+
+
+def _i8(shape, seed, lo=-127, hi=128):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi, shape, generator=g, dtype=torch.int8)
+
+
+# ------------------------------------------------------------------------------ quantize
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,k", [(1, 16), (5, 200), (7, 300), (64, 1024), (33, 4096), (3, 14336), (2, 40000),
+                                    (9, 1)])
+def test_quant_rows(gpu, dtype, rows, k):
+    x = _rand((rows, k), DT[dtype], seed=rows * 1000 + k, outliers=1e-3)
+    from torch_xdna import kernels
+
+    xq, sx = kernels.quant_rows(x.to(gpu))
+    q_ref, s_ref = O.quant_rows(_f32(x))
+    k_pad = -(-k // 16) * 16
+    assert xq.shape == (rows, k_pad)
+    assert np.array_equal(_np(xq)[:, :k], q_ref)
+    assert not _np(xq)[:, k:].any()
+    assert np.array_equal(_np(sx).view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_quant_rows_ties_zero_rows_strided(gpu):
+    from torch_xdna import kernels
+
+    # amax 127 makes s == 1 exactly, so x = k + 0.5 are exact ties (round half to even);
+    # amax 254 makes s == 2, so odd integers x are ties too; an all-zero row gives zeros.
+    rows = [[127.0, 2.5, -3.5, 0.5, -0.5, 1.5, 126.5, -126.5] + [0.0] * 8,
+            [254.0, 5.0, -5.0, 7.0, -7.0, 1.0, 3.0, -1.0] + [0.0] * 8,
+            [0.0] * 16]
+    base = torch.tensor(rows, dtype=torch.float32)
+    big = torch.zeros(3, 48)
+    big[:, :16] = base
+    xq, sx = kernels.quant_rows(big.to(gpu)[:, :16])    # a view with row stride 48 != K
+    q_ref, s_ref = O.quant_rows(base.numpy())
+    assert np.array_equal(_np(xq)[:, :16], q_ref)
+    assert np.array_equal(_np(sx), s_ref)
+    assert _np(xq)[0, :8].tolist() == [127, 2, -4, 0, 0, 2, 126, -126]
+    assert _np(xq)[1, :8].tolist() == [127, 2, -2, 4, -4, 0, 2, 0]
+
+
+# ------------------------------------------------------------------------------ int32 GEMM
+GEMM_SHAPES = [(1, 16, 64), (3, 50, 208), (16, 4096, 1024), (64, 1000, 512), (65, 300, 208), (200, 300, 208),
+               (256, 512, 1024), (1000, 777, 96), (2048, 2048, 256), (4096, 4096, 128), (333, 4112, 48)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+def test_gemm_i32(gpu, m, n, k):
+    from torch_xdna import kernels
+
+    a = _i8((m, k), seed=m + 7 * n + 13 * k)
+    w = _i8((n, k), seed=m + 7 * n + 13 * k + 1)
+    c = kernels.mm_i8(a.to(gpu), w.to(gpu))
+    want = c_oracle.gemm_i32(a.numpy(), w.numpy())
+    got = _np(c)
+    assert got.dtype == np.int32 and np.array_equal(got, want), f"{(got != want).sum()} of {got.size} differ"
+
+
+def test_gemm_i32_extremes(gpu):
+    """|sum| up to K * 127^2 with K = 16384 (no int32 overflow, no saturation)."""
+    from torch_xdna import kernels
+
+    k = 16384
+    a = torch.full((20, k), 127, dtype=torch.int8)
+    a[1::2] = -127
+    w = torch.full((33, k), 127, dtype=torch.int8)
+    c = _np(kernels.mm_i8(a.to(gpu), w.to(gpu)))
+    assert c[0, 0] == 127 * 127 * k and c[1, 0] == -127 * 127 * k
+    assert np.array_equal(c, c_oracle.gemm_i32(a.numpy(), w.numpy()))
+
+
+# ------------------------------------------------------------------------------ fused dequant GEMM
+@pytest.mark.parametrize("out", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("m,n,k,bias", [(1, 4096, 1024, True), (16, 1000, 512, False), (128, 3072, 1024, True),
+                                        (300, 520, 1024, True), (700, 300, 208, False), (2048, 1024, 256, True)])
+def test_gemm_dequant(gpu, out, m, n, k, bias):
+    from torch_xdna import kernels
+
+    x = _rand((m, k), torch.float32, seed=m + n + k, outliers=1e-3)
+    wt = _rand((n, k), torch.float32, seed=m + n + k + 1, scale=0.02)
+    b = _rand((n,), torch.float32, seed=m + n + k + 2, scale=0.01) if bias else None
+    xq_r, sx_r = O.quant_rows(x.numpy())
+    wq_r, sw_r = O.quant_rows(wt.numpy())
+    k_pad = -(-k // 16) * 16
+    xq, sx = kernels.quant_rows(x.to(gpu), k_pad)
+    wq, sw = kernels.quant_rows(wt.to(gpu), k_pad)
+    y = kernels.mm_i8_dequant(xq, sx, wq, sw, None if b is None else b.to(gpu), DT[out])
+    acc = c_oracle.gemm_i32(xq_r, wq_r)
+    want = O.to_dtype(O.dequant(acc, sx_r, sw_r, None if b is None else b.numpy()), out)
+    got = _f32(y)
+    bad = ~((got == want) | (np.isnan(got) & np.isnan(want)))
+    assert not bad.any(), f"{bad.sum()} of {got.size} differ, e.g. {got[bad][:4]} vs {want[bad][:4]}"
+
+
+# ------------------------------------------------------------------------------ conv
+def _conv_case(n, ci, co, h, w, seed):
+    x = _rand((n, ci, h, w), torch.float32, seed=seed)
+    wt = _rand((co, ci, 3, 3), torch.float32, seed=seed + 1, scale=0.05)
+    return x, wt
+
+
+@pytest.mark.parametrize("n,ci,co,h,w", [(2, 3, 48, 13, 37), (1, 64, 128, 16, 64), (2, 16, 20, 5, 7),
+                                         (1, 256, 256, 8, 64), (3, 40, 64, 9, 9),
+                                         (1, 32, 256, 64, 256),      # 128x128 tiles
+                                         (1, 16, 256, 256, 256)])    # 256x256 tiles
+@pytest.mark.parametrize("relu", [False, True])
+def test_conv3x3(gpu, n, ci, co, h, w, relu):
+    from torch_xdna import kernels
+
+    x, wt = _conv_case(n, ci, co, h, w, seed=n * 131 + ci * 7 + co + h + w)
+    c_pad = -(-ci // 16) * 16
+    xq, sx = kernels.conv_quant(x.to(gpu), c_pad)
+    wq, sw = kernels.conv_weight_pack(wt.to(gpu), c_pad)
+    xq_r, sx_r = O.conv_quant_images(x.numpy())
+    wq_r, sw_r = O.conv_weight_quant(wt.numpy())
+    # quantize + layout
+    assert np.array_equal(_np(xq)[..., :ci], xq_r.transpose(0, 2, 3, 1)) and not _np(xq)[..., ci:].any()
+    assert np.array_equal(_np(sx), sx_r)
+    assert np.array_equal(_np(wq)[:, :, :ci], wq_r.reshape(co, ci, 9).transpose(0, 2, 1))
+    assert not _np(wq)[:, :, ci:].any() and np.array_equal(_np(sw), sw_r)
+    # calibration on image 0, then the requantized integers
+    acc = c_oracle.conv3x3_acc(xq_r, wq_r)
+    top = kernels.conv3x3_calibrate(xq[:1], wq, relu)
+    want_top = int(np.clip(acc[0], 0, None).max()) if relu else int(np.abs(acc[0]).max())
+    assert top == want_top
+    shift = O.shift_from_top(float(top), relu)
+    q = kernels.conv3x3(xq, wq, shift, relu)
+    want_q = O.requant(acc, shift, relu)
+    got_q = _np(q).transpose(0, 3, 1, 2)
+    assert got_q.dtype == want_q.dtype and np.array_equal(got_q, want_q), f"{(got_q != want_q).sum()} differ"
+    # dequant back to NCHW float
+    scale = O.conv_scale(sw_r, shift)
+    bias = _rand((co,), torch.float32, seed=5, scale=0.1)
+    y = kernels.conv_dequant(q, relu, torch.from_numpy(scale).to(gpu), sx, bias.to(gpu), torch.float32)
+    assert np.array_equal(_np(y), O.conv_dequant(want_q, scale, sx_r, bias.numpy()))
+
+
+def test_conv_layouts(gpu):
+    from torch_xdna import kernels
+
+    xq = _i8((2, 19, 5, 11), seed=3)
+    nhwc = kernels.nchw_to_nhwc(xq.to(gpu), 32)
+    assert np.array_equal(_np(nhwc)[..., :19], xq.numpy().transpose(0, 2, 3, 1)) and not _np(nhwc)[..., 19:].any()
+    q = _i8((2, 5, 11, 21), seed=4)
+    back = kernels.nhwc_to_nchw(q.to(gpu))
+    assert np.array_equal(_np(back), q.numpy().transpose(0, 3, 1, 2))

@@ -1,0 +1,130 @@
+// Shared device helpers and host-side error plumbing for the xdna HIP library (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "xdna_hip.h"
+
+namespace xdna {
+
+// ------------------------------------------------------------------------------ host errors
+// The last failure's message for xdna_last_error(); one per host thread.
+void set_error(const std::string& msg);
+
+#define XDNA_REQUIRE(cond, msg)                                  \
+  do {                                                           \
+    if (!(cond)) {                                               \
+      ::xdna::set_error(std::string(__func__) + ": " + (msg));   \
+      return XDNA_EINVAL;                                        \
+    }                                                            \
+  } while (0)
+
+// Status of the launches just made on this thread (hipGetLastError), as an ABI status.
+int launch_status(const char* where);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+__host__ __device__ inline bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// ------------------------------------------------------------------------------ device types
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// float32 -> bfloat16 bits, round to nearest even (NaN stays a quiet NaN), the rounding torch's
+// `.to(torch.bfloat16)` applies.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// float32 -> float16 bits with round to nearest even (v_cvt_f16_f32 under the default mode).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Element loads of the floating-point input dtypes as float32 (exact widening).
+template <int DT>
+__device__ __forceinline__ float load_as_f32(const void* base, int64_t i);
+
+template <>
+__device__ __forceinline__ float load_as_f32<XDNA_F32>(const void* base, int64_t i) {
+  return reinterpret_cast<const float*>(base)[i];
+}
+template <>
+__device__ __forceinline__ float load_as_f32<XDNA_BF16>(const void* base, int64_t i) {
+  return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
+}
+template <>
+__device__ __forceinline__ float load_as_f32<XDNA_F16>(const void* base, int64_t i) {
+  return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void store_from_f32(void* base, int64_t i, float v);
+
+template <>
+__device__ __forceinline__ void store_from_f32<XDNA_F32>(void* base, int64_t i, float v) {
+  reinterpret_cast<float*>(base)[i] = v;
+}
+template <>
+__device__ __forceinline__ void store_from_f32<XDNA_BF16>(void* base, int64_t i, float v) {
+  reinterpret_cast<uint16_t*>(base)[i] = f32_to_bf16_bits(v);
+}
+template <>
+__device__ __forceinline__ void store_from_f32<XDNA_F16>(void* base, int64_t i, float v) {
+  reinterpret_cast<uint16_t*>(base)[i] = f32_to_f16_bits(v);
+}
+
+// round_half_even(x / s) for |x / s| <= 128, equal to rintf of the correctly rounded float32
+// quotient (what torch.round(x / s) computes). The product with the reciprocal is within 2^-15 of
+// the rounded quotient for these magnitudes, so the two round to the same integer unless the
+// product lies within 2^-14 of a half-integer; only then is the IEEE division done.
+__device__ __forceinline__ float round_div(float x, float s, float r) {
+  float t = x * r;
+  float f = t - floorf(t);
+  if (fabsf(f - 0.5f) < 6.103515625e-05f) t = x / s;
+  return rintf(t);
+}
+
+// Quantized value of x for a row scale s (with r = 1 / s): clamp(round(x / s), -127, 127).
+__device__ __forceinline__ int quant1(float x, float s, float r) {
+  float q = round_div(x, s, r);
+  q = fminf(fmaxf(q, -127.0f), 127.0f);
+  return (int)q;
+}
+
+// The row scale from the row's max |x|: max(amax, 1e-8f) / 127 with IEEE division.
+__device__ __forceinline__ float scale_from_amax(float amax) {
+  float a = amax > 1e-8f ? amax : 1e-8f;
+  if (amax != amax) a = amax;   // NaN propagates as torch.clamp does
+  return a / 127.0f;
+}
+
+// Wavefront (64 lanes) max reduction.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+}  // namespace xdna

@@ -1,0 +1,533 @@
+// Quantize, dequantize and layout kernels of the int8 hot path (gfx950).
+//
+//  * quant_rows: per-row symmetric int8 (torch_xdna/runtime.py:145-148, :366-368, :64-65). One
+//    group of TPR threads per row keeps the row in registers, so the row is read from HBM once:
+//    a coalesced 16-byte-per-lane load, a wavefront max reduction, then the divide/round/clamp.
+//  * conv_quant_nhwc: per-image amax (conv.py:45) as a grid-wide reduction, then the quantize
+//    fused with the NCHW -> NHWC transpose through LDS, so the int8 conv input is written once in
+//    the layout the implicit GEMM reads.
+//  * conv_weight_pack: quantize-once of a conv weight into [Co][9][Ci_pad] (conv.py:58-60).
+//  * conv_dequant: NHWC int8 -> NCHW float with q * (scale[o] * sx[b]) + bias (conv.py:48-50).
+//
+// All floating-point arithmetic here is compiled without contraction (-ffp-contract=off), so
+// every product and sum rounds once as in torch's CPU kernels.
+#include <mutex>
+#include <string>
+
+#include "xdna_common.h"
+
+namespace xdna {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int launch_status(const char* where) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error(std::string(where) + ": " + hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  return XDNA_OK;
+}
+
+// ------------------------------------------------------------------------------ quant_rows
+// 16-byte vector of input elements: 8 x 16-bit or 4 x float32.
+template <int DT>
+struct Vec16 {
+  static constexpr int N = (DT == XDNA_F32) ? 4 : 8;
+  uint4 raw;
+  __device__ __forceinline__ float get(int i) const {
+    if constexpr (DT == XDNA_F32) {
+      const float* f = reinterpret_cast<const float*>(&raw);
+      return f[i];
+    } else {
+      const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
+      if constexpr (DT == XDNA_BF16) return bf16_bits_to_f32(h[i]);
+      else return f16_bits_to_f32(h[i]);
+    }
+  }
+};
+
+template <int TPR>
+__device__ __forceinline__ float group_max(float v, float* red) {
+  v = wave_max(v);
+  if constexpr (TPR == 64) {
+    return v;
+  } else {
+    constexpr int W = TPR / 64;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;          // TPR == blockDim.x for TPR > 64
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int i = 1; i < W; ++i) m = fmaxf(m, red[i]);
+    return m;
+  }
+}
+
+// Vector path: k % VEC == 0, ld_x % VEC == 0, x 16-byte aligned, ld_q % 16 == 0, q aligned.
+// Rows of up to TPR * MAXV vectors stay in registers; longer rows are read twice.
+template <int DT, int TPR, int MAXV>
+__global__ __launch_bounds__(256) void quant_rows_vec_kernel(const void* __restrict__ x, int64_t rows, int64_t k,
+                                                             int64_t ld_x, int8_t* __restrict__ q, int64_t ld_q,
+                                                             int64_t k_pad, float* __restrict__ s) {
+  using V = Vec16<DT>;
+  constexpr int VEC = V::N;
+  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
+  __shared__ float red[4];
+  const int groups = 256 / TPR;
+  const int64_t row = (int64_t)blockIdx.x * groups + threadIdx.x / TPR;
+  const int t = threadIdx.x % TPR;
+  const bool active = row < rows;
+  const int64_t nvec = k / VEC;
+  const char* xr = reinterpret_cast<const char*>(x) + (active ? row : 0) * ld_x * ESZ;
+  int8_t* qr = q + (active ? row : 0) * ld_q;
+
+  V v[MAXV];
+  float amax = 0.0f;
+  const bool cached = nvec <= (int64_t)TPR * MAXV;
+  if (active) {
+    if (cached) {
+#pragma unroll
+      for (int j = 0; j < MAXV; ++j) {
+        int64_t iv = t + (int64_t)j * TPR;
+        if (iv < nvec) v[j].raw = *reinterpret_cast<const uint4*>(xr + iv * 16);
+        else v[j].raw = make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < MAXV; ++j)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) amax = fmaxf(amax, fabsf(v[j].get(e)));
+    } else {
+      for (int64_t iv = t; iv < nvec; iv += TPR) {
+        V u;
+        u.raw = *reinterpret_cast<const uint4*>(xr + iv * 16);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) amax = fmaxf(amax, fabsf(u.get(e)));
+      }
+    }
+  }
+  amax = group_max<TPR>(amax, red);
+  if (!active) return;
+  const float sc = scale_from_amax(amax);
+  const float rc = 1.0f / sc;
+  if (t == 0) s[row] = sc;
+
+  auto emit = [&](const V& u, int64_t iv) {
+    uint32_t w[VEC / 4];
+#pragma unroll
+    for (int g = 0; g < VEC / 4; ++g) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) packed |= ((uint32_t)(uint8_t)(int8_t)quant1(u.get(g * 4 + e), sc, rc)) << (8 * e);
+      w[g] = packed;
+    }
+    if constexpr (VEC == 8) *reinterpret_cast<uint2*>(qr + iv * VEC) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t*>(qr + iv * VEC) = w[0];
+  };
+  if (cached) {
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      int64_t iv = t + (int64_t)j * TPR;
+      if (iv < nvec) emit(v[j], iv);
+    }
+  } else {
+    for (int64_t iv = t; iv < nvec; iv += TPR) {
+      V u;
+      u.raw = *reinterpret_cast<const uint4*>(xr + iv * 16);
+      emit(u, iv);
+    }
+  }
+  for (int64_t c = k + t; c < k_pad; c += TPR) qr[c] = 0;
+}
+
+// Scalar path for any k / stride / alignment: one block per row, the row read twice.
+template <int DT>
+__global__ __launch_bounds__(256) void quant_rows_scalar_kernel(const void* __restrict__ x, int64_t rows, int64_t k,
+                                                                int64_t ld_x, int8_t* __restrict__ q, int64_t ld_q,
+                                                                int64_t k_pad, float* __restrict__ s) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * ld_x;
+  float amax = 0.0f;
+  for (int64_t i = threadIdx.x; i < k; i += 256) amax = fmaxf(amax, fabsf(load_as_f32<DT>(x, base + i)));
+  amax = group_max<256>(amax, red);
+  const float sc = scale_from_amax(amax);
+  const float rc = 1.0f / sc;
+  if (threadIdx.x == 0) s[row] = sc;
+  int8_t* qr = q + row * ld_q;
+  for (int64_t i = threadIdx.x; i < k; i += 256) qr[i] = (int8_t)quant1(load_as_f32<DT>(x, base + i), sc, rc);
+  for (int64_t i = k + threadIdx.x; i < k_pad; i += 256) qr[i] = 0;
+}
+
+template <int DT>
+int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8_t* q, int64_t ld_q, int64_t k_pad,
+                      float* s, hipStream_t st) {
+  constexpr int VEC = (DT == XDNA_F32) ? 4 : 8;
+  const bool vec_ok = (k % VEC == 0) && (ld_x % VEC == 0) && aligned(x, 16) && aligned(q, 16) && (ld_q % 16 == 0);
+  if (!vec_ok) {
+    quant_rows_scalar_kernel<DT><<<dim3((unsigned)rows), 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
+    return launch_status("quant_rows_scalar");
+  }
+  const int64_t nvec = k / VEC;
+  if (nvec <= 64 * 8) {  // one wavefront per row, four rows per block
+    quant_rows_vec_kernel<DT, 64, 8><<<dim3((unsigned)cdiv(rows, 4)), 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
+  } else {               // one block per row
+    quant_rows_vec_kernel<DT, 256, 16><<<dim3((unsigned)rows), 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
+  }
+  return launch_status("quant_rows");
+}
+
+// ------------------------------------------------------------------------------ fills / pads
+__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__global__ void pad_rows_i8_kernel(const int8_t* __restrict__ src, int64_t rows, int64_t cols, int64_t ld_src,
+                                   int8_t* __restrict__ dst, int64_t ld_dst, int64_t cols_pad) {
+  const int64_t row = blockIdx.y;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < cols_pad; c += (int64_t)gridDim.x * blockDim.x)
+    dst[row * ld_dst + c] = c < cols ? src[row * ld_src + c] : (int8_t)0;
+}
+
+// ------------------------------------------------------------------------------ conv quantize
+// Per-image max |x| over nb images of `per` elements: grid (blocks, nb), atomic max on the float
+// bits (order-preserving for non-negative floats) into amax[b], which starts at 0.
+template <int DT>
+__global__ __launch_bounds__(256) void image_absmax_kernel(const void* __restrict__ x, int64_t per,
+                                                           uint32_t* __restrict__ amax_bits) {
+  __shared__ float red[4];
+  const int64_t b = blockIdx.y;
+  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
+  const char* xb = reinterpret_cast<const char*>(x) + b * per * ESZ;
+  float m = 0.0f;
+  const bool vec_ok = ((per * ESZ) % 16 == 0) && aligned(x, 16);
+  if (vec_ok) {
+    using V = Vec16<DT>;
+    const int64_t nvec = per * ESZ / 16;
+    for (int64_t iv = (int64_t)blockIdx.x * 256 + threadIdx.x; iv < nvec; iv += (int64_t)gridDim.x * 256) {
+      V u;
+      u.raw = *reinterpret_cast<const uint4*>(xb + iv * 16);
+#pragma unroll
+      for (int e = 0; e < V::N; ++e) m = fmaxf(m, fabsf(u.get(e)));
+    }
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < per; i += (int64_t)gridDim.x * 256)
+      m = fmaxf(m, fabsf(load_as_f32<DT>(xb, i)));
+  }
+  m = group_max<256>(m, red);
+  if (threadIdx.x == 0) atomicMax(amax_bits + b, __float_as_uint(m));
+}
+
+// Quantize + NCHW -> NHWC: tile of 64 channels x 64 pixels per block (256 threads). Wave w
+// reads channels [w*16, w*16+16) of the tile, lane = pixel, so every global read is 64
+// consecutive pixels of one channel; four channels pack into one LDS word per pixel. The
+// write-out gives each thread 16 channels of one pixel (a 16-byte store).
+template <int DT>
+__global__ __launch_bounds__(256) void conv_quant_nhwc_kernel(const void* __restrict__ x, int64_t ch, int64_t hw,
+                                                              const uint32_t* __restrict__ amax_bits,
+                                                              int8_t* __restrict__ q, int64_t c_pad,
+                                                              float* __restrict__ sx) {
+  __shared__ uint32_t tile[64][17];
+  const int64_t b = blockIdx.z;
+  const int64_t p0 = (int64_t)blockIdx.x * 64;
+  const int64_t c0 = (int64_t)blockIdx.y * 64;
+  const float sc = scale_from_amax(__uint_as_float(amax_bits[b]));
+  const float rc = 1.0f / sc;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) sx[b] = sc;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t p = p0 + lane;
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t c = c0 + wave * 16 + c4 * 4 + e;
+      int qv = 0;
+      if (c < ch && p < hw) qv = quant1(load_as_f32<DT>(x, (b * ch + c) * hw + p), sc, rc);
+      packed |= ((uint32_t)(uint8_t)(int8_t)qv) << (8 * e);
+    }
+    tile[lane][wave * 4 + c4] = packed;
+  }
+  __syncthreads();
+  const int pix = threadIdx.x >> 2;
+  const int part = threadIdx.x & 3;
+  const int64_t po = p0 + pix;
+  const int64_t co = c0 + part * 16;
+  if (po < hw && co < c_pad) {
+    uint4 v = make_uint4(tile[pix][part * 4 + 0], tile[pix][part * 4 + 1], tile[pix][part * 4 + 2],
+                         tile[pix][part * 4 + 3]);
+    *reinterpret_cast<uint4*>(q + (b * hw + po) * c_pad + co) = v;
+  }
+}
+
+// Conv weight quantize-once: one block per output channel.
+template <int DT>
+__global__ __launch_bounds__(256) void conv_weight_pack_kernel(const void* __restrict__ w, int64_t ci,
+                                                               int8_t* __restrict__ wq, int64_t ci_pad,
+                                                               float* __restrict__ sw) {
+  __shared__ float red[4];
+  const int64_t o = blockIdx.x;
+  const int64_t per = ci * 9;
+  const int64_t base = o * per;
+  float m = 0.0f;
+  for (int64_t i = threadIdx.x; i < per; i += 256) m = fmaxf(m, fabsf(load_as_f32<DT>(w, base + i)));
+  m = group_max<256>(m, red);
+  const float sc = scale_from_amax(m);
+  const float rc = 1.0f / sc;
+  if (threadIdx.x == 0) sw[o] = sc;
+  int8_t* out = wq + o * 9 * ci_pad;
+  for (int64_t i = threadIdx.x; i < 9 * ci_pad; i += 256) {
+    const int64_t tap = i / ci_pad, c = i % ci_pad;
+    out[i] = c < ci ? (int8_t)quant1(load_as_f32<DT>(w, base + c * 9 + tap), sc, rc) : (int8_t)0;
+  }
+}
+
+// NHWC q (int8 / uint8) -> NCHW float: y[b, o, p] = (float)q * (scale[o] * sx[b]) (+ bias[o]).
+// Tile of 64 pixels x 64 channels; reads 64 contiguous channel bytes per pixel, writes 64
+// contiguous pixels per channel.
+template <int DT, bool RELU>
+__global__ __launch_bounds__(256) void conv_dequant_kernel(const void* __restrict__ qv, int64_t hw, int64_t co,
+                                                           const float* __restrict__ scale,
+                                                           const float* __restrict__ sx,
+                                                           const float* __restrict__ bias, void* __restrict__ y) {
+  __shared__ uint8_t tile[64][68];
+  const int64_t b = blockIdx.z;
+  const int64_t p0 = (int64_t)blockIdx.x * 64;
+  const int64_t o0 = (int64_t)blockIdx.y * 64;
+  const uint8_t* q = reinterpret_cast<const uint8_t*>(qv);
+  // load: thread -> (pixel t/4, 16 channels)
+  {
+    const int pix = threadIdx.x >> 2;
+    const int part = threadIdx.x & 3;
+    const int64_t p = p0 + pix;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int64_t o = o0 + part * 16 + e;
+      tile[pix][part * 16 + e] = (p < hw && o < co) ? q[(b * hw + p) * co + o] : 0;
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t p = p0 + lane;
+  const float sxb = sx[b];
+  for (int j = 0; j < 16; ++j) {
+    const int oi = wave * 16 + j;
+    const int64_t o = o0 + oi;
+    if (o >= co || p >= hw) continue;
+    const uint8_t raw = tile[lane][oi];
+    const float qf = RELU ? (float)raw : (float)(int8_t)raw;
+    const float f = scale[o] * sxb;
+    float v = qf * f;
+    if (bias) v = v + bias[o];
+    store_from_f32<DT>(y, (b * co + o) * hw + p, v);
+  }
+}
+
+// int8 NCHW -> NHWC with channel padding (tile 64 channels x 64 pixels).
+__global__ __launch_bounds__(256) void nchw_to_nhwc_i8_kernel(const int8_t* __restrict__ src, int64_t ch, int64_t hw,
+                                                              int8_t* __restrict__ dst, int64_t c_pad) {
+  __shared__ int8_t tile[64][80];
+  const int64_t b = blockIdx.z;
+  const int64_t p0 = (int64_t)blockIdx.x * 64;
+  const int64_t c0 = (int64_t)blockIdx.y * 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int j = 0; j < 16; ++j) {
+    const int ci = wave * 16 + j;
+    const int64_t c = c0 + ci, p = p0 + lane;
+    tile[lane][ci] = (c < ch && p < hw) ? src[(b * ch + c) * hw + p] : (int8_t)0;
+  }
+  __syncthreads();
+  const int pix = threadIdx.x >> 2, part = threadIdx.x & 3;
+  const int64_t p = p0 + pix, c = c0 + part * 16;
+  if (p < hw && c < c_pad) {
+    for (int e = 0; e < 16; ++e) dst[(b * hw + p) * c_pad + c + e] = tile[pix][part * 16 + e];
+  }
+}
+
+// int8 NHWC (ch channels, unpadded) -> NCHW.
+__global__ __launch_bounds__(256) void nhwc_to_nchw_i8_kernel(const int8_t* __restrict__ src, int64_t ch, int64_t hw,
+                                                              int8_t* __restrict__ dst) {
+  __shared__ int8_t tile[64][68];
+  const int64_t b = blockIdx.z;
+  const int64_t p0 = (int64_t)blockIdx.x * 64;
+  const int64_t c0 = (int64_t)blockIdx.y * 64;
+  {
+    const int pix = threadIdx.x >> 2, part = threadIdx.x & 3;
+    const int64_t p = p0 + pix;
+    for (int e = 0; e < 16; ++e) {
+      const int64_t c = c0 + part * 16 + e;
+      tile[pix][part * 16 + e] = (p < hw && c < ch) ? src[(b * hw + p) * ch + c] : (int8_t)0;
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t p = p0 + lane;
+  for (int j = 0; j < 16; ++j) {
+    const int ci = wave * 16 + j;
+    const int64_t c = c0 + ci;
+    if (c < ch && p < hw) dst[(b * ch + c) * hw + p] = tile[lane][ci];
+  }
+}
+
+inline bool float_dtype(int dt) { return dt == XDNA_F32 || dt == XDNA_BF16 || dt == XDNA_F16; }
+
+}  // namespace xdna
+
+using namespace xdna;
+
+extern "C" {
+
+int xdna_abi_version(void) { return XDNA_ABI_VERSION; }
+
+const char* xdna_last_error(void) { return g_last_error.c_str(); }
+
+int xdna_device_info(int* num_cus, int* gfx_major, int* gfx_minor) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error(std::string("xdna_device_info: ") + hipGetErrorString(e));
+    return XDNA_ENODEV;
+  }
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) {
+    set_error(std::string("xdna_device_info: ") + hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  if (num_cus) *num_cus = prop.multiProcessorCount;
+  if (gfx_major) *gfx_major = prop.major;
+  if (gfx_minor) *gfx_minor = prop.minor;
+  return XDNA_OK;
+}
+
+int xdna_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ld_x, int8_t* q, int64_t ld_q,
+                    int64_t k_pad, float* s, void* stream) {
+  XDNA_REQUIRE(float_dtype(x_dtype), "x_dtype must be XDNA_F32, XDNA_BF16 or XDNA_F16");
+  XDNA_REQUIRE(rows >= 0 && k >= 1 && ld_x >= k && k_pad >= k && ld_q >= k_pad, "bad sizes");
+  XDNA_REQUIRE(rows < (1ll << 31), "rows must be < 2^31");
+  if (rows == 0) return XDNA_OK;
+  XDNA_REQUIRE(x && q && s, "null pointer");
+  hipStream_t st = as_stream(stream);
+  switch (x_dtype) {
+    case XDNA_F32: return launch_quant_rows<XDNA_F32>(x, rows, k, ld_x, q, ld_q, k_pad, s, st);
+    case XDNA_BF16: return launch_quant_rows<XDNA_BF16>(x, rows, k, ld_x, q, ld_q, k_pad, s, st);
+    default: return launch_quant_rows<XDNA_F16>(x, rows, k, ld_x, q, ld_q, k_pad, s, st);
+  }
+}
+
+int xdna_pad_rows_i8(const int8_t* src, int64_t rows, int64_t cols, int64_t ld_src, int8_t* dst, int64_t ld_dst,
+                     int64_t cols_pad, void* stream) {
+  XDNA_REQUIRE(rows >= 0 && cols >= 0 && ld_src >= cols && cols_pad >= cols && ld_dst >= cols_pad, "bad sizes");
+  XDNA_REQUIRE(rows < 65536 * 1024ll, "too many rows");
+  if (rows == 0 || cols_pad == 0) return XDNA_OK;
+  unsigned bx = (unsigned)std::min<int64_t>(cdiv(cols_pad, 256), 64);
+  dim3 grid(bx, 1, 1);
+  for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+    const int64_t r = std::min<int64_t>(65535, rows - r0);
+    grid.y = (unsigned)r;
+    pad_rows_i8_kernel<<<grid, 256, 0, as_stream(stream)>>>(src + r0 * ld_src, r, cols, ld_src, dst + r0 * ld_dst,
+                                                           ld_dst, cols_pad);
+  }
+  return launch_status("pad_rows_i8");
+}
+
+int xdna_conv_quant_nhwc(const void* x, int x_dtype, int64_t nb, int64_t ch, int64_t h, int64_t w, int8_t* q,
+                         int64_t c_pad, float* sx, float* amax_ws, void* stream) {
+  XDNA_REQUIRE(float_dtype(x_dtype), "x_dtype must be XDNA_F32, XDNA_BF16 or XDNA_F16");
+  XDNA_REQUIRE(nb >= 0 && ch >= 1 && h >= 1 && w >= 1 && c_pad >= ch && c_pad % 16 == 0, "bad sizes");
+  XDNA_REQUIRE(nb < 65536, "batch must be < 65536");
+  if (nb == 0) return XDNA_OK;
+  XDNA_REQUIRE(x && q && sx && amax_ws, "null pointer");
+  XDNA_REQUIRE(aligned(q, 16), "q must be 16-byte aligned");
+  hipStream_t st = as_stream(stream);
+  const int64_t hw = h * w, per = ch * hw;
+  uint32_t* bits = reinterpret_cast<uint32_t*>(amax_ws);
+  fill_u32_kernel<<<dim3((unsigned)cdiv(nb, 256)), 256, 0, st>>>(bits, nb, 0u);
+  const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(per, 256 * 16), 1024));
+  dim3 g1(blocks, (unsigned)nb, 1);
+  dim3 g2((unsigned)cdiv(hw, 64), (unsigned)cdiv(c_pad, 64), (unsigned)nb);
+  XDNA_REQUIRE(cdiv(hw, 64) < (1ll << 31) && cdiv(c_pad, 64) < 65536, "image too large");
+  switch (x_dtype) {
+    case XDNA_F32:
+      image_absmax_kernel<XDNA_F32><<<g1, 256, 0, st>>>(x, per, bits);
+      conv_quant_nhwc_kernel<XDNA_F32><<<g2, 256, 0, st>>>(x, ch, hw, bits, q, c_pad, sx);
+      break;
+    case XDNA_BF16:
+      image_absmax_kernel<XDNA_BF16><<<g1, 256, 0, st>>>(x, per, bits);
+      conv_quant_nhwc_kernel<XDNA_BF16><<<g2, 256, 0, st>>>(x, ch, hw, bits, q, c_pad, sx);
+      break;
+    default:
+      image_absmax_kernel<XDNA_F16><<<g1, 256, 0, st>>>(x, per, bits);
+      conv_quant_nhwc_kernel<XDNA_F16><<<g2, 256, 0, st>>>(x, ch, hw, bits, q, c_pad, sx);
+  }
+  return launch_status("conv_quant_nhwc");
+}
+
+int xdna_conv_weight_pack(const void* w, int w_dtype, int64_t co, int64_t ci, int8_t* wq, int64_t ci_pad, float* sw,
+                          void* stream) {
+  XDNA_REQUIRE(float_dtype(w_dtype), "w_dtype must be XDNA_F32, XDNA_BF16 or XDNA_F16");
+  XDNA_REQUIRE(co >= 1 && ci >= 1 && ci_pad >= ci && ci_pad % 16 == 0 && co < (1ll << 31), "bad sizes");
+  XDNA_REQUIRE(w && wq && sw, "null pointer");
+  hipStream_t st = as_stream(stream);
+  switch (w_dtype) {
+    case XDNA_F32: conv_weight_pack_kernel<XDNA_F32><<<dim3((unsigned)co), 256, 0, st>>>(w, ci, wq, ci_pad, sw); break;
+    case XDNA_BF16: conv_weight_pack_kernel<XDNA_BF16><<<dim3((unsigned)co), 256, 0, st>>>(w, ci, wq, ci_pad, sw); break;
+    default: conv_weight_pack_kernel<XDNA_F16><<<dim3((unsigned)co), 256, 0, st>>>(w, ci, wq, ci_pad, sw);
+  }
+  return launch_status("conv_weight_pack");
+}
+
+int xdna_conv_dequant(const void* q, int relu, int64_t nb, int64_t h, int64_t w, int64_t co, const float* scale,
+                      const float* sx, const float* bias, void* y, int y_dtype, void* stream) {
+  XDNA_REQUIRE(float_dtype(y_dtype), "y_dtype must be XDNA_F32, XDNA_BF16 or XDNA_F16");
+  XDNA_REQUIRE(nb >= 0 && h >= 1 && w >= 1 && co >= 1 && nb < 65536, "bad sizes");
+  if (nb == 0) return XDNA_OK;
+  XDNA_REQUIRE(q && scale && sx && y, "null pointer");
+  const int64_t hw = h * w;
+  XDNA_REQUIRE(cdiv(co, 64) < 65536, "too many channels");
+  dim3 g((unsigned)cdiv(hw, 64), (unsigned)cdiv(co, 64), (unsigned)nb);
+  hipStream_t st = as_stream(stream);
+#define XDNA_DQ(DT)                                                                                   \
+  if (relu) conv_dequant_kernel<DT, true><<<g, 256, 0, st>>>(q, hw, co, scale, sx, bias, y);       \
+  else conv_dequant_kernel<DT, false><<<g, 256, 0, st>>>(q, hw, co, scale, sx, bias, y);
+  switch (y_dtype) {
+    case XDNA_F32: XDNA_DQ(XDNA_F32) break;
+    case XDNA_BF16: XDNA_DQ(XDNA_BF16) break;
+    default: XDNA_DQ(XDNA_F16)
+  }
+#undef XDNA_DQ
+  return launch_status("conv_dequant");
+}
+
+int xdna_nchw_to_nhwc_i8(const int8_t* src, int64_t nb, int64_t ch, int64_t h, int64_t w, int8_t* dst, int64_t c_pad,
+                         void* stream) {
+  XDNA_REQUIRE(nb >= 0 && ch >= 1 && h >= 1 && w >= 1 && c_pad >= ch && c_pad % 16 == 0 && nb < 65536, "bad sizes");
+  if (nb == 0) return XDNA_OK;
+  XDNA_REQUIRE(src && dst, "null pointer");
+  const int64_t hw = h * w;
+  dim3 g((unsigned)cdiv(hw, 64), (unsigned)cdiv(c_pad, 64), (unsigned)nb);
+  nchw_to_nhwc_i8_kernel<<<g, 256, 0, as_stream(stream)>>>(src, ch, hw, dst, c_pad);
+  return launch_status("nchw_to_nhwc_i8");
+}
+
+int xdna_nhwc_to_nchw_i8(const void* src, int64_t nb, int64_t ch, int64_t h, int64_t w, void* dst, void* stream) {
+  XDNA_REQUIRE(nb >= 0 && ch >= 1 && h >= 1 && w >= 1 && nb < 65536, "bad sizes");
+  if (nb == 0) return XDNA_OK;
+  XDNA_REQUIRE(src && dst, "null pointer");
+  const int64_t hw = h * w;
+  dim3 g((unsigned)cdiv(hw, 64), (unsigned)cdiv(ch, 64), (unsigned)nb);
+  nhwc_to_nchw_i8_kernel<<<g, 256, 0, as_stream(stream)>>>(reinterpret_cast<const int8_t*>(src), ch, hw,
+                                                           reinterpret_cast<int8_t*>(dst));
+  return launch_status("nhwc_to_nchw_i8");
+}
+
+}  // extern "C"

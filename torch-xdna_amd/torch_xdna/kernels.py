@@ -1,0 +1,320 @@
+"""The GPU side: the HIP library `_lib/libxdna_hip.so` (gfx950) through its C ABI.
+
+Mirrors the role of the reference's NPU interface (torch_xdna/kernels.py in the reference):
+`available()` / `unavailable_reason()` / `mark_broken()` decide whether the device may be used,
+and one module-level launcher per kernel family (`mm_i8` and friends) does a launch, so tests can
+monkeypatch a launcher exactly as the reference's tests patch `kernels.mm_i8`
+(tests/test_backend.py:139-146, :165-168).
+
+Every launcher takes torch tensors on one GPU, allocates its outputs with torch's caching
+allocator on that device, enqueues on torch's current stream and returns without synchronizing.
+A non-zero status from the library raises RuntimeError with the library's message. There is no
+CPU fallback in this module: if the library is missing, the launchers raise.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libxdna_hip.so")
+ABI_VERSION = 1
+
+F32, BF16, F16 = 0, 1, 2
+_DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+_lock = threading.RLock()
+_state = {"ok": None, "error": None}
+_lib = None
+_cus = {}
+
+
+def round_up(x, m):
+    return -(-x // m) * m
+
+
+# ------------------------------------------------------------------------------ availability
+def available() -> bool:
+    """True if xdna ops can run on the GPU in this process (library loads, a GPU is visible)."""
+    with _lock:
+        if _state["ok"] is None:
+            try:
+                for var in ("TORCH_XDNA_DISABLE_GPU", "TORCH_XDNA_DISABLE_NPU"):
+                    if os.environ.get(var) == "1":
+                        raise RuntimeError(f"disabled by {var}=1")
+                lib()
+                if not torch.cuda.is_available():
+                    raise RuntimeError("no GPU visible to torch (torch.cuda.is_available() is False)")
+                _state["ok"] = True
+            except Exception as e:  # any missing piece means: no GPU route
+                _state["ok"], _state["error"] = False, f"{type(e).__name__}: {e}"
+        return _state["ok"]
+
+
+def unavailable_reason():
+    return _state["error"]
+
+
+def mark_broken(err: BaseException):
+    """Launches kept failing: stop routing to the GPU for the rest of the process."""
+    with _lock:
+        _state["ok"], _state["error"] = False, f"{type(err).__name__}: {err}"
+
+
+def reset():
+    """Forget the availability decision (tests and env changes)."""
+    with _lock:
+        _state["ok"], _state["error"] = None, None
+
+
+def lib():
+    """The loaded library; raises if it is not built or its ABI version differs."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(f"HIP library not built: {LIB_PATH} (run `make -C torch-xdna_amd` "
+                                   "or __graft_entry__.build())")
+            L = ctypes.CDLL(LIB_PATH)
+            L.xdna_abi_version.restype = ctypes.c_int
+            got = L.xdna_abi_version()
+            if got != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH} has ABI version {got}, expected {ABI_VERSION}")
+            _declare(L)
+            _lib = L
+        return _lib
+
+
+def _declare(L):
+    p, i64, i = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    sig = {
+        "xdna_last_error": ([], ctypes.c_char_p),
+        "xdna_device_info": ([p, p, p], i),
+        "xdna_quant_rows": ([p, i, i64, i64, i64, p, i64, i64, p, p], i),
+        "xdna_gemm_i8_i32": ([p, i64, p, i64, p, i64, i64, i64, i64, p], i),
+        "xdna_gemm_i8_dequant": ([p, i64, p, p, i64, p, p, p, i, i64, i64, i64, i64, p], i),
+        "xdna_pad_rows_i8": ([p, i64, i64, i64, p, i64, i64, p], i),
+        "xdna_conv_quant_nhwc": ([p, i, i64, i64, i64, i64, p, i64, p, p, p], i),
+        "xdna_conv_weight_pack": ([p, i, i64, i64, p, i64, p, p], i),
+        "xdna_conv3x3_i8": ([p, i64, i64, i64, i64, p, i64, i, i, p, p, p], i),
+        "xdna_conv_dequant": ([p, i, i64, i64, i64, i64, p, p, p, p, i, p], i),
+        "xdna_nchw_to_nhwc_i8": ([p, i64, i64, i64, i64, p, i64, p], i),
+        "xdna_nhwc_to_nchw_i8": ([p, i64, i64, i64, i64, p, p], i),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes, f.restype = args, res
+
+
+EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
+           "xdna_gemm_i8_dequant", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc", "xdna_conv_weight_pack",
+           "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_nchw_to_nhwc_i8", "xdna_nhwc_to_nchw_i8")
+
+
+def _check(status, what):
+    if status != 0:
+        msg = lib().xdna_last_error().decode(errors="replace")
+        raise RuntimeError(f"xdna {what} failed (status {status}): {msg}")
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _need_gpu(*ts):
+    dev = ts[0].device
+    for t in ts:
+        if t is not None and (t.device.type != "cuda" or t.device != dev):
+            raise ValueError(f"xdna launchers take tensors on one GPU, got {t.device} and {dev}")
+    return dev
+
+
+def num_cus(dev) -> int:
+    """Compute units of the device (the library's launch shaping uses the same figure)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _cus:
+        n, a, b = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        with torch.cuda.device(idx):
+            _check(lib().xdna_device_info(ctypes.byref(n), ctypes.byref(a), ctypes.byref(b)), "device_info")
+        _cus[idx] = n.value
+    return _cus[idx]
+
+
+def gemm_variant(dev, M, N) -> str:
+    """Which GEMM kernel the library runs for M x N (mirrors launch_mm's choice): one NPU-program
+    key of the reference (runtime.py:207) corresponds to one (variant, N, K) here."""
+    if M <= 64:
+        return "small"
+    cus = num_cus(dev)
+    tiles = lambda bm, bn: -(-M // bm) * -(-N // bn)  # noqa: E731
+    if M >= 256 and N >= 256 and tiles(256, 256) >= cus:
+        return "t256"
+    if M >= 128 and N >= 128 and tiles(128, 128) >= cus:
+        return "t128"
+    return "t64"
+
+
+# ------------------------------------------------------------------------------ launchers
+def quant_rows(x2d, k_pad=None):
+    """(xq int8 [R, k_pad], sx float32 [R]) of a [R, K] float tensor (bf16/fp16/fp32), K zero-padded
+    to k_pad (default: the next multiple of 16). Same integers and scales as
+    `torch.round(x.float() / s).clamp(-127, 127)` with s = amax.clamp(1e-8) / 127."""
+    dev = _need_gpu(x2d)
+    if x2d.dtype not in _DTYPE_CODE:
+        raise TypeError(f"quant_rows takes float32/bfloat16/float16, got {x2d.dtype}")
+    R, K = x2d.shape
+    if x2d.stride(1) != 1:
+        x2d = x2d.contiguous()
+    k_pad = round_up(K, 16) if k_pad is None else k_pad
+    xq = torch.empty((R, k_pad), dtype=torch.int8, device=dev)
+    sx = torch.empty((R,), dtype=torch.float32, device=dev)
+    if R:
+        with torch.cuda.device(dev):
+            _check(lib().xdna_quant_rows(_ptr(x2d), _DTYPE_CODE[x2d.dtype], R, K, x2d.stride(0), _ptr(xq), k_pad,
+                                         k_pad, _ptr(sx), _stream(dev)), "quant_rows")
+    return xq, sx
+
+
+def pad_k(xq, k_pad):
+    """An int8 [R, K] tensor as [R, k_pad] with 16-byte aligned rows (copy only when needed)."""
+    dev = _need_gpu(xq)
+    R, K = xq.shape
+    if K == k_pad and xq.stride(1) == 1 and xq.stride(0) % 16 == 0 and xq.data_ptr() % 16 == 0:
+        return xq
+    if xq.stride(1) != 1:
+        xq = xq.contiguous()
+    out = torch.empty((R, k_pad), dtype=torch.int8, device=dev)
+    if R:
+        with torch.cuda.device(dev):
+            _check(lib().xdna_pad_rows_i8(_ptr(xq), R, K, xq.stride(0), _ptr(out), k_pad, k_pad, _stream(dev)),
+                   "pad_rows_i8")
+    return out
+
+
+def mm_i8(a, w, out=None):
+    """c [M, N] int32 = a [M, Kp] @ w [N, Kp]^T, int8 operands with 16-byte aligned rows, Kp % 16 == 0
+    (the role of the reference's kernels.mm_i8, without its padding rules)."""
+    dev = _need_gpu(a, w)
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"mm_i8: K mismatch {a.shape} vs {w.shape}")
+    c = torch.empty((M, N), dtype=torch.int32, device=dev) if out is None else out
+    if M and N:
+        with torch.cuda.device(dev):
+            _check(lib().xdna_gemm_i8_i32(_ptr(a), a.stride(0), _ptr(w), w.stride(0), _ptr(c), c.stride(0), M, N, K,
+                                          _stream(dev)), "gemm_i8_i32")
+    return c
+
+
+def mm_i8_dequant(a, sx, w, sw, bias, out_dtype):
+    """y [M, N] = ((float(a @ w^T) * sx[:, None]) * sw[None, :] + bias) as out_dtype, in one kernel."""
+    dev = _need_gpu(a, sx, w, sw, bias)
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"mm_i8_dequant: K mismatch {a.shape} vs {w.shape}")
+    y = torch.empty((M, N), dtype=out_dtype, device=dev)
+    if M and N:
+        with torch.cuda.device(dev):
+            _check(lib().xdna_gemm_i8_dequant(_ptr(a), a.stride(0), _ptr(sx), _ptr(w), w.stride(0), _ptr(sw),
+                                              _ptr(bias), _ptr(y), _DTYPE_CODE[out_dtype], y.stride(0), M, N, K,
+                                              _stream(dev)), "gemm_i8_dequant")
+    return y
+
+
+def conv_quant(x, c_pad):
+    """Per-image int8 of an NCHW float x -> (xq NHWC [N, H, W, c_pad] int8, sx float32 [N])."""
+    dev = _need_gpu(x)
+    x = x.contiguous()
+    n, c, h, w = x.shape
+    xq = torch.empty((n, h, w, c_pad), dtype=torch.int8, device=dev)
+    sx = torch.empty((n,), dtype=torch.float32, device=dev)
+    ws = torch.empty((n,), dtype=torch.float32, device=dev)
+    if n:
+        with torch.cuda.device(dev):
+            _check(lib().xdna_conv_quant_nhwc(_ptr(x), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(xq), c_pad, _ptr(sx),
+                                              _ptr(ws), _stream(dev)), "conv_quant_nhwc")
+    return xq, sx
+
+
+def conv_weight_pack(weight, ci_pad):
+    """Quantize-once of a [Co, Ci, 3, 3] weight on its GPU -> (wq [Co, 9, ci_pad] int8, sw [Co])."""
+    dev = _need_gpu(weight)
+    wt = weight.detach().contiguous()
+    if wt.dtype not in _DTYPE_CODE:
+        wt = wt.float()
+    co, ci = wt.shape[:2]
+    wq = torch.empty((co, 9, ci_pad), dtype=torch.int8, device=dev)
+    sw = torch.empty((co,), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib().xdna_conv_weight_pack(_ptr(wt), _DTYPE_CODE[wt.dtype], co, ci, _ptr(wq), ci_pad, _ptr(sw),
+                                           _stream(dev)), "conv_weight_pack")
+    return wq, sw
+
+
+def conv3x3(xq, wq, shift, relu):
+    """int8 NHWC [N, H, W, c_pad] (*) wq [Co, 9, c_pad] -> NHWC [N, H, W, Co] int8 (uint8 if relu),
+    requantized by `shift` with round half up and saturation."""
+    dev = _need_gpu(xq, wq)
+    n, h, w, c_pad = xq.shape
+    co = wq.shape[0]
+    y = torch.empty((n, h, w, co), dtype=torch.uint8 if relu else torch.int8, device=dev)
+    if n:
+        with torch.cuda.device(dev):
+            _check(lib().xdna_conv3x3_i8(_ptr(xq), n, h, w, c_pad, _ptr(wq), co, int(shift), int(bool(relu)),
+                                         _ptr(y), None, _stream(dev)), "conv3x3_i8")
+    return y
+
+
+def conv3x3_calibrate(xq, wq, relu):
+    """max(acc, 0) (relu) or max |acc| over the int32 sums of NHWC xq; synchronizes (first call only)."""
+    dev = _need_gpu(xq, wq)
+    n, h, w, c_pad = xq.shape
+    co = wq.shape[0]
+    top = torch.empty((1,), dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib().xdna_conv3x3_i8(_ptr(xq), n, h, w, c_pad, _ptr(wq), co, 1, int(bool(relu)), None, _ptr(top),
+                                     _stream(dev)), "conv3x3_i8 (calibrate)")
+    return int(top.item())
+
+
+def conv_dequant(q, relu, scale, sx, bias, out_dtype):
+    """NHWC q [N, H, W, Co] -> NCHW y = q * (scale[co] * sx[n]) (+ bias[co]) as out_dtype."""
+    dev = _need_gpu(q, scale, sx, bias)
+    n, h, w, co = q.shape
+    y = torch.empty((n, co, h, w), dtype=out_dtype, device=dev)
+    if n:
+        with torch.cuda.device(dev):
+            _check(lib().xdna_conv_dequant(_ptr(q), int(bool(relu)), n, h, w, co, _ptr(scale), _ptr(sx), _ptr(bias),
+                                           _ptr(y), _DTYPE_CODE[out_dtype], _stream(dev)), "conv_dequant")
+    return y
+
+
+def nchw_to_nhwc(xq, c_pad):
+    """int8 NCHW [N, C, H, W] -> NHWC [N, H, W, c_pad] (zero channels past C)."""
+    dev = _need_gpu(xq)
+    xq = xq.contiguous()
+    n, c, h, w = xq.shape
+    out = torch.empty((n, h, w, c_pad), dtype=torch.int8, device=dev)
+    if n:
+        with torch.cuda.device(dev):
+            _check(lib().xdna_nchw_to_nhwc_i8(_ptr(xq), n, c, h, w, _ptr(out), c_pad, _stream(dev)), "nchw_to_nhwc")
+    return out
+
+
+def nhwc_to_nchw(q):
+    """NHWC [N, H, W, C] (int8 or uint8) -> NCHW [N, C, H, W] of the same dtype."""
+    dev = _need_gpu(q)
+    q = q.contiguous()
+    n, h, w, c = q.shape
+    out = torch.empty((n, c, h, w), dtype=q.dtype, device=dev)
+    if n:
+        with torch.cuda.device(dev):
+            _check(lib().xdna_nhwc_to_nchw_i8(_ptr(q), n, c, h, w, _ptr(out), _stream(dev)), "nhwc_to_nchw")
+    return out
