@@ -1,0 +1,379 @@
+"""Benchmark of the int8 hot path on one MI355X: W8A8 GEMM and int8 conv3x3 TOPS vs the rooflines.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c1|c3|c4|c5|quant]
+
+One step is one pass of the hot path over one batch of synthetic, seeded input (BASELINE.json
+configs; seed 0), with inputs and device-resident int8 weights already in HBM:
+
+  c2 (default)  Qwen3-0.6B projections as xdna::linear_cat runs them on the GPU: for M in
+                {128, 512, 1024, 3000}, bf16 x -> quantize -> int8 MFMA GEMM with the fused
+                dequantize epilogue -> bf16, for qkv (N 4096, K 1024), gate/up (N 6144, K 1024) and
+                down (N 1024, K 3072): 12 GEMMs + 12 quantizes per step.
+  c1            one W8A8 linear, fp32 x [128, 1024], W [3072, 1024], bias.
+  c3            4 x (conv3x3 + ReLU), 256 ch, 1x256x64x64, quantize -> conv -> dequantize per layer.
+  c4            conv3x3 256->256 on 1x256x1536x64 (int8 conv kernel, the shift already fixed).
+  c5            W8A8 GEMM, bf16 in/out with bias, K 4096 N 14336 M 8192 (the largest config).
+  quant         the activation quantize kernel alone, bf16 [8192, 14336].
+
+Weight / activation sets are rotated so a step's working set exceeds the 256 MB MALL. Timing:
+W untimed steps, then K steps bracketed by torch.cuda.synchronize(); the dominant kernel is also
+timed per launch with HIP events on the stream it runs on (torch's current stream). Rank 0 prints
+one JSON line. The CPU baseline is the reference's CPU route (oracle/cpu_route.py: torch CPU
+quantize, torch._int_mm or an exact float conv, dequantize) timed on the host cores on a bounded
+sample of the same workload.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "torch-xdna_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+from torch_xdna import kernels  # noqa: E402
+
+PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, TOP/s (5.0 POP/s)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "quant"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+class Timer:
+    """Per-launch HIP-event timing of one kernel family on torch's current stream."""
+
+    def __init__(self):
+        self.pairs = []
+
+    def __call__(self, fn, *a):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        out = fn(*a)
+        e.record()
+        self.pairs.append((s, e))
+        return out
+
+    def ms(self):
+        torch.cuda.synchronize()
+        return [s.elapsed_time(e) for s, e in self.pairs]
+
+
+# ------------------------------------------------------------------------------ GEMM workloads
+def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed=0):
+    """Per set: for each (M, N, K): x [M, K], quantized weight [N, K] + sw (+ bias) on the GPU."""
+    g = gen(seed)
+    per_set = sum(M * K * x_dtype.itemsize + N * K + M * N * 2 + M * K for M, N, K in shapes)
+    nsets = max(nsets_min, -(-(MALL_BYTES + (64 << 20)) // per_set))
+    sets = []
+    for _ in range(nsets):
+        items = []
+        for M, N, K in shapes:
+            x = torch.randn(M, K, generator=g)
+            x = torch.where(torch.rand(M, K, generator=g) < 1e-3, x * 20, x).to(x_dtype).to(dev)
+            w = (torch.randn(N, K, generator=g) * 0.02).to(dev)
+            b = (torch.randn(N, generator=g) * 0.01).to(dev) if bias else None
+            wq, sw = kernels.quant_rows(w)
+            items.append((x, wq, sw, b, M, N, K))
+        sets.append(items)
+    torch.cuda.synchronize()
+    return sets
+
+
+def run_gemm_step(items, timer=None, qtimer=None):
+    for x, wq, sw, b, M, N, K in items:
+        xq, sx = qtimer(kernels.quant_rows, x) if qtimer else kernels.quant_rows(x)
+        if timer:
+            timer(kernels.mm_i8_dequant, xq, sx, wq, sw, b, x.dtype)
+        else:
+            kernels.mm_i8_dequant(xq, sx, wq, sw, b, x.dtype)
+
+
+def gemm_bytes(M, N, K, xbytes, ybytes, bias):
+    """Algorithmic HBM bytes of the fused-epilogue GEMM launch: A int8 + W int8 + sx + sw (+ bias) + y."""
+    return M * K + N * K + 4 * M + 4 * N + (4 * N if bias else 0) + M * N * ybytes
+
+
+def quant_bytes(M, K, xbytes):
+    return M * K * xbytes + M * K + 4 * M
+
+
+# ------------------------------------------------------------------------------ CPU baseline
+def cpu_baseline_gemm(shapes, x_dtype, bias, budget_s=15.0):
+    """The reference CPU route (oracle/cpu_route.py) on the same shapes: 5 warm-up, then reps until
+    about budget_s, min of the per-step times (tools/cpu_baseline.py:14-26 protocol)."""
+    from oracle import cpu_route
+
+    g = gen(1)
+    data = []
+    for M, N, K in shapes:
+        x = torch.randn(M, K, generator=g).to(x_dtype)
+        w = torch.randn(N, K, generator=g) * 0.02
+        b = torch.randn(N, generator=g) * 0.01 if bias else None
+        w_kn, sw = cpu_route.weight_quant(w)
+        data.append((x, w_kn, sw, b))
+
+    def step():
+        for x, w_kn, sw, b in data:
+            cpu_route.linear(x, w_kn, sw, b)
+
+    for _ in range(2):
+        step()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < 60 and (time.perf_counter() < t_end or len(ts) < 3):
+        t = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t)
+    ts.sort()
+    ops = sum(2 * M * N * K for M, N, K in shapes)
+    return ops / ts[0] / 1e12, len(ts), ts[0]
+
+
+def cpu_baseline_conv(n, c, h, w, layers, relu=True, budget_s=15.0):
+    from oracle import cpu_route
+
+    g = gen(1)
+    x = torch.randn(n, c, h, w, generator=g)
+    convs = []
+    for _ in range(layers):
+        L = cpu_route.ConvLayerCPU(torch.randn(c, c, 3, 3, generator=g) * 0.02, relu)
+        convs.append(L)
+
+    def step():
+        y = x
+        for L in convs:
+            xq, sx = cpu_route.conv_quant(y)
+            if L.shift is None:
+                L.calibrate(xq[0])
+            y = cpu_route.conv_dequant(L(xq), L.scale, sx, None, torch.float32)
+
+    step()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < 60 and (time.perf_counter() < t_end or len(ts) < 2):
+        t = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t)
+    ts.sort()
+    ops = 2 * n * h * w * c * c * 9 * layers
+    return ops / ts[0] / 1e12, len(ts), ts[0]
+
+
+# ------------------------------------------------------------------------------ main
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    kernels.lib()   # fails loudly if the HIP library is not built
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    res = {"metric": "W8A8 GEMM & int8 conv3x3 TOPS on 1 MI355X; % of int8 MFMA peak / HBM BW",
+           "unit": "TOPS", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic (seed 0, randn)"}
+    bench = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
+             "quant": bench_quant}[a.workload]
+    res.update(bench(a, dev))
+    print(json.dumps(res), flush=True)
+
+
+def timed_steps(a, step):
+    for i in range(a.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        step(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / a.steps
+
+
+def gemm_result(a, dev, shapes, x_dtype, bias, workload, label):
+    sets = gemm_sets(shapes, dev, x_dtype=x_dtype, bias=bias)
+    sec = timed_steps(a, lambda i: run_gemm_step(sets[i % len(sets)]))
+    # per-launch timing of the dominant kernel (GEMM) and of the quantize, over a few more steps
+    gt, qt = Timer(), Timer()
+    reps = max(3, min(a.steps, 10))
+    for i in range(reps):
+        run_gemm_step(sets[i % len(sets)], gt, qt)
+    g_ms, q_ms = gt.ms(), qt.ms()
+    ops_step = sum(2 * M * N * K for M, N, K in shapes)
+    yb = 2 if x_dtype != torch.float32 else 4
+    xb = x_dtype.itemsize
+    g_ops = ops_step * reps
+    g_bytes = sum(gemm_bytes(M, N, K, xb, yb, bias) for M, N, K in shapes) * reps
+    g_sec = sum(g_ms) / 1e3
+    q_bytes = sum(quant_bytes(M, K, xb) for M, N, K in shapes) * reps
+    achieved = g_ops / g_sec / 1e12
+    out = {"value": round(ops_step / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
+           "config": {"workload": workload, "shapes_mnk": shapes, "x_dtype": str(x_dtype).replace("torch.", ""),
+                      "bias": bias, "rotating_sets": len(sets)},
+           "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                        "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                        "kernel": "mm_tile_kernel / mm_small_kernel (EPI_DQ)",
+                        "avg_launch_us": round(sum(g_ms) / len(g_ms) * 1e3, 2),
+                        "hbm_GBs_equiv": round(g_bytes / g_sec / 1e9, 1)},
+           "quantize": {"achieved_GBs": round(q_bytes / (sum(q_ms) / 1e3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                        "avg_launch_us": round(sum(q_ms) / len(q_ms) * 1e3, 2)},
+           "per_shape": []}
+    n = len(shapes)
+    for j, (M, N, K) in enumerate(shapes):
+        gj = [g_ms[i * n + j] for i in range(reps)]
+        t = sorted(gj)[len(gj) // 2] / 1e3
+        b = gemm_bytes(M, N, K, xb, yb, bias)
+        out["per_shape"].append({"mnk": [M, N, K], "us": round(t * 1e6, 2), "TOPS": round(2 * M * N * K / t / 1e12, 1),
+                                 "GBs": round(b / t / 1e9, 1)})
+    if not a.no_cpu_baseline:
+        tops, nrep, best = cpu_baseline_gemm(shapes, x_dtype, bias)
+        out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"{label}: full step, min of {nrep} reps "
+                               f"({best * 1e3:.1f} ms), torch CPU quantize + torch._int_mm + dequantize"}
+    return out
+
+
+def bench_c2(a, dev):
+    shapes = []
+    for M in (128, 512, 1024, 3000):
+        shapes += [(M, 4096, 1024), (M, 6144, 1024), (M, 1024, 3072)]
+    return gemm_result(a, dev, shapes, torch.bfloat16, False,
+                       "C2 Qwen3-0.6B linear_cat qkv/gate-up/down, M in {128,512,1024,3000}, bf16", "C2")
+
+
+def bench_c1(a, dev):
+    return gemm_result(a, dev, [(128, 3072, 1024)], torch.float32, True, "C1 single W8A8 linear fp32 128x3072x1024",
+                       "C1")
+
+
+def bench_c5(a, dev):
+    return gemm_result(a, dev, [(8192, 14336, 4096)], torch.bfloat16, True,
+                       "C5 W8A8 GEMM M=8192 N=14336 K=4096 bf16 + bias", "C5")
+
+
+def bench_quant(a, dev):
+    g = gen(0)
+    M, K = 8192, 14336
+    xs = [torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev) for _ in range(2)]
+    sec = timed_steps(a, lambda i: kernels.quant_rows(xs[i % 2]))
+    t = Timer()
+    for i in range(10):
+        t(kernels.quant_rows, xs[i % 2])
+    ms = t.ms()
+    b = quant_bytes(M, K, 2)
+    gbs = b / (sum(ms) / len(ms) / 1e3) / 1e9
+    return {"metric": "activation quantize GB/s on 1 MI355X", "unit": "GB/s", "value": round(b / sec / 1e9, 1),
+            "ms_per_step": round(sec * 1e3, 4), "dtype": "bf16->int8",
+            "config": {"workload": "quantize bf16 [8192, 14336] per row"},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": "quant_rows_vec_kernel"}}
+
+
+def conv_layer_data(dev, n, c, h, w, seed=0):
+    g = gen(seed)
+    x = torch.randn(n, c, h, w, generator=g).to(dev)
+    wt = (torch.randn(c, c, 3, 3, generator=g) * 0.02).to(dev)
+    c_pad = -(-c // 16) * 16
+    wq, sw = kernels.conv_weight_pack(wt, c_pad)
+    return x, wq, sw, c_pad
+
+
+def bench_c4(a, dev):
+    n, c, h, w = 1, 256, 1536, 64
+    sets = []
+    for s in range(3):
+        x, wq, sw, c_pad = conv_layer_data(dev, n, c, h, w, seed=s)
+        xq, sx = kernels.conv_quant(x, c_pad)
+        shift = 10
+        sets.append((xq, wq, shift))
+    torch.cuda.synchronize()
+    sec = timed_steps(a, lambda i: kernels.conv3x3(sets[i % 3][0], sets[i % 3][1], sets[i % 3][2], True))
+    t = Timer()
+    for i in range(10):
+        t(kernels.conv3x3, sets[i % 3][0], sets[i % 3][1], sets[i % 3][2], True)
+    ms = t.ms()
+    ops = 2 * n * h * w * c * c * 9
+    ach = ops / (sum(ms) / len(ms) / 1e3) / 1e12
+    out = {"value": round(ops / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
+           "config": {"workload": "C4 int8 conv3x3 256->256 on 1x256x1536x64, ReLU, NHWC int8 in/out"},
+           "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                        "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None, "kernel": "mm_tile_kernel (conv)"}}
+    if not a.no_cpu_baseline:
+        tops, nrep, best = cpu_baseline_conv(1, 256, 128, 64, 1)
+        out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"one layer at 1x256x128x64 (1/12 of the image rows), "
+                               f"min of {nrep} reps ({best * 1e3:.1f} ms): torch CPU quantize + fp32 conv2d of the "
+                               "int8 values + shift + dequantize"}
+    return out
+
+
+def bench_c3(a, dev):
+    n, c, h, w, L = 1, 256, 64, 64, 4
+    g = gen(0)
+    x = torch.randn(n, c, h, w, generator=g).to(dev)
+    c_pad = c
+    layers = []
+    for _ in range(L):
+        wt = (torch.randn(c, c, 3, 3, generator=g) * 0.02).to(dev)
+        layers.append(kernels.conv_weight_pack(wt, c_pad) + (None,))
+    # calibrate the shifts on the first pass (first call of each layer)
+    shifts = []
+    y = x
+    for wq, sw, _ in layers:
+        xq, sx = kernels.conv_quant(y, c_pad)
+        top = kernels.conv3x3_calibrate(xq[:1], wq, True)
+        import math
+        shift = min(31, max(1, math.ceil(math.log2(max(top * 1.25, 1.0) / 255))))
+        shifts.append(shift)
+        scale = sw * 2.0 ** shift
+        y = kernels.conv_dequant(kernels.conv3x3(xq, wq, shift, True), True, scale, sx, None, torch.float32)
+    scales = [sw * 2.0 ** s for (wq, sw, _), s in zip(layers, shifts)]
+
+    def step(i, ct=None):
+        y = x
+        for (wq, sw, _), s, sc in zip(layers, shifts, scales):
+            xq, sx = kernels.conv_quant(y, c_pad)
+            q = ct(kernels.conv3x3, xq, wq, s, True) if ct else kernels.conv3x3(xq, wq, s, True)
+            y = kernels.conv_dequant(q, True, sc, sx, None, torch.float32)
+        return y
+
+    sec = timed_steps(a, step)
+    ct = Timer()
+    for i in range(5):
+        step(i, ct)
+    ms = ct.ms()
+    ops = 2 * n * h * w * c * c * 9
+    ach = ops / (sum(ms) / len(ms) / 1e3) / 1e12
+    out = {"value": round(ops * L / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
+           "config": {"workload": "C3 4x (conv3x3 256->256 + ReLU) on 1x256x64x64, quantize/conv/dequantize per layer"},
+           "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                        "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None, "kernel": "mm_tile_kernel (conv)"}}
+    if not a.no_cpu_baseline:
+        tops, nrep, best = cpu_baseline_conv(n, c, h, w, L)
+        out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"full C3 step, min of {nrep} reps ({best * 1e3:.1f} ms)"}
+    return out
+
+
+if __name__ == "__main__":
+    main()

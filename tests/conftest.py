@@ -34,3 +34,21 @@ def gpu():
 
     kernels.lib()  # raises loudly if the HIP library is not built
     return torch.device("cuda", 0)
+
+
+@pytest.fixture(autouse=True)
+def reset_state():
+    """Fresh process-global state per test (the reference runs each case in its own process)."""
+    import torch
+
+    yield
+    from torch_xdna import conv, kernels, runtime
+
+    runtime.stats.reset()
+    runtime.decisions.clear()
+    runtime._failed.clear()
+    runtime._verified.clear()
+    runtime._weights.clear()
+    conv._layers.clear()
+    kernels.reset()
+    torch._dynamo.reset()

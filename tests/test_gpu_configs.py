@@ -1,0 +1,181 @@
+"""BASELINE.json configs C1-C5 on the MI355X through the public ops, against the oracle.
+
+C1, C2, C3 and the decode GEMMs of C5 are compared in full (int32 sums from the C oracle, the rest
+from the numpy oracle). The full-size C4 conv and the M=8192 C5 GEMM are too large for a CPU oracle
+within seconds, so they are checked by size-independent properties: exact row and column checksums
+of the int32 GEMM (sum_n C = A (sum_n W), sum_m C = (sum_m A) W^T, in int64), and exact values at a
+few thousand random positions (int64 dot products / conv sums on the CPU), for the int32 output and
+for the fused bf16 / requantized outputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import c_oracle
+from oracle import xdna_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _cid(**kw):
+    from torch_xdna import Config, ops
+
+    return ops.config_id(Config(**kw))
+
+
+def _stats():
+    from torch_xdna import runtime
+
+    return runtime.stats.as_dict()
+
+
+def test_c1_single_linear(gpu):
+    g = _gen(0)
+    x = torch.randn(128, 1024, generator=g)
+    w = torch.randn(3072, 1024, generator=g) * 0.02
+    b = torch.randn(3072, generator=g) * 0.01
+    y = torch.ops.xdna.linear(x.to(gpu), w.to(gpu), b.to(gpu), False, _cid(policy="gpu", verify="off"))
+    assert _stats()["calls"] == {"gpu": 1}
+    xq, sx = O.quant_rows(x.numpy())
+    wq, sw = O.quant_rows(w.numpy())
+    want = O.dequant(c_oracle.gemm_i32(xq, wq), sx, sw, b.numpy())
+    assert np.array_equal(y.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("M", [128, 512, 1024, 3000])
+def test_c2_linear_cat(gpu, M):
+    g = _gen(M)
+    x = torch.randn(M, 1024, generator=g).to(torch.bfloat16)
+    xd = torch.randn(M, 3072, generator=g).to(torch.bfloat16)
+    qkv = [torch.randn(n, 1024, generator=g) * 0.02 for n in (2048, 1024, 1024)]
+    gu = [torch.randn(3072, 1024, generator=g) * 0.02 for _ in range(2)]
+    down = torch.randn(1024, 3072, generator=g) * 0.02
+    cid = _cid(policy="gpu", verify="off")
+    for inp, ws in ((x, qkv), (x, gu), (xd, [down])):
+        if len(ws) > 1:
+            y = torch.ops.xdna.linear_cat(inp.to(gpu), [w.to(gpu) for w in ws], [None] * len(ws), cid)
+        else:
+            y = torch.ops.xdna.linear(inp.to(gpu), ws[0].to(gpu), None, False, cid)
+        xq, sx = O.quant_rows(inp.float().numpy())
+        wq, sw = O.weight_quant_cat([w.numpy() for w in ws])
+        want = O.to_bf16(O.dequant(c_oracle.gemm_i32(xq, wq), sx, sw))
+        got = y.float().cpu().numpy()
+        assert y.dtype == torch.bfloat16 and np.array_equal(got, want), f"{(got != want).sum()} differ"
+    assert _stats()["calls"] == {"gpu": 3}
+
+
+def test_c3_conv_chain(gpu):
+    """4 x (conv3x3 256->256 + ReLU) on 1x256x64x64 through torch.compile, each layer's shift fixed on
+    its first call, against the oracle's chain (quantize -> conv -> requant -> dequantize per layer)."""
+    from models import VGGBlock, run
+
+    torch.manual_seed(0)
+    net = VGGBlock(256, 4).eval()
+    for c in net.convs:
+        with torch.no_grad():
+            c.weight.copy_(torch.randn(c.weight.shape, generator=_gen(11)) * 0.02)
+    x = torch.randn(1, 256, 64, 64, generator=_gen(12))
+    y = run(net.to(gpu), x.to(gpu), policy="gpu", fallback="eager")
+    s = _stats()
+    assert s["calls"] == {"gpu": 4} and not s["fallbacks"], s
+    h = x.numpy()
+    for c in net.convs:
+        xq, sx = O.conv_quant_images(h)
+        wq, sw = O.conv_weight_quant(c.weight.detach().cpu().numpy())
+        acc = c_oracle.conv3x3_acc(xq, wq)
+        shift = O.calibrate_shift(acc[0], True)
+        h = O.conv_dequant(O.requant(acc, shift, True), O.conv_scale(sw, shift), sx)
+    assert np.array_equal(y.cpu().numpy(), h)
+
+
+def _sampled_conv_check(xq_nchw, wq, q_nhwc, shift, relu, n_samples, seed):
+    rng = np.random.default_rng(seed)
+    nb, ci, h, w = xq_nchw.shape
+    co = wq.shape[0]
+    xp = np.zeros((nb, ci, h + 2, w + 2), np.int64)
+    xp[:, :, 1:h + 1, 1:w + 1] = xq_nchw
+    wl = wq.astype(np.int64)
+    for _ in range(n_samples):
+        b, y, x, o = rng.integers(nb), rng.integers(h), rng.integers(w), rng.integers(co)
+        acc = int((xp[b, :, y:y + 3, x:x + 3] * wl[o]).sum())
+        want = O.requant(np.array([acc]), shift, relu)[0]
+        assert q_nhwc[b, y, x, o] == want, (b, y, x, o)
+
+
+@pytest.mark.parametrize("shape", [(1, 256, 1536, 64), (8, 256, 256, 256)])
+def test_c4_large_conv_sampled(gpu, shape):
+    from torch_xdna import kernels
+
+    nb, c, h, w = shape
+    x = torch.randn(*shape, generator=_gen(21)).to(gpu)
+    wt = (torch.randn(c, c, 3, 3, generator=_gen(22)) * 0.02).to(gpu)
+    xq, sx = kernels.conv_quant(x, c)
+    wq, sw = kernels.conv_weight_pack(wt, c)
+    top = kernels.conv3x3_calibrate(xq[:1], wq, True)
+    shift = O.shift_from_top(float(top), True)
+    q = kernels.conv3x3(xq, wq, shift, True)
+    xq_nchw = xq.permute(0, 3, 1, 2).cpu().numpy()
+    wq_ref = wq.cpu().numpy().reshape(c, 3, 3, c).transpose(0, 3, 1, 2)
+    # the calibration max is reached somewhere and bounds every sampled |acc|
+    assert top > 0
+    _sampled_conv_check(xq_nchw, wq_ref, q.cpu().numpy(), shift, True, 3000, seed=1)
+    # quantize parity on the full tensor (cheap in numpy)
+    xq_r, sx_r = O.conv_quant_images(x.cpu().numpy())
+    assert np.array_equal(xq_nchw, xq_r) and np.array_equal(sx.cpu().numpy(), sx_r)
+
+
+@pytest.mark.parametrize("M,N,K", [(8192, 14336, 4096), (8192, 4096, 14336), (2048, 4096, 4096)])
+def test_c5_large_gemm_properties(gpu, M, N, K):
+    from torch_xdna import kernels
+
+    g = _gen(M + N + K)
+    x = torch.randn(M, K, generator=g)
+    x = torch.where(torch.rand(M, K, generator=g) < 1e-3, x * 20, x).to(torch.bfloat16)
+    w = torch.randn(N, K, generator=g) * 0.02
+    b = torch.randn(N, generator=g) * 0.01
+    xq, sx = kernels.quant_rows(x.to(gpu))
+    wq, sw = kernels.quant_rows(w.to(gpu))
+    acc = kernels.mm_i8(xq, wq)
+    y = kernels.mm_i8_dequant(xq, sx, wq, sw, b.to(gpu), torch.bfloat16)
+    # quantize parity in full
+    xq_r, sx_r = O.quant_rows(x.float().numpy())
+    assert np.array_equal(xq.cpu().numpy(), xq_r) and np.array_equal(sx.cpu().numpy(), sx_r)
+    A = xq.cpu().numpy().astype(np.int64)
+    W = wq.cpu().numpy().astype(np.int64)
+    # exact checksums in int64
+    row = acc.to(torch.int64).sum(1).cpu().numpy()
+    col = acc.to(torch.int64).sum(0).cpu().numpy()
+    assert np.array_equal(row, A @ W.sum(0)), "row checksums differ"
+    assert np.array_equal(col, W @ A.sum(0)), "column checksums differ"
+    # exact entries at random positions, for the int32 and the fused bf16 outputs
+    rng = np.random.default_rng(0)
+    ms, ns = rng.integers(0, M, 4000), rng.integers(0, N, 4000)
+    want = np.einsum("ik,ik->i", A[ms], W[ns])
+    accc = acc.cpu().numpy()
+    assert np.array_equal(accc[ms, ns], want)
+    yw = O.to_bf16(((want.astype(np.float32) * sx_r[ms]) * sw.cpu().numpy()[ns]) + b.numpy()[ns])
+    assert np.array_equal(y.float().cpu().numpy()[ms, ns], yw)
+
+
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (14336, 4096), (4096, 14336)])
+def test_c5_decode_gemm(gpu, M, N, K):
+    from torch_xdna import kernels
+
+    g = _gen(M * 7 + N + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = torch.randn(N, K, generator=g) * 0.02
+    b = torch.randn(N, generator=g) * 0.01
+    xq, sx = kernels.quant_rows(x.to(gpu))
+    wq, sw = kernels.quant_rows(w.to(gpu))
+    y = kernels.mm_i8_dequant(xq, sx, wq, sw, b.to(gpu), torch.bfloat16)
+    acc = kernels.mm_i8(xq, wq)
+    xq_r, sx_r = O.quant_rows(x.float().numpy())
+    wq_r, sw_r = O.quant_rows(w.numpy())
+    acc_r = c_oracle.gemm_i32(xq_r, wq_r)
+    assert np.array_equal(acc.cpu().numpy(), acc_r)
+    assert np.array_equal(y.float().cpu().numpy(), O.to_bf16(O.dequant(acc_r, sx_r, sw_r, b.numpy())))

@@ -1,0 +1,266 @@
+"""xdna::conv3x3: 3x3, stride-1, padding-1 convolutions of a parameter weight, int8 on the GPU.
+
+Mirrors the reference's conv runtime (torch_xdna/conv.py in the reference). Math, unchanged:
+
+  weights     int8 per output channel, quantized once (conv.py:58-60)
+  activations int8 per image (sx, conv.py:45-46)
+  sums        exact int32, requantized by one shift: round half up, saturate to int8, or to
+              [0, 255] with a fused ReLU (conv.py:89-92). The shift is fixed on the layer's first
+              call from image 0's integer sums with 25% headroom (conv.py:71-76).
+  output      q * (sw[co] * 2^shift * sx) (+ bias) (conv.py:48-50)
+
+The GPU route runs the HIP kernels: the per-image quantize writes the int8 activation straight into
+NHWC (channels padded to 16), the implicit-GEMM MFMA conv fuses the requantize, and the dequantize
+reads NHWC and writes NCHW. On a GPU graph the whole composite is the one opaque op
+xdna::conv3x3_fused; the reference's int8-in / int8-out xdna::conv3x3 op keeps its NCHW contract
+(with layout kernels around the same conv). The CPU route is the reference's exact float conv of
+the integers; a layer's first GPU launch is compared with it bit for bit, and a layer that
+disagrees or fails stays on the CPU.
+"""
+
+import logging
+import math
+import threading
+import time
+import weakref
+
+import torch
+
+from . import kernels
+from .runtime import GPUResultMismatch, _require_lib, _time, decisions, stats
+
+log = logging.getLogger("torch_xdna")
+_lock = threading.RLock()
+_layers = {}            # (id(weight), H, W, relu) -> (weakref to weight, ConvLayer)
+
+
+def supported(ci, co, h, w):
+    """Shapes the pass rewrites: up to 512 input channels (the reference's limit, kept so the same
+    convs are rewritten; the GPU kernel itself takes any channel count)."""
+    return 1 <= ci <= 512 and co >= 1 and h >= 1 and w >= 1
+
+
+def conv3x3_int8(x, weight, bias, relu: bool, cfg_id: int):
+    """relu?(conv2d(x, weight, bias, padding=1)) through int8: what the backend puts in the graph.
+
+    On the CPU (conv.py:43-51): quantize and dequantize are torch ops around xdna::conv3x3. On the GPU
+    the composite is the single op xdna::conv3x3_fused (HIP quantize, conv, dequantize)."""
+    if x.device.type == "cuda":
+        return torch.ops.xdna.conv3x3_fused(x, weight, bias, relu, cfg_id)
+    sx = x.abs().amax(dim=(1, 2, 3), keepdim=True).float().clamp(min=1e-8) / 127
+    xq = torch.round(x.float() / sx).clamp(-127, 127).to(torch.int8)
+    q, scale = torch.ops.xdna.conv3x3(xq, weight, relu, cfg_id)
+    y = q.float() * (scale.view(1, -1, 1, 1) * sx)
+    if bias is not None:
+        y = y + bias.float().view(1, -1, 1, 1)
+    return y.to(x.dtype)
+
+
+class ConvLayer:
+    """One conv weight at one input size: int8 weights (per device), the shift, the device choice."""
+
+    def __init__(self, weight, h, w, relu):
+        self.src = weight.detach()
+        self.co, self.ci = int(weight.shape[0]), int(weight.shape[1])
+        self.ci_pad = kernels.round_up(self.ci, 16)
+        self.h, self.w, self.relu = h, w, relu
+        self.shift = None
+        self.device = None      # "gpu" or "cpu" once the first call has decided
+        self._cpu = None
+        self._gpu = {}
+        self._scale = {}
+        self.name = f"conv3x3 {self.ci}->{self.co} {h}x{w}" + (" relu" if relu else "")
+
+    # -------------------------------------------------------------- weights
+    def cpu_weights(self):
+        """(wq int8 [Co, Ci, 3, 3], sw [Co], exact float dtype) on the CPU (conv.py:58-63)."""
+        if self._cpu is None:
+            wf = self.src.cpu().float()
+            sw = wf.abs().amax(dim=(1, 2, 3)).clamp(min=1e-8) / 127
+            wq = torch.round(wf / sw[:, None, None, None]).clamp(-127, 127).to(torch.int8)
+            # |sums| <= 127 * sum |wq| per channel: below 2^24 a float32 conv of the integers is exact
+            dt = torch.float32 if 127 * float(wq.abs().sum(dim=(1, 2, 3)).max()) < 2 ** 24 else torch.float64
+            self._cpu = (wq, sw, dt)
+        return self._cpu
+
+    def gpu_weights(self, dev):
+        """(wq int8 [Co, 9, Ci_pad], sw [Co]) on dev, quantized there by the HIP kernel."""
+        hit = self._gpu.get(dev)
+        if hit is None:
+            hit = self._gpu[dev] = kernels.conv_weight_pack(self.src.to(dev), self.ci_pad)
+        return hit
+
+    def sw(self, dev):
+        return self.gpu_weights(dev)[1] if dev.type == "cuda" else self.cpu_weights()[1]
+
+    def scale(self, dev):
+        """sw * 2^shift as float32 on dev (conv.py:76); the power of two makes the product exact."""
+        hit = self._scale.get(dev)
+        if hit is None:
+            hit = self._scale[dev] = self.sw(dev) * 2.0 ** self.shift
+        return hit
+
+    # -------------------------------------------------------------- calibration (first call)
+    def _set_shift(self, top):
+        self.shift = min(31, max(1, math.ceil(math.log2(max(top * 1.25, 1.0) / (255 if self.relu else 127)))))
+
+    def calibrate_cpu(self, xq0):
+        """conv.py:71-75 from image 0 (NCHW int8 [Ci, H, W])."""
+        acc = self._acc(xq0[None].cpu())
+        self._set_shift(float(acc.clamp(min=0).max()) if self.relu else float(acc.abs().max()))
+
+    def calibrate_gpu(self, xq_nhwc0):
+        """The same from the GPU's int32 sums of image 0 (NHWC int8 [1, H, W, Ci_pad])."""
+        wq, _ = self.gpu_weights(xq_nhwc0.device)
+        self._set_shift(float(kernels.conv3x3_calibrate(xq_nhwc0, wq, self.relu)))
+
+    # -------------------------------------------------------------- the two routes
+    def _acc(self, xq):
+        wq, _, dt = self.cpu_weights()
+        return torch.nn.functional.conv2d(xq.to(dt), wq.to(dt), padding=1)
+
+    def cpu(self, xq):
+        """The integers on the CPU (conv.py:89-92): exact sums, round half up, saturate. NCHW."""
+        q = (self._acc(xq.cpu()).to(torch.int32) + (1 << (self.shift - 1))) >> self.shift
+        return q.clamp_(0, 255).to(torch.uint8) if self.relu else q.clamp_(-128, 127).to(torch.int8)
+
+    def gpu_nhwc(self, xq_nhwc, verify=False, xq_nchw=None):
+        """The GPU conv of an NHWC int8 activation -> NHWC int8/uint8 q."""
+        wq, _ = self.gpu_weights(xq_nhwc.device)
+        q = kernels.conv3x3(xq_nhwc, wq, self.shift, self.relu)
+        stats.launches += 1
+        if verify:
+            if xq_nchw is None:
+                xq_nchw = xq_nhwc[..., :self.ci].permute(0, 3, 1, 2)
+            want = self.cpu(xq_nchw)
+            got = q.permute(0, 3, 1, 2).cpu()
+            if not torch.equal(got, want):
+                raise GPUResultMismatch(f"GPU {self.name} disagrees with the CPU: "
+                                        f"{int((got != want).sum())} of {want.numel()} values differ")
+        return q
+
+    def gpu(self, xq, verify=False):
+        """xdna::conv3x3's contract on the GPU: NCHW int8 in, NCHW int8/uint8 out."""
+        dev = kernels.gpu_device(xq)
+        xg = xq.to(dev)
+        q = self.gpu_nhwc(kernels.nchw_to_nhwc(xg, self.ci_pad), verify, xq_nchw=xq)
+        return kernels.nhwc_to_nchw(q)
+
+
+def _layer(weight, h, w, relu):
+    key = (id(weight), h, w, relu)
+    hit = _layers.get(key)
+    if hit is not None and hit[0]() is weight:
+        return hit[1]
+    layer = ConvLayer(weight, h, w, relu)
+    _layers[key] = (weakref.ref(weight), layer)
+    return layer
+
+
+def _failed(layer, e):
+    layer.device = "cpu"
+    stats.fallbacks.append((layer.name, f"{type(e).__name__}: {e}"[:300]))
+    log.warning("torch_xdna: GPU %s failed (%s); it runs on the CPU from now on", layer.name, e)
+
+
+def _gpu_route(cfg, layer, on_gpu):
+    if cfg.policy == "cpu" or layer.device == "cpu":
+        return False
+    if on_gpu:
+        _require_lib()
+    return kernels.available()
+
+
+def _first_call(cfg, layer, run_gpu, run_cpu, on_gpu):
+    """Verify the layer's first GPU launch and pick its device (conv.py:122-138)."""
+    try:
+        run_gpu(cfg.verify != "off")
+        layer.device = "gpu"
+        if cfg.policy == "auto" and not on_gpu:   # host tensors: time both, keep the faster
+            gpu_ms, cpu_ms = _time(lambda: run_gpu(False)), _time(run_cpu)
+            layer.device = "gpu" if gpu_ms < cpu_ms else "cpu"
+            decisions[(layer.name,)] = (layer.device, round(gpu_ms, 3), round(cpu_ms, 3))
+            if cfg.verbose:
+                log.warning("torch_xdna autotune %s: gpu %.3f ms, cpu %.3f ms -> %s", layer.name, gpu_ms, cpu_ms,
+                            layer.device)
+    except Exception as e:      # launch failure or a mismatch
+        _failed(layer, e)
+
+
+def _account(device, t0, n, layer):
+    stats.calls[device] += 1
+    stats.seconds[device] += time.perf_counter() - t0
+    stats.macs[device] += n * layer.co * layer.ci * layer.h * layer.w * 9
+
+
+def conv3x3(cfg, xq, weight, relu):
+    """(q, scale) of xdna::conv3x3 for int8 xq [N, Ci, H, W], on the GPU or the CPU (conv.py:164-189)."""
+    n, ci, h, w = xq.shape
+    t0 = time.perf_counter()
+    on_gpu = xq.device.type == "cuda"
+    with _lock:
+        layer = _layer(weight, h, w, relu)
+        use_gpu = _gpu_route(cfg, layer, on_gpu)
+        if layer.shift is None:
+            if use_gpu:
+                dev = kernels.gpu_device(xq)
+                layer.calibrate_gpu(kernels.nchw_to_nhwc(xq[:1].to(dev), layer.ci_pad))
+            else:
+                layer.calibrate_cpu(xq[0])
+        if layer.device is None:
+            if use_gpu:
+                _first_call(cfg, layer, lambda v: layer.gpu(xq, verify=v), lambda: layer.cpu(xq), on_gpu)
+            else:
+                layer.device = "cpu"
+        q, device = None, "cpu"
+        if layer.device == "gpu" and use_gpu:
+            try:
+                q, device = layer.gpu(xq, verify=cfg.verify == "always"), "gpu"
+            except Exception as e:
+                _failed(layer, e)
+        if q is None:
+            q = layer.cpu(xq)
+    _account(device, t0, n, layer)
+    # a fresh tensor: Inductor may reuse an extern op's output buffer once it is dead
+    return q.to(xq.device), layer.scale(xq.device).to(xq.device).clone()
+
+
+def conv3x3_fused(cfg, x, weight, bias, relu):
+    """The GPU form of conv3x3_int8: y = dequant(conv3x3(quant(x))) with all three in HIP kernels and
+    the activation kept NHWC int8 in between. Falls back to the reference composite on the CPU."""
+    n, ci, h, w = x.shape
+    t0 = time.perf_counter()
+    on_gpu = x.device.type == "cuda"
+    with _lock:
+        layer = _layer(weight, h, w, relu)
+        y, device = None, "cpu"
+        if on_gpu and _gpu_route(cfg, layer, on_gpu):
+            try:
+                xq, sx = kernels.conv_quant(x, layer.ci_pad)
+                if layer.shift is None:
+                    layer.calibrate_gpu(xq[:1])
+                if layer.device is None:
+                    _first_call(cfg, layer, lambda v: layer.gpu_nhwc(xq, verify=v), None, on_gpu)
+                if layer.device == "gpu":
+                    q = layer.gpu_nhwc(xq, verify=cfg.verify == "always")
+                    b = None if bias is None else bias.to(x.device, torch.float32).contiguous()
+                    y = kernels.conv_dequant(q, relu, layer.scale(x.device), sx, b, x.dtype)
+                    device = "gpu"
+            except Exception as e:
+                _failed(layer, e)
+                y = None
+        if y is None:
+            xc = x.cpu()
+            sx = xc.abs().amax(dim=(1, 2, 3), keepdim=True).float().clamp(min=1e-8) / 127
+            xq = torch.round(xc.float() / sx).clamp(-127, 127).to(torch.int8)
+            if layer.shift is None:
+                layer.calibrate_cpu(xq[0])
+            if layer.device is None:
+                layer.device = "cpu"
+            q = layer.cpu(xq)
+            y = q.float() * (layer.scale(torch.device("cpu")).view(1, -1, 1, 1) * sx)
+            if bias is not None:
+                y = y + bias.cpu().float().view(1, -1, 1, 1)
+            y = y.to(x.dtype).to(x.device)
+    _account(device, t0, n, layer)
+    return y

@@ -134,6 +134,11 @@ def _need_gpu(*ts):
     return dev
 
 
+def gpu_device(t):
+    """The GPU a tensor's GPU route runs on: its own device, or the current GPU for host tensors."""
+    return t.device if t.device.type == "cuda" else torch.device("cuda", torch.cuda.current_device())
+
+
 def num_cus(dev) -> int:
     """Compute units of the device (the library's launch shaping uses the same figure)."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
@@ -160,10 +165,11 @@ def gemm_variant(dev, M, N) -> str:
 
 
 # ------------------------------------------------------------------------------ launchers
-def quant_rows(x2d, k_pad=None):
+def quant_rows(x2d, k_pad=None, out=None):
     """(xq int8 [R, k_pad], sx float32 [R]) of a [R, K] float tensor (bf16/fp16/fp32), K zero-padded
     to k_pad (default: the next multiple of 16). Same integers and scales as
-    `torch.round(x.float() / s).clamp(-127, 127)` with s = amax.clamp(1e-8) / 127."""
+    `torch.round(x.float() / s).clamp(-127, 127)` with s = amax.clamp(1e-8) / 127.
+    `out=(xq, sx)` writes into given tensors (rows of xq may be a slice of a larger buffer)."""
     dev = _need_gpu(x2d)
     if x2d.dtype not in _DTYPE_CODE:
         raise TypeError(f"quant_rows takes float32/bfloat16/float16, got {x2d.dtype}")
@@ -171,12 +177,18 @@ def quant_rows(x2d, k_pad=None):
     if x2d.stride(1) != 1:
         x2d = x2d.contiguous()
     k_pad = round_up(K, 16) if k_pad is None else k_pad
-    xq = torch.empty((R, k_pad), dtype=torch.int8, device=dev)
-    sx = torch.empty((R,), dtype=torch.float32, device=dev)
+    if out is None:
+        xq = torch.empty((R, k_pad), dtype=torch.int8, device=dev)
+        sx = torch.empty((R,), dtype=torch.float32, device=dev)
+    else:
+        xq, sx = out
+        _need_gpu(x2d, xq, sx)
+        if xq.shape != (R, k_pad) or xq.stride(1) != 1 or sx.shape != (R,) or not sx.is_contiguous():
+            raise ValueError("quant_rows: bad out tensors")
     if R:
         with torch.cuda.device(dev):
-            _check(lib().xdna_quant_rows(_ptr(x2d), _DTYPE_CODE[x2d.dtype], R, K, x2d.stride(0), _ptr(xq), k_pad,
-                                         k_pad, _ptr(sx), _stream(dev)), "quant_rows")
+            _check(lib().xdna_quant_rows(_ptr(x2d), _DTYPE_CODE[x2d.dtype], R, K, x2d.stride(0), _ptr(xq),
+                                         xq.stride(0), k_pad, _ptr(sx), _stream(dev)), "quant_rows")
     return xq, sx
 
 
