@@ -37,11 +37,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // float32 -> bfloat16 bits, round to nearest even (NaN stays a quiet NaN), the rounding torch's
 // `.to(torch.bfloat16)` applies.
+// Branch-free: both results are computed and selected.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet = (u >> 16) | 0x0040u;
+  return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? quiet : rounded);
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }

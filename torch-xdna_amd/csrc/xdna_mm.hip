@@ -72,6 +72,7 @@ __device__ __forceinline__ i32x16 mfma32x32x32(const i32x4& a, const i32x4& b, c
 template <int EPI>
 struct EpiCols {
   float sw[4], b[4];
+  __device__ __forceinline__ EpiCols() {}
   __device__ __forceinline__ EpiCols(const EpiArgs& e, int64_t n, int64_t N) {
     if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16) {
       if (n + 3 < N && (reinterpret_cast<uintptr_t>(e.sw + n) & 15) == 0) {
@@ -96,10 +97,50 @@ struct EpiCols {
   }
 };
 
-// One lane's four outputs: row m, columns n .. n+3 (acc[r] is column n + r).
-template <int EPI>
+// One lane's four outputs: row m, columns n .. n+3 (acc[r] is column n + r). FULL: the caller has
+// established that the whole tile is in bounds and vector stores are allowed (no per-element tests).
+template <int EPI, bool FULL = false>
 __device__ __forceinline__ void epilogue4(const EpiArgs& e, int64_t m, int64_t n, int64_t M, int64_t N,
-                                          const i32x4& acc, int& calib, const EpiCols<EPI>& cols) {
+                                          const i32x4& acc, int& calib, const EpiCols<EPI>& cols, float sxm) {
+  if constexpr (FULL) {
+    if constexpr (EPI == EPI_CALIB) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) calib = max(calib, e.relu ? max(acc[r], 0) : abs(acc[r]));
+    } else if constexpr (EPI == EPI_I32) {
+      *reinterpret_cast<i32x4*>(reinterpret_cast<int32_t*>(e.out) + m * e.ldo + n) = acc;
+    } else if constexpr (EPI == EPI_REQUANT) {
+      const int half = 1 << (e.shift - 1);
+      uint32_t packed = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int q = (acc[r] + half) >> e.shift;    // arithmetic shift: floor, i.e. round half up
+        q = e.relu ? min(max(q, 0), 255) : min(max(q, -128), 127);
+        packed |= ((uint32_t)(q & 0xff)) << (8 * r);
+      }
+      *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(e.out) + m * e.ldo + n) = packed;
+    } else {
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float t = (float)acc[r];
+        t = t * sxm;
+        t = t * cols.sw[r];
+        if (e.bias) t = t + cols.b[r];         // uniform test: the bias pointer is a kernel argument
+        v[r] = t;
+      }
+      const int64_t off = m * e.ldo + n;
+      if constexpr (EPI == EPI_DQ_F32) {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(e.out) + off) = f32x4{v[0], v[1], v[2], v[3]};
+      } else {
+        uint16_t h[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[r] = EPI == EPI_DQ_BF16 ? f32_to_bf16_bits(v[r]) : f32_to_f16_bits(v[r]);
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(e.out) + off) =
+            make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+      }
+    }
+    return;
+  }
   if (m >= M) return;
   if constexpr (EPI == EPI_CALIB) {
 #pragma unroll
@@ -139,7 +180,6 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& e, int64_t m, int64_t n
         if (n + r < N) o[r] = (uint8_t)(qv[r] & 0xff);
     }
   } else {  // EPI_DQ_*: ((float)acc * sx[m]) * sw[n] (+ bias[n]), each step rounded once
-    const float sxm = e.sx[m];
     float v[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -272,6 +312,21 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
   int64_t tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = tm * BM, n0 = tn * BN;
+
+  // The epilogue's per-row and per-column scales do not depend on K: load them now, so they arrive
+  // during the K loop. Read-back layout: row rr * 8 + (lane >> 3), columns 4 * (lane & 7) .. +3.
+  constexpr bool DQ = EPI == EPI_DQ_F32 || EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16;
+  float sx_pre[DQ ? TM / 8 : 1];
+  if constexpr (DQ) {
+#pragma unroll
+    for (int rr = 0; rr < TM / 8; ++rr) {
+      const int64_t m = m0 + wm * TM + rr * 8 + (lane >> 3);
+      sx_pre[rr] = m < M ? e.sx[m] : 0.0f;
+    }
+  }
+  EpiCols<EPI> cols_pre[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) cols_pre[j] = EpiCols<EPI>(e, n0 + wn * TN + j * 32 + (lane & 7) * 4, N);
 
   const __amdgpu_buffer_rsrc_t ra_rsrc = make_rsrc(a, (uint32_t)(CONV ? (M * cg.c_pad) : (M * lda)));
   const __amdgpu_buffer_rsrc_t rw_rsrc = make_rsrc(w, (uint32_t)(N * ldw));
@@ -471,6 +526,8 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
   __syncthreads();                       // every wave is done with the K-loop's LDS stages
   int8_t* stg = lds0 + wave * TM * PITCH;
   int calib = 0;
+  // uniform: the whole tile is inside M x N and the output rows take 4-wide vector stores
+  const bool full = m0 + BM <= M && n0 + BN <= N && (EPI == EPI_CALIB || e.vec_ok);
   const int rsub = lane >> 3;            // read-back: row rr * 8 + rsub, columns 4 * (lane & 7) .. +3
   const int cq = lane & 7;
 #pragma unroll
@@ -484,12 +541,19 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
       }
     }
     const int64_t n = n0 + wn * TN + j * 32 + cq * 4;
-    EpiCols<EPI> cols(e, n, N);
-#pragma unroll 4
-    for (int rr = 0; rr < TM / 8; ++rr) {
-      const int row = rr * 8 + rsub;
-      const i32x4 v = *reinterpret_cast<const i32x4*>(stg + row * PITCH + cq * 16);
-      epilogue4<EPI>(e, m0 + wm * TM + row, n, M, N, v, calib, cols);
+    if (full) {
+#pragma unroll
+      for (int rr = 0; rr < TM / 8; ++rr) {
+        const int row = rr * 8 + rsub;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(stg + row * PITCH + cq * 16);
+        epilogue4<EPI, true>(e, m0 + wm * TM + row, n, M, N, v, calib, cols_pre[j], sx_pre[DQ ? rr : 0]);
+      }
+    } else {
+      for (int rr = 0; rr < TM / 8; ++rr) {
+        const int row = rr * 8 + rsub;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(stg + row * PITCH + cq * 16);
+        epilogue4<EPI, false>(e, m0 + wm * TM + row, n, M, N, v, calib, cols_pre[j], sx_pre[DQ ? rr : 0]);
+      }
     }
   }
   calib_flush<EPI>(e, calib);
@@ -543,7 +607,10 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
   for (int v = 1; v < WAVES; ++v) acc += red[v][lane];
   int calib = 0;
   const EpiCols<EPI> cols(e, n0 + 4 * (lane >> 4), N);
-  epilogue4<EPI>(e, m0 + (lane & 15), n0 + 4 * (lane >> 4), M, N, acc, calib, cols);
+  const int64_t mrow = m0 + (lane & 15);
+  float sxm = 0.0f;
+  if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16) sxm = mrow < M ? e.sx[mrow] : 0.0f;
+  epilogue4<EPI>(e, mrow, n0 + 4 * (lane >> 4), M, N, acc, calib, cols, sxm);
   calib_flush<EPI>(e, calib);
 }
 
