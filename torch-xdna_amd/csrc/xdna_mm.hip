@@ -28,6 +28,9 @@
 // columns, its waves split K, each lane streams 32 contiguous weight bytes per step (so every
 // weight row is read as whole 128-byte lines), and the partial sums meet in LDS.
 #include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <string>
 #include <type_traits>
 
@@ -274,6 +277,20 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t off, in
 // Scheduling groups for __builtin_amdgcn_sched_group_barrier.
 constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100;
 
+// Emits NX groups "1 instruction of kind X, then its share of NM MFMAs" (shares differ by at most
+// one), i.e. spreads NX memory instructions evenly over NM MFMAs in the scheduling region.
+template <int X, int NX, int NM, int G>
+struct PinGroups {
+  __device__ __forceinline__ static void emit() {
+    if constexpr (G < NX) {
+      __builtin_amdgcn_sched_group_barrier(X, 1, 0);
+      constexpr int nm = NM * (G + 1) / NX - NM * G / NX;
+      if constexpr (nm > 0) __builtin_amdgcn_sched_group_barrier(SG_MFMA, nm, 0);
+      PinGroups<X, NX, NM, G + 1>::emit();
+    }
+  }
+};
+
 
 // Tile engine. Each K slice (128 bytes of K) of the A and W tiles is brought into LDS by the DMA
 // form of the buffer load: one wave instruction fills 8 whole 128-byte LDS rows, and each lane
@@ -463,15 +480,7 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
   // Pinned order inside each sub-step: the next sub-step's fragment reads are spread between this
   // sub-step's MFMAs (one read per NMF / NRD MFMAs), so no MFMA waits on LDS.
   constexpr int NMF = FM * FN, NRD = FM + FN, NDMA = IA + IW;
-  auto pin_reads = [&]() {
-    if constexpr (NMF % NRD == 0) {
-#pragma unroll
-      for (int g = 0; g < NRD; ++g) {
-        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, NMF / NRD, 0);
-      }
-    }
-  };
+  auto pin_reads = [&]() { PinGroups<SG_DS_READ, NRD, NMF, 0>::emit(); };
   auto substep = [&](const int8_t* stage, int ks_next, int set_next, int set) {
     read_frags(stage, ks_next, set_next);
     mfmas(set);
@@ -497,13 +506,7 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
     if constexpr (NEXT) read_frags(nxt, 0, 0);
     mfmas(1);
     // DMA issue spread over the last sub-step's MFMAs
-    if constexpr (DMA && NMF >= NDMA && NMF % NDMA == 0) {
-#pragma unroll
-      for (int g = 0; g < NDMA; ++g) {
-        __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, NMF / NDMA, 0);
-      }
-    }
+    if constexpr (DMA) PinGroups<SG_VMEM_READ, NDMA, NMF, 0>::emit();
     __builtin_amdgcn_sched_barrier(0);
   };
   using T_ = std::integral_constant<bool, true>;
@@ -516,15 +519,15 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
 
   // Epilogue through LDS. The 32x32 accumulator of tile (j, i) holds, in lane l, output row
   // m = i * 32 + l % 32 of the wave tile and, in element 4 * g + r, column 8 * g + 4 * (l / 32) + r of
-  // column block j. Each column block is written to a per-wave LDS staging area as int32 rows of
-  // 32 columns (pitch 144 bytes: conflict-free for these 16-byte writes and reads), then read back
-  // four consecutive columns per lane, eight lanes per row, and finished by the epilogue: every store
-  // instruction writes whole contiguous row pieces instead of 4 columns of 64 different rows.
+  // column block j. Each accumulator block goes to a per-wave LDS staging area as 32 int32 rows of
+  // 32 columns (pitch 144 bytes: conflict-free for these 16-byte writes and reads), and is read back
+  // four consecutive columns per lane, eight lanes per row, for the epilogue: every store instruction
+  // writes whole contiguous row pieces instead of 4 columns of 64 different rows.
   constexpr int PITCH = 144;
-  static_assert(NW * TM * PITCH <= 2 * STAGE, "staging does not fit in LDS");
+  static_assert(NW * 32 * PITCH <= 2 * STAGE, "staging does not fit in LDS");
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();                       // every wave is done with the K-loop's LDS stages
-  int8_t* stg = lds0 + wave * TM * PITCH;
+  int8_t* stg = lds0 + wave * 32 * PITCH;
   int calib = 0;
   // uniform: the whole tile is inside M x N and the output rows take 4-wide vector stores
   const bool full = m0 + BM <= M && n0 + BN <= N && (EPI == EPI_CALIB || e.vec_ok);
@@ -532,27 +535,22 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
   const int cq = lane & 7;
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
+    const int64_t n = n0 + wn * TN + j * 32 + cq * 4;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const i32x4 v = {acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]};
-        *reinterpret_cast<i32x4*>(stg + (i * 32 + (lane & 31)) * PITCH + (8 * g + 4 * (lane >> 5)) * 4) = v;
+        *reinterpret_cast<i32x4*>(stg + (lane & 31) * PITCH + (8 * g + 4 * (lane >> 5)) * 4) = v;
       }
-    }
-    const int64_t n = n0 + wn * TN + j * 32 + cq * 4;
-    if (full) {
 #pragma unroll
-      for (int rr = 0; rr < TM / 8; ++rr) {
+      for (int rr = 0; rr < 4; ++rr) {
         const int row = rr * 8 + rsub;
         const i32x4 v = *reinterpret_cast<const i32x4*>(stg + row * PITCH + cq * 16);
-        epilogue4<EPI, true>(e, m0 + wm * TM + row, n, M, N, v, calib, cols_pre[j], sx_pre[DQ ? rr : 0]);
-      }
-    } else {
-      for (int rr = 0; rr < TM / 8; ++rr) {
-        const int row = rr * 8 + rsub;
-        const i32x4 v = *reinterpret_cast<const i32x4*>(stg + row * PITCH + cq * 16);
-        epilogue4<EPI, false>(e, m0 + wm * TM + row, n, M, N, v, calib, cols_pre[j], sx_pre[DQ ? rr : 0]);
+        const int64_t m = m0 + wm * TM + i * 32 + row;
+        const float sxm = sx_pre[DQ ? i * 4 + rr : 0];
+        if (full) epilogue4<EPI, true>(e, m, n, M, N, v, calib, cols_pre[j], sxm);
+        else epilogue4<EPI, false>(e, m, n, M, N, v, calib, cols_pre[j], sxm);
       }
     }
   }
@@ -616,7 +614,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
 
 // ------------------------------------------------------------------------------ dispatch
 struct TileCfg {
-  int bm, bn;
+  int bm, bn, waves;
 };
 
 int g_num_cus = 0;
@@ -633,14 +631,27 @@ int num_cus() {
   return g_num_cus;
 }
 
-// Pick the largest tile that still gives every CU work; a 256x256 tile needs 128 KB of LDS and
-// runs one workgroup per CU, a 128x128 tile two to three, a 64x64 tile up to eight.
+// Tile choice, from a sweep of every tile shape over the BASELINE shapes on MI355X: 256 x 256 tiles
+// with 8 waves (two per SIMD, one workgroup per CU) win from about 1.75 rounds of such tiles; 128 x 128
+// tiles (two workgroups per CU) win whenever they fill the CUs once; 64 x 64 tiles win for smaller
+// problems and for N <= 64.
 TileCfg pick_tile(int64_t M, int64_t N) {
+  // XDNA_GEMM_TILE=<bm>x<bn> forces a tile shape (tile sweeps); ignored unless it names a built one
+  if (const char* env = std::getenv("XDNA_GEMM_TILE")) {
+    int bm = 0, bn = 0, waves = 4;
+    const int got = std::sscanf(env, "%dx%dw%d", &bm, &bn, &waves);
+    if (got >= 2 && ((bm == 256 && bn == 256 && (waves == 4 || waves == 8)) ||
+                     (waves == 4 && ((bm == 256 && bn == 128) || (bm == 128 && (bn == 256 || bn == 128)) ||
+                                     (bm == 64 && bn == 64)))))
+      return {bm, bn, waves};
+  }
   const int64_t cus = num_cus();
-  auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  if (M >= 256 && N >= 256 && tiles(256, 256) >= cus) return {256, 256};
-  if (M >= 128 && N >= 128 && tiles(128, 128) >= cus) return {128, 128};
-  return {64, 64};
+  if (M <= 64 || N <= 64) return {64, 64, 4};
+  const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (4 * t256 >= 7 * cus) return {256, 256, 8};
+  if (t128 >= cus) return {128, 128, 4};
+  return {64, 64, 4};
 }
 
 // Buffer resources address at most 2 GB; larger operands are processed in row chunks.
@@ -657,17 +668,25 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
   }
   dim3 grid((unsigned)tiles, 1, 1);
   const bool kfull = K % 128 == 0;
-#define XDNA_TILE(BM_, BN_)                                                                                \
-  if (kfull) mm_tile_kernel<BM_, BN_, 2, 2, CONVM, EPI, true><<<grid, 256, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e); \
-  else mm_tile_kernel<BM_, BN_, 2, 2, CONVM, EPI, false><<<grid, 256, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
-  if (t.bm == 256) {
+#define XDNA_TILE_W(BM_, BN_, WM_, WN_)                                                                       \
+  if (kfull) mm_tile_kernel<BM_, BN_, WM_, WN_, CONVM, EPI, true><<<grid, WM_ * WN_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e); \
+  else mm_tile_kernel<BM_, BN_, WM_, WN_, CONVM, EPI, false><<<grid, WM_ * WN_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
+#define XDNA_TILE(BM_, BN_) XDNA_TILE_W(BM_, BN_, 2, 2)
+  if (t.bm == 256 && t.bn == 256 && t.waves == 8) {
+    XDNA_TILE_W(256, 256, 2, 4)
+  } else if (t.bm == 256 && t.bn == 256) {
     XDNA_TILE(256, 256)
+  } else if (t.bm == 256) {
+    XDNA_TILE(256, 128)
+  } else if (t.bn == 256) {
+    XDNA_TILE(128, 256)
   } else if (t.bm == 128) {
     XDNA_TILE(128, 128)
   } else {
     XDNA_TILE(64, 64)
   }
 #undef XDNA_TILE
+#undef XDNA_TILE_W
   return launch_status("mm_tile");
 }
 

@@ -151,17 +151,18 @@ def num_cus(dev) -> int:
 
 
 def gemm_variant(dev, M, N) -> str:
-    """Which GEMM kernel the library runs for M x N (mirrors launch_mm's choice): one NPU-program
+    """Which GEMM kernel the library runs for M x N (mirrors the library's pick_tile): one NPU-program
     key of the reference (runtime.py:207) corresponds to one (variant, N, K) here."""
     if M <= 64:
         return "small"
     cus = num_cus(dev)
-    tiles = lambda bm, bn: -(-M // bm) * -(-N // bn)  # noqa: E731
-    if M >= 256 and N >= 256 and tiles(256, 256) >= cus:
-        return "t256"
-    if M >= 128 and N >= 128 and tiles(128, 128) >= cus:
-        return "t128"
-    return "t64"
+    if N <= 64:
+        return "t64x64"
+    if 4 * (-(-M // 256) * -(-N // 256)) >= 7 * cus:
+        return "t256x256w8"
+    if -(-M // 128) * -(-N // 128) >= cus:
+        return "t128x128"
+    return "t64x64"
 
 
 # ------------------------------------------------------------------------------ launchers
