@@ -13,7 +13,9 @@ configs; seed 0), with inputs and device-resident int8 weights already in HBM:
   c3            4 x (conv3x3 + ReLU), 256 ch, 1x256x64x64, quantize -> conv -> dequantize per layer.
   c4            conv3x3 256->256 on 1x256x1536x64 (int8 conv kernel, the shift already fixed).
   c5            W8A8 GEMM, bf16 in/out with bias, K 4096 N 14336 M 8192 (the largest config).
+  decode        the C5 decode GEMMs (M 1 and 16), HBM-bound: roofline in GB/s of algorithmic bytes.
   quant         the activation quantize kernel alone, bf16 [8192, 14336].
+  copy          calibration of the HBM byte counters (a 1 GiB read + 1 GiB write elementwise kernel).
 
 Weight / activation sets are rotated so a step's working set exceeds the 256 MB MALL. Timing:
 W untimed steps, then K steps bracketed by torch.cuda.synchronize(); the dominant kernel is also
@@ -48,7 +50,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "quant"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "decode", "quant", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -63,10 +65,10 @@ class Timer:
     def __init__(self):
         self.pairs = []
 
-    def __call__(self, fn, *a):
+    def __call__(self, fn, *a, **kw):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        out = fn(*a)
+        out = fn(*a, **kw)
         e.record()
         self.pairs.append((s, e))
         return out
@@ -194,57 +196,89 @@ def main():
            "unit": "TOPS", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic (seed 0, randn)"}
     bench = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
-             "quant": bench_quant}[a.workload]
+             "decode": bench_decode, "quant": bench_quant, "copy": bench_copy}[a.workload]
     res.update(bench(a, dev))
     print(json.dumps(res), flush=True)
 
 
-def timed_steps(a, step):
+def timed_steps(a, step, timer):
+    """W untimed steps, then K timed steps bracketed by synchronize. step(i, t) launches one step;
+    t is the Timer during the timed steps (it records HIP events around the dominant kernel's
+    launches on torch's current stream, the stream they run on) and None during the warm-up."""
     for i in range(a.warmup):
-        step(i)
+        step(i, None)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
-        step(i)
+        step(i, timer)
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / a.steps
 
 
-def gemm_result(a, dev, shapes, x_dtype, bias, workload, label):
+def traffic(workload):
+    """Measured HBM bytes per launch of the dominant kernel (FETCH_SIZE + WRITE_SIZE per dispatch,
+    scaled by the same counters on a copy of known size), from profiles/hbm_traffic.json, which
+    records the rocprofv3 commands that measured them; None when not measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
+            t = json.load(f)[workload]
+        return t["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def roofline_us(ops, nbytes):
+    """Lower bound on a launch's duration from the two MI355X ceilings, in microseconds."""
+    return max(ops / (PEAK_INT8_TOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) * 1e6
+
+
+def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
     sets = gemm_sets(shapes, dev, x_dtype=x_dtype, bias=bias)
-    sec = timed_steps(a, lambda i: run_gemm_step(sets[i % len(sets)]))
-    # per-launch timing of the dominant kernel (GEMM) and of the quantize, over a few more steps
-    gt, qt = Timer(), Timer()
-    reps = max(3, min(a.steps, 10))
-    for i in range(reps):
-        run_gemm_step(sets[i % len(sets)], gt, qt)
-    g_ms, q_ms = gt.ms(), qt.ms()
+    gt = Timer()
+    sec = timed_steps(a, lambda i, t: run_gemm_step(sets[i % len(sets)], t), gt)
+    g_ms = gt.ms()
+    reps = a.steps
+    # per-launch timing of the quantize kernel, over a few steps after the timed region
+    qt = Timer()
+    qreps = 3
+    for i in range(qreps):
+        run_gemm_step(sets[i % len(sets)], None, qt)
+    q_ms = qt.ms()
     ops_step = sum(2 * M * N * K for M, N, K in shapes)
     yb = 2 if x_dtype != torch.float32 else 4
     xb = x_dtype.itemsize
-    g_ops = ops_step * reps
-    g_bytes = sum(gemm_bytes(M, N, K, xb, yb, bias) for M, N, K in shapes) * reps
     g_sec = sum(g_ms) / 1e3
-    q_bytes = sum(quant_bytes(M, K, xb) for M, N, K in shapes) * reps
-    achieved = g_ops / g_sec / 1e12
+    g_bytes = sum(gemm_bytes(M, N, K, xb, yb, bias) for M, N, K in shapes) * reps
+    q_bytes = sum(quant_bytes(M, K, xb) for M, N, K in shapes) * qreps
+    achieved = ops_step * reps / g_sec / 1e12
+    bound_us = sum(roofline_us(2 * M * N * K, gemm_bytes(M, N, K, xb, yb, bias)) for M, N, K in shapes)
     out = {"value": round(ops_step / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
            "config": {"workload": workload, "shapes_mnk": shapes, "x_dtype": str(x_dtype).replace("torch.", ""),
                       "bias": bias, "rotating_sets": len(sets)},
            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                        "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
-                        "kernel": "mm_tile_kernel / mm_small_kernel (EPI_DQ)",
-                        "avg_launch_us": round(sum(g_ms) / len(g_ms) * 1e3, 2),
-                        "hbm_GBs_equiv": round(g_bytes / g_sec / 1e9, 1)},
+                        "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic(label.lower()),
+                        "kernel": "mm_tile_kernel (EPI_DQ_BF16/F32)" if min(s[0] for s in shapes) > 64
+                        else "mm_small_kernel (EPI_DQ_BF16)" if max(s[0] for s in shapes) <= 64
+                        else "mm_tile_kernel / mm_small_kernel (EPI_DQ)",
+                        "launches": len(g_ms), "avg_launch_us": round(sum(g_ms) / len(g_ms) * 1e3, 2),
+                        "alg_bytes_per_launch": round(g_bytes / len(g_ms)),
+                        "hbm_GBs_equiv": round(g_bytes / g_sec / 1e9, 1),
+                        "frac_of_attainable": round(bound_us * reps / (g_sec * 1e6), 4)},
            "quantize": {"achieved_GBs": round(q_bytes / (sum(q_ms) / 1e3) / 1e9, 1), "peak": PEAK_HBM_GBS,
                         "avg_launch_us": round(sum(q_ms) / len(q_ms) * 1e3, 2)},
            "per_shape": []}
+    if bound == "hbm":
+        gbs = g_bytes / g_sec / 1e9
+        out["roofline"].update({"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                "frac": round(gbs / PEAK_HBM_GBS, 4), "TOPS": round(achieved, 2)})
     n = len(shapes)
     for j, (M, N, K) in enumerate(shapes):
         gj = [g_ms[i * n + j] for i in range(reps)]
         t = sorted(gj)[len(gj) // 2] / 1e3
         b = gemm_bytes(M, N, K, xb, yb, bias)
         out["per_shape"].append({"mnk": [M, N, K], "us": round(t * 1e6, 2), "TOPS": round(2 * M * N * K / t / 1e12, 1),
-                                 "GBs": round(b / t / 1e9, 1)})
+                                 "GBs": round(b / t / 1e9, 1),
+                                 "roofline_us": round(roofline_us(2 * M * N * K, b), 2)})
     if not a.no_cpu_baseline:
         tops, nrep, best = cpu_baseline_gemm(shapes, x_dtype, bias)
         out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
@@ -271,14 +305,21 @@ def bench_c5(a, dev):
                        "C5 W8A8 GEMM M=8192 N=14336 K=4096 bf16 + bias", "C5")
 
 
+def bench_decode(a, dev):
+    shapes = [(M, N, K) for M in (1, 16) for N, K in ((4096, 4096), (14336, 4096), (4096, 14336))]
+    out = gemm_result(a, dev, shapes, torch.bfloat16, True,
+                      "C5 decode W8A8 GEMMs M in {1,16}, (N,K) in {(4096,4096),(14336,4096),(4096,14336)}, "
+                      "bf16 + bias", "decode", bound="hbm")
+    out["unit"] = "TOPS"
+    return out
+
+
 def bench_quant(a, dev):
     g = gen(0)
     M, K = 8192, 14336
     xs = [torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev) for _ in range(2)]
-    sec = timed_steps(a, lambda i: kernels.quant_rows(xs[i % 2]))
     t = Timer()
-    for i in range(10):
-        t(kernels.quant_rows, xs[i % 2])
+    sec = timed_steps(a, lambda i, tm: tm(kernels.quant_rows, xs[i % 2]) if tm else kernels.quant_rows(xs[i % 2]), t)
     ms = t.ms()
     b = quant_bytes(M, K, 2)
     gbs = b / (sum(ms) / len(ms) / 1e3) / 1e9
@@ -286,7 +327,27 @@ def bench_quant(a, dev):
             "ms_per_step": round(sec * 1e3, 4), "dtype": "bf16->int8",
             "config": {"workload": "quantize bf16 [8192, 14336] per row"},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": "quant_rows_vec_kernel"}}
+                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic("quant"),
+                         "kernel": "quant_rows_vec_kernel", "alg_bytes_per_launch": b}}
+
+
+def bench_copy(a, dev):
+    """Calibration for the HBM counters: an elementwise kernel that reads and writes 1 GiB each
+    (bitwise_not of int32), whose FETCH_SIZE / WRITE_SIZE should read 1 GiB each."""
+    n = 1 << 28
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (n,), dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    t = Timer()
+    sec = timed_steps(a, lambda i, tm: tm(torch.bitwise_not, src, out=dst) if tm
+                      else torch.bitwise_not(src, out=dst), t)
+    ms = t.ms()
+    b = 2 * n * 4
+    gbs = b / (sum(ms) / len(ms) / 1e3) / 1e9
+    return {"metric": "copy GB/s on 1 MI355X (counter calibration)", "unit": "GB/s",
+            "value": round(b / sec / 1e9, 1), "ms_per_step": round(sec * 1e3, 4), "dtype": "int32",
+            "config": {"workload": "bitwise_not int32 [2^28]: reads 1 GiB, writes 1 GiB"},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": b, "kernel": "torch elementwise"}}
 
 
 def conv_layer_data(dev, n, c, h, w, seed=0):
@@ -307,17 +368,17 @@ def bench_c4(a, dev):
         shift = 10
         sets.append((xq, wq, shift))
     torch.cuda.synchronize()
-    sec = timed_steps(a, lambda i: kernels.conv3x3(sets[i % 3][0], sets[i % 3][1], sets[i % 3][2], True))
     t = Timer()
-    for i in range(10):
-        t(kernels.conv3x3, sets[i % 3][0], sets[i % 3][1], sets[i % 3][2], True)
+    sec = timed_steps(a, lambda i, tm: (tm or (lambda f, *x: f(*x)))(kernels.conv3x3, *sets[i % 3], True), t)
     ms = t.ms()
     ops = 2 * n * h * w * c * c * 9
     ach = ops / (sum(ms) / len(ms) / 1e3) / 1e12
     out = {"value": round(ops / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
            "config": {"workload": "C4 int8 conv3x3 256->256 on 1x256x1536x64, ReLU, NHWC int8 in/out"},
            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                        "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None, "kernel": "mm_tile_kernel (conv)"}}
+                        "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic("c4"), "kernel": "mm_tile_kernel (conv)",
+                        "avg_launch_us": round(sum(ms) / len(ms) * 1e3, 2),
+                        "alg_bytes_per_launch": n * c * h * w * 2 + 9 * c * c + 4 * c}}
     if not a.no_cpu_baseline:
         tops, nrep, best = cpu_baseline_conv(1, 256, 128, 64, 1)
         out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
@@ -357,17 +418,16 @@ def bench_c3(a, dev):
             y = kernels.conv_dequant(q, True, sc, sx, None, torch.float32)
         return y
 
-    sec = timed_steps(a, step)
     ct = Timer()
-    for i in range(5):
-        step(i, ct)
+    sec = timed_steps(a, step, ct)
     ms = ct.ms()
     ops = 2 * n * h * w * c * c * 9
     ach = ops / (sum(ms) / len(ms) / 1e3) / 1e12
     out = {"value": round(ops * L / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
            "config": {"workload": "C3 4x (conv3x3 256->256 + ReLU) on 1x256x64x64, quantize/conv/dequantize per layer"},
            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                        "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None, "kernel": "mm_tile_kernel (conv)"}}
+                        "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic("c3"), "kernel": "mm_tile_kernel (conv)",
+                        "avg_launch_us": round(sum(ms) / len(ms) * 1e3, 2)}}
     if not a.no_cpu_baseline:
         tops, nrep, best = cpu_baseline_conv(n, c, h, w, L)
         out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),

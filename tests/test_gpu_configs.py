@@ -1,8 +1,9 @@
 """BASELINE.json configs C1-C5 on the MI355X through the public ops, against the oracle.
 
-C1, C2, C3 and the decode GEMMs of C5 are compared in full (int32 sums from the C oracle, the rest
-from the numpy oracle). The full-size C4 conv and the M=8192 C5 GEMM are too large for a CPU oracle
-within seconds, so they are checked by size-independent properties: exact row and column checksums
+C1, C2, C3, the VGG16 layers of C4 and the decode / M=256 GEMMs of C5 are compared in full (int32
+sums from the C oracle, the rest from the numpy oracle). The full-size 256-channel C4 convs and the
+M=8192 C5 GEMMs are too large for a CPU oracle within seconds, so they are checked by
+size-independent properties: exact row and column checksums
 of the int32 GEMM (sum_n C = A (sum_n W), sum_m C = (sum_m A) W^T, in int64), and exact values at a
 few thousand random positions (int64 dot products / conv sums on the CPU), for the int32 output and
 for the fused bf16 / requantized outputs.
@@ -128,6 +129,38 @@ def test_c4_large_conv_sampled(gpu, shape):
     assert np.array_equal(xq_nchw, xq_r) and np.array_equal(sx.cpu().numpy(), sx_r)
 
 
+# VGG16's thirteen 3x3 convs have these nine distinct (Ci, Co, H=W) shapes
+VGG16_LAYERS = [(3, 64, 224), (64, 64, 224), (64, 128, 112), (128, 128, 112), (128, 256, 56), (256, 256, 56),
+                (256, 512, 28), (512, 512, 28), (512, 512, 14)]
+
+
+@pytest.mark.parametrize("ci,co,hw", VGG16_LAYERS)
+def test_c4_vgg16_layer(gpu, ci, co, hw):
+    """C4's VGG16 layers at batch 8 with ReLU: the quantized images and packed weights, the GPU
+    calibration max on image 0 (it must give the oracle's shift), and every requantized output of the
+    batch, against the C oracle's exact sums."""
+    from torch_xdna import kernels
+
+    g = _gen(ci * 1000 + hw)
+    x = torch.randn(8, ci, hw, hw, generator=g)
+    wt = torch.randn(co, ci, 3, 3, generator=g) * 0.02
+    c_pad = kernels.round_up(ci, 16)
+    xq, sx = kernels.conv_quant(x.to(gpu), c_pad)
+    wq, sw = kernels.conv_weight_pack(wt.to(gpu), c_pad)
+    xq_r, sx_r = O.conv_quant_images(x.numpy())
+    wq_r, sw_r = O.conv_weight_quant(wt.numpy())
+    assert np.array_equal(xq[..., :ci].permute(0, 3, 1, 2).cpu().numpy(), xq_r)
+    assert not xq[..., ci:].any() and np.array_equal(sx.cpu().numpy(), sx_r)
+    wq_g = wq.view(co, 3, 3, c_pad)
+    assert np.array_equal(wq_g[..., :ci].permute(0, 3, 1, 2).cpu().numpy(), wq_r) and not wq_g[..., ci:].any()
+    assert np.array_equal(sw.cpu().numpy(), sw_r)
+    acc = c_oracle.conv3x3_acc(xq_r, wq_r)
+    shift = O.calibrate_shift(acc[0], True)
+    assert kernels.conv3x3_calibrate(xq[:1], wq, True) == int(np.maximum(acc[0], 0).max())
+    q = kernels.conv3x3(xq, wq, shift, True)
+    assert np.array_equal(q.permute(0, 3, 1, 2).cpu().numpy(), O.requant(acc, shift, True))
+
+
 @pytest.mark.parametrize("M,N,K", [(8192, 14336, 4096), (8192, 4096, 14336), (2048, 4096, 4096)])
 def test_c5_large_gemm_properties(gpu, M, N, K):
     from torch_xdna import kernels
@@ -161,9 +194,10 @@ def test_c5_large_gemm_properties(gpu, M, N, K):
     assert np.array_equal(y.float().cpu().numpy()[ms, ns], yw)
 
 
-@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("M", [1, 16, 256])
 @pytest.mark.parametrize("N,K", [(4096, 4096), (14336, 4096), (4096, 14336)])
 def test_c5_decode_gemm(gpu, M, N, K):
+    """C5's decode and M=256 GEMMs, every output against the C oracle."""
     from torch_xdna import kernels
 
     g = _gen(M * 7 + N + K)

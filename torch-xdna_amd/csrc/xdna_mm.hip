@@ -2,15 +2,18 @@
 //
 // One tile engine serves both ops. A workgroup computes a BM x BN tile of D = A * W^T with
 // A [M, K] and W [N, K] int8, both K-contiguous, accumulating in int32 with
-// v_mfma_i32_16x16x64_i8. The MFMA is issued as D^T = W * A^T (W fragment in srcA, A fragment in
-// srcB), so each lane ends up holding four consecutive output columns n of one row m, and the
-// epilogue writes 16-byte (int32 / fp32) or 8-byte (bf16) pieces of output rows.
+// v_mfma_i32_32x32x32_i8 (the full-rate int8 MFMA of gfx950). The MFMA is issued as
+// D^T = W * A^T (W fragment in srcA, A fragment in srcB), so each lane holds consecutive output
+// columns n of one row m. Tiles: 256x256 with 8 waves (two per SIMD), 256x128 / 128x256 /
+// 128x128 with 4 waves, 64x64 with 4 waves; the host picks one per shape.
 //
-// K is staged through LDS in 128-byte slices, double-buffered: while the waves run the MFMAs of
-// slice kt from one LDS buffer, the next slice's global loads are in flight in registers and are
-// written to the other buffer afterwards (one barrier per slice). LDS rows are 128 bytes; the
-// 16-byte chunk c of row r is stored at chunk c ^ (r & 7), so the eight rows a fragment read
-// touches in one pass land in eight different bank groups.
+// K is staged through LDS in 128-byte slices, two stages deep, by the LDS-DMA form of the raw
+// buffer load: each lane's 16 bytes land at M0 + 16 * lane, so no VGPRs carry the tile. The DMA
+// of slice kt + 2 is issued after the one barrier per slice and overlaps the MFMAs of kt + 1.
+// LDS rows are 128 bytes; the 16-byte chunk c of row r sits at chunk c ^ f(r) with
+// f(r) = (r & 7) ^ ((r >> 3) & 1), which keeps the 8- and 16-lane phases of a fragment read on
+// distinct bank groups and is periodic in 16 rows, so fragment offsets are immediates.
+// Out-of-range rows, K chunks and conv halo pixels are out-of-range buffer loads, which read 0.
 //
 // Integer sums are exact, so the order in which K is split between lanes, MFMAs or waves does not
 // change the result: the only requirement is that the A and W fragments of one MFMA pair the same
