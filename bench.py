@@ -19,8 +19,10 @@ configs; seed 0), with inputs and device-resident int8 weights already in HBM:
 
 Weight / activation sets are rotated so a step's working set exceeds the 256 MB MALL. Timing:
 W untimed steps, then K steps bracketed by torch.cuda.synchronize(); the dominant kernel is also
-timed per launch with HIP events on the stream it runs on (torch's current stream). Rank 0 prints
-one JSON line. The CPU baseline is the reference's CPU route (oracle/cpu_route.py: torch CPU
+timed per launch with HIP events on the stream it runs on (torch's current stream). The timed
+steps are enqueued behind a GPU spin kernel that outlasts the host's enqueue time, so they run back
+to back and the events measure GPU time only; the ungated wall-clock time per step (host launch
+cost included) is reported beside it. Rank 0 prints one JSON line. The CPU baseline is the reference's CPU route (oracle/cpu_route.py: torch CPU
 quantize, torch._int_mm or an exact float conv, dequantize) timed on the host cores on a bounded
 sample of the same workload.
 """
@@ -97,6 +99,21 @@ def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed
         sets.append(items)
     torch.cuda.synchronize()
     return sets
+
+
+def run_gemm_step_split(items, ev=None):
+    """One step ordered as all activation quantizes, then all fused GEMMs (the same work as
+    run_gemm_step); ev = three events recorded at the start, between the two groups and at the end,
+    so ev[1] -> ev[2] brackets exactly the step's GEMM launches, back to back."""
+    if ev:
+        ev[0].record()
+    qs = [kernels.quant_rows(x) for x, *_ in items]
+    if ev:
+        ev[1].record()
+    for (x, wq, sw, b, M, N, K), (xq, sx) in zip(items, qs):
+        kernels.mm_i8_dequant(xq, sx, wq, sw, b, x.dtype)
+    if ev:
+        ev[2].record()
 
 
 def run_gemm_step(items, timer=None, qtimer=None):
@@ -202,15 +219,76 @@ def main():
 
 
 def timed_steps(a, step, timer):
-    """W untimed steps, then K timed steps bracketed by synchronize. step(i, t) launches one step;
-    t is the Timer during the timed steps (it records HIP events around the dominant kernel's
-    launches on torch's current stream, the stream they run on) and None during the warm-up."""
+    """W warm-up steps, an ungated wall-clock pass of the K steps (host launch cost included), then
+    the gated timed region (gated_timed_steps). Returns (GPU seconds per step, host seconds per step)."""
     for i in range(a.warmup):
         step(i, None)
+    host = eager_seconds(a, step)
+    return gated_timed_steps(a, step, timer, host * 1e3), host
+
+
+_SLEEP_CYCLES_PER_MS = None
+
+
+def gate(ms):
+    """Holds torch's current stream for about `ms` milliseconds with a GPU spin kernel, so that the
+    host can enqueue a whole timed region before the GPU reaches it: the region's kernels then run
+    back to back and HIP events between them bracket GPU work only."""
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        e0.record()
+        torch.cuda._sleep(2_000_000)
+        e1.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = 2_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(ms * _SLEEP_CYCLES_PER_MS))
+
+
+def gated_timed_steps(a, step, timer, host_ms_per_step):
+    """The timed region: a gate covering the host's enqueue time of the K steps (1.5 x the measured
+    ungated time + 2 ms), then K eager steps between two events; step(i, t) records per-launch
+    events of the dominant kernel with t. Returns GPU seconds per step."""
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gate(1.5 * host_ms_per_step * a.steps + 2.0)
+    e0.record()
+    for i in range(a.steps):
+        step(i, timer)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / a.steps
+
+
+def per_shape_us(sets, launches=10):
+    """Microseconds per launch of each shape's fused GEMM: `launches` back-to-back launches of that
+    shape (cycling through the weight sets) behind a gate, between two events."""
+    out = []
+    for j in range(len(sets[0])):
+        ops = []
+        for i in range(launches):
+            x, wq, sw, b, M, N, K = sets[i % len(sets)][j]
+            ops.append((kernels.quant_rows(x), wq, sw, b, x.dtype))
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        gate(2.0)
+        e0.record()
+        for (xq, sx), wq, sw, b, dt in ops:
+            kernels.mm_i8_dequant(xq, sx, wq, sw, b, dt)
+        e1.record()
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) * 1e3 / launches)
+    return out
+
+
+def eager_seconds(a, step):
+    """Wall-clock seconds per step of K steps launched eagerly without a gate (host launch cost
+    included)."""
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
-        step(i, timer)
+        step(i, None)
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / a.steps
 
@@ -234,25 +312,31 @@ def roofline_us(ops, nbytes):
 
 def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
     sets = gemm_sets(shapes, dev, x_dtype=x_dtype, bias=bias)
-    gt = Timer()
-    sec = timed_steps(a, lambda i, t: run_gemm_step(sets[i % len(sets)], t), gt)
-    g_ms = gt.ms()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(a.steps)]
+    step = lambda i, t: run_gemm_step_split(sets[i % len(sets)], ev[i] if t else None)   # noqa: E731
+    for i in range(a.warmup):
+        step(i, None)
+    host = eager_seconds(a, step)
+    sec = gated_timed_steps(a, step, True, host * 1e3)
+    q_ms = [e[0].elapsed_time(e[1]) for e in ev]      # per step: the quantizes, back to back
+    g_ms = [e[1].elapsed_time(e[2]) for e in ev]      # per step: the GEMMs, back to back
     reps = a.steps
-    # per-launch timing of the quantize kernel, over a few steps after the timed region
-    qt = Timer()
-    qreps = 3
-    for i in range(qreps):
-        run_gemm_step(sets[i % len(sets)], None, qt)
-    q_ms = qt.ms()
+    per_shape = per_shape_us(sets)
     ops_step = sum(2 * M * N * K for M, N, K in shapes)
     yb = 2 if x_dtype != torch.float32 else 4
     xb = x_dtype.itemsize
-    g_sec = sum(g_ms) / 1e3
+    nshape = len(shapes)
+    g_sec = sum(g_ms) / 1e3                            # GEMM launches of the timed steps
     g_bytes = sum(gemm_bytes(M, N, K, xb, yb, bias) for M, N, K in shapes) * reps
-    q_bytes = sum(quant_bytes(M, K, xb) for M, N, K in shapes) * qreps
+    q_bytes = sum(quant_bytes(M, K, xb) for M, N, K in shapes) * reps
+    q_sec = sum(q_ms) / 1e3
     achieved = ops_step * reps / g_sec / 1e12
     bound_us = sum(roofline_us(2 * M * N * K, gemm_bytes(M, N, K, xb, yb, bias)) for M, N, K in shapes)
     out = {"value": round(ops_step / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
+           "host_ms_per_step": round(host * 1e3, 4),
+           "timing": "GPU time of K eager steps enqueued behind a gate (kernels back to back), each "
+                     "step's quantizes then its GEMMs with events between; host_ms_per_step: the same "
+                     "steps launched without a gate, wall clock",
            "config": {"workload": workload, "shapes_mnk": shapes, "x_dtype": str(x_dtype).replace("torch.", ""),
                       "bias": bias, "rotating_sets": len(sets)},
            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
@@ -260,21 +344,19 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
                         "kernel": "mm_tile_kernel (EPI_DQ_BF16/F32)" if min(s[0] for s in shapes) > 64
                         else "mm_small_kernel (EPI_DQ_BF16)" if max(s[0] for s in shapes) <= 64
                         else "mm_tile_kernel / mm_small_kernel (EPI_DQ)",
-                        "launches": len(g_ms), "avg_launch_us": round(sum(g_ms) / len(g_ms) * 1e3, 2),
-                        "alg_bytes_per_launch": round(g_bytes / len(g_ms)),
+                        "launches": nshape * reps, "avg_launch_us": round(g_sec / (nshape * reps) * 1e6, 2),
+                        "alg_bytes_per_launch": round(g_bytes / (nshape * reps)),
                         "hbm_GBs_equiv": round(g_bytes / g_sec / 1e9, 1),
                         "frac_of_attainable": round(bound_us * reps / (g_sec * 1e6), 4)},
-           "quantize": {"achieved_GBs": round(q_bytes / (sum(q_ms) / 1e3) / 1e9, 1), "peak": PEAK_HBM_GBS,
-                        "avg_launch_us": round(sum(q_ms) / len(q_ms) * 1e3, 2)},
+           "quantize": {"achieved_GBs": round(q_bytes / q_sec / 1e9, 1), "peak": PEAK_HBM_GBS,
+                        "avg_launch_us": round(q_sec / (nshape * reps) * 1e6, 2)},
            "per_shape": []}
     if bound == "hbm":
         gbs = g_bytes / g_sec / 1e9
         out["roofline"].update({"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                 "frac": round(gbs / PEAK_HBM_GBS, 4), "TOPS": round(achieved, 2)})
-    n = len(shapes)
     for j, (M, N, K) in enumerate(shapes):
-        gj = [g_ms[i * n + j] for i in range(reps)]
-        t = sorted(gj)[len(gj) // 2] / 1e3
+        t = per_shape[j] / 1e6
         b = gemm_bytes(M, N, K, xb, yb, bias)
         out["per_shape"].append({"mnk": [M, N, K], "us": round(t * 1e6, 2), "TOPS": round(2 * M * N * K / t / 1e12, 1),
                                  "GBs": round(b / t / 1e9, 1),
@@ -319,12 +401,12 @@ def bench_quant(a, dev):
     M, K = 8192, 14336
     xs = [torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev) for _ in range(2)]
     t = Timer()
-    sec = timed_steps(a, lambda i, tm: tm(kernels.quant_rows, xs[i % 2]) if tm else kernels.quant_rows(xs[i % 2]), t)
+    sec, host = timed_steps(a, lambda i, tm: tm(kernels.quant_rows, xs[i % 2]) if tm else kernels.quant_rows(xs[i % 2]), t)
     ms = t.ms()
     b = quant_bytes(M, K, 2)
     gbs = b / (sum(ms) / len(ms) / 1e3) / 1e9
     return {"metric": "activation quantize GB/s on 1 MI355X", "unit": "GB/s", "value": round(b / sec / 1e9, 1),
-            "ms_per_step": round(sec * 1e3, 4), "dtype": "bf16->int8",
+            "ms_per_step": round(sec * 1e3, 4), "host_ms_per_step": round(host * 1e3, 4), "dtype": "bf16->int8",
             "config": {"workload": "quantize bf16 [8192, 14336] per row"},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic("quant"),
@@ -338,13 +420,14 @@ def bench_copy(a, dev):
     src = torch.randint(-2 ** 31, 2 ** 31 - 1, (n,), dtype=torch.int32, device=dev)
     dst = torch.empty_like(src)
     t = Timer()
-    sec = timed_steps(a, lambda i, tm: tm(torch.bitwise_not, src, out=dst) if tm
+    sec, host = timed_steps(a, lambda i, tm: tm(torch.bitwise_not, src, out=dst) if tm
                       else torch.bitwise_not(src, out=dst), t)
     ms = t.ms()
     b = 2 * n * 4
     gbs = b / (sum(ms) / len(ms) / 1e3) / 1e9
     return {"metric": "copy GB/s on 1 MI355X (counter calibration)", "unit": "GB/s",
-            "value": round(b / sec / 1e9, 1), "ms_per_step": round(sec * 1e3, 4), "dtype": "int32",
+            "value": round(b / sec / 1e9, 1), "ms_per_step": round(sec * 1e3, 4), "host_ms_per_step": round(host * 1e3, 4),
+            "dtype": "int32",
             "config": {"workload": "bitwise_not int32 [2^28]: reads 1 GiB, writes 1 GiB"},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": b, "kernel": "torch elementwise"}}
@@ -369,11 +452,12 @@ def bench_c4(a, dev):
         sets.append((xq, wq, shift))
     torch.cuda.synchronize()
     t = Timer()
-    sec = timed_steps(a, lambda i, tm: (tm or (lambda f, *x: f(*x)))(kernels.conv3x3, *sets[i % 3], True), t)
+    sec, host = timed_steps(a, lambda i, tm: (tm or (lambda f, *x: f(*x)))(kernels.conv3x3, *sets[i % 3], True), t)
     ms = t.ms()
     ops = 2 * n * h * w * c * c * 9
     ach = ops / (sum(ms) / len(ms) / 1e3) / 1e12
     out = {"value": round(ops / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
+           "host_ms_per_step": round(host * 1e3, 4),
            "config": {"workload": "C4 int8 conv3x3 256->256 on 1x256x1536x64, ReLU, NHWC int8 in/out"},
            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic("c4"), "kernel": "mm_tile_kernel (conv)",
@@ -419,11 +503,12 @@ def bench_c3(a, dev):
         return y
 
     ct = Timer()
-    sec = timed_steps(a, step, ct)
+    sec, host = timed_steps(a, step, ct)
     ms = ct.ms()
     ops = 2 * n * h * w * c * c * 9
     ach = ops / (sum(ms) / len(ms) / 1e3) / 1e12
     out = {"value": round(ops * L / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
+           "host_ms_per_step": round(host * 1e3, 4),
            "config": {"workload": "C3 4x (conv3x3 256->256 + ReLU) on 1x256x64x64, quantize/conv/dequantize per layer"},
            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic("c3"), "kernel": "mm_tile_kernel (conv)",

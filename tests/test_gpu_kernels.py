@@ -129,6 +129,29 @@ def test_gemm_dequant(gpu, out, m, n, k, bias):
     assert not bad.any(), f"{bad.sum()} of {got.size} differ, e.g. {got[bad][:4]} vs {want[bad][:4]}"
 
 
+@pytest.mark.parametrize("out", ["f32", "bf16", "f16"])
+def test_gemm_dequant_range(gpu, out):
+    """Scales from 1e-45 to 3e38 put the fused epilogue's outputs in every float range (zero,
+    subnormal in f32 / bf16 / f16, normal, overflow to inf) through the products and the hardware
+    round-to-nearest-even conversions, against the oracle's float32 products and casts."""
+    from torch_xdna import kernels
+
+    m, n, k = 256, 512, 128
+    a, w = _i8((m, k), 1), _i8((n, k), 2)
+    rng = np.random.default_rng(3)
+    sx = (10.0 ** rng.uniform(-30, 15, m)).astype(np.float32)
+    sw = (10.0 ** rng.uniform(-20, 15, n)).astype(np.float32)
+    sx[:4] = [0.0, 1e-45, np.finfo(np.float32).tiny, 3e38]
+    y = kernels.mm_i8_dequant(a.to(gpu), torch.from_numpy(sx).to(gpu), w.to(gpu), torch.from_numpy(sw).to(gpu),
+                              None, DT[out])
+    with np.errstate(over="ignore", under="ignore"):
+        want = O.to_dtype(O.dequant(c_oracle.gemm_i32(_np(a), _np(w)), sx, sw), out)
+    got = _f32(y)
+    assert np.isinf(want).any() and (want[np.isfinite(want) & (want != 0)] != 0).any()
+    bad = ~((got == want) | (np.isnan(got) & np.isnan(want)))
+    assert not bad.any(), f"{bad.sum()} of {got.size} differ, e.g. {got[bad][:4]} vs {want[bad][:4]}"
+
+
 # ------------------------------------------------------------------------------ conv
 def _conv_case(n, ci, co, h, w, seed):
     x = _rand((n, ci, h, w), torch.float32, seed=seed)
@@ -181,3 +204,39 @@ def test_conv_layouts(gpu):
     q = _i8((2, 5, 11, 21), seed=4)
     back = kernels.nhwc_to_nchw(q.to(gpu))
     assert np.array_equal(_np(back), q.numpy().transpose(0, 3, 1, 2))
+
+
+# ------------------------------------------------------------------------------ HIP graph capture
+def test_graph_replay(gpu):
+    """The launchers captured into one HIP graph (activation quantize, fused GEMM, conv quantize, conv,
+    conv dequantize): three replays, with new inputs copied in and eager work plus synchronization
+    between them, each bit-identical to the eager result on the same inputs."""
+    from torch_xdna import kernels
+
+    x = _rand((300, 1024), torch.bfloat16, seed=51).to(gpu)
+    wq, sw = kernels.quant_rows(_rand((520, 1024), torch.float32, seed=52, scale=0.02).to(gpu))
+    xc = _rand((2, 64, 20, 24), torch.float32, seed=53).to(gpu)
+    cwq, csw = kernels.conv_weight_pack(_rand((64, 64, 3, 3), torch.float32, seed=54, scale=0.05).to(gpu), 64)
+    scale = csw * 2.0 ** 9
+
+    def path():
+        xq, sx = kernels.quant_rows(x)
+        y = kernels.mm_i8_dequant(xq, sx, wq, sw, None, torch.bfloat16)
+        cq, csx = kernels.conv_quant(xc, 64)
+        q = kernels.conv3x3(cq, cwq, 9, True)
+        return y, kernels.conv_dequant(q, True, scale, csx, None, torch.float32)
+
+    path()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = path()
+    for rep in range(3):
+        x.copy_(_rand((300, 1024), torch.bfloat16, seed=60 + rep).to(gpu))
+        xc.copy_(_rand((2, 64, 20, 24), torch.float32, seed=70 + rep).to(gpu))
+        want = path()                       # eager work between the replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for got, ref in zip(outs, want):
+            assert torch.equal(got, ref), f"replay {rep} differs from the eager result"

@@ -53,7 +53,7 @@ struct EpiArgs {
   int shift;            // EPI_REQUANT
   int relu;             // EPI_REQUANT / EPI_CALIB
   int32_t* acc_max;     // EPI_CALIB
-  int vec_ok;           // output rows allow 4-wide vector stores
+  int vec_ok;           // output 16-byte aligned, row stride a multiple of 8 elements
 };
 
 struct ConvGeom {
@@ -73,157 +73,132 @@ __device__ __forceinline__ i32x16 mfma32x32x32(const i32x4& a, const i32x4& b, c
 }
 
 // ------------------------------------------------------------------------------ epilogue
-// Per-column values of four consecutive output columns n .. n+3 (weight scales and bias of the
+// Per-column values of CW consecutive output columns n .. n+CW-1 (weight scales and bias of the
 // dequantize), loaded once per column block and reused for every row.
-template <int EPI>
+template <int EPI, int CW = 4>
 struct EpiCols {
-  float sw[4], b[4];
+  float sw[CW], b[CW];
   __device__ __forceinline__ EpiCols() {}
   __device__ __forceinline__ EpiCols(const EpiArgs& e, int64_t n, int64_t N) {
     if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16) {
-      if (n + 3 < N && (reinterpret_cast<uintptr_t>(e.sw + n) & 15) == 0) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(e.sw + n);
-        sw[0] = v[0], sw[1] = v[1], sw[2] = v[2], sw[3] = v[3];
-      } else {
+      load(e.sw, n, N, sw);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sw[r] = n + r < N ? e.sw[n + r] : 0.0f;
+      for (int r = 0; r < CW; ++r) b[r] = 0.0f;
+      if (e.bias) load(e.bias, n, N, b);
+    }
+  }
+  __device__ __forceinline__ static void load(const float* p, int64_t n, int64_t N, float (&v)[CW]) {
+    if (n + CW - 1 < N && (reinterpret_cast<uintptr_t>(p + n) & 15) == 0) {
+#pragma unroll
+      for (int q = 0; q < CW / 4; ++q) {
+        const f32x4 t = *reinterpret_cast<const f32x4*>(p + n + 4 * q);
+        v[4 * q] = t[0], v[4 * q + 1] = t[1], v[4 * q + 2] = t[2], v[4 * q + 3] = t[3];
       }
+    } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) b[r] = 0.0f;
-      if (e.bias) {
-        if (n + 3 < N && (reinterpret_cast<uintptr_t>(e.bias + n) & 15) == 0) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(e.bias + n);
-          b[0] = v[0], b[1] = v[1], b[2] = v[2], b[3] = v[3];
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) b[r] = n + r < N ? e.bias[n + r] : 0.0f;
-        }
-      }
+      for (int r = 0; r < CW; ++r) v[r] = n + r < N ? p[n + r] : 0.0f;
     }
   }
 };
 
-// One lane's four outputs: row m, columns n .. n+3 (acc[r] is column n + r). FULL: the caller has
-// established that the whole tile is in bounds and vector stores are allowed (no per-element tests).
-template <int EPI, bool FULL = false>
-__device__ __forceinline__ void epilogue4(const EpiArgs& e, int64_t m, int64_t n, int64_t M, int64_t N,
-                                          const i32x4& acc, int& calib, const EpiCols<EPI>& cols, float sxm) {
-  if constexpr (FULL) {
-    if constexpr (EPI == EPI_CALIB) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) calib = max(calib, e.relu ? max(acc[r], 0) : abs(acc[r]));
-    } else if constexpr (EPI == EPI_I32) {
-      *reinterpret_cast<i32x4*>(reinterpret_cast<int32_t*>(e.out) + m * e.ldo + n) = acc;
-    } else if constexpr (EPI == EPI_REQUANT) {
-      const int half = 1 << (e.shift - 1);
-      uint32_t packed = 0;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int q = (acc[r] + half) >> e.shift;    // arithmetic shift: floor, i.e. round half up
-        q = e.relu ? min(max(q, 0), 255) : min(max(q, -128), 127);
-        packed |= ((uint32_t)(q & 0xff)) << (8 * r);
-      }
-      *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(e.out) + m * e.ldo + n) = packed;
-    } else {
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float t = (float)acc[r];
-        t = t * sxm;
-        t = t * cols.sw[r];
-        if (e.bias) t = t + cols.b[r];         // uniform test: the bias pointer is a kernel argument
-        v[r] = t;
-      }
-      const int64_t off = m * e.ldo + n;
-      if constexpr (EPI == EPI_DQ_F32) {
-        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(e.out) + off) = f32x4{v[0], v[1], v[2], v[3]};
-      } else {
-        uint16_t h[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) h[r] = EPI == EPI_DQ_BF16 ? f32_to_bf16_bits(v[r]) : f32_to_f16_bits(v[r]);
-        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(e.out) + off) =
-            make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
-      }
-    }
-    return;
-  }
-  if (m >= M) return;
+// One lane's CW outputs: row m, columns n .. n+CW-1 (acc[r] is column n + r). FULL: the caller has
+// established that the whole tile is in bounds and the output rows take CW-wide vector stores, so
+// there are no per-element tests. e.vec_ok: output rows are 16-byte aligned with a row stride that
+// is a multiple of 8 elements (CW-wide stores at column multiples of CW are aligned).
+template <int EPI, bool FULL, int CW>
+__device__ __forceinline__ void epilogue_w(const EpiArgs& e, int64_t m, int64_t n, int64_t M, int64_t N,
+                                           const int32_t (&acc)[CW], int& calib, const EpiCols<EPI, CW>& cols,
+                                           float sxm) {
+  static_assert(CW == 4 || CW == 8, "4 or 8 columns per lane");
+  if (!FULL && m >= M) return;
+  const bool vec = FULL || (e.vec_ok && n + CW - 1 < N);
   if constexpr (EPI == EPI_CALIB) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if (n + r < N) {
-        int v = acc[r];
-        v = e.relu ? max(v, 0) : abs(v);
-        calib = max(calib, v);
-      }
-    }
+    for (int r = 0; r < CW; ++r)
+      if (FULL || n + r < N) calib = max(calib, e.relu ? max(acc[r], 0) : abs(acc[r]));
   } else if constexpr (EPI == EPI_I32) {
     int32_t* c = reinterpret_cast<int32_t*>(e.out) + m * e.ldo + n;
-    if (e.vec_ok && n + 3 < N) {
-      *reinterpret_cast<i32x4*>(c) = acc;
+    if (vec) {
+#pragma unroll
+      for (int q = 0; q < CW / 4; ++q)
+        *reinterpret_cast<i32x4*>(c + 4 * q) = i32x4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int r = 0; r < CW; ++r)
         if (n + r < N) c[r] = acc[r];
     }
   } else if constexpr (EPI == EPI_REQUANT) {
     const int half = 1 << (e.shift - 1);
-    uint32_t packed = 0;
-    int qv[4];
+    uint32_t packed[CW / 4];
+    int qv[CW];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < CW; ++r) {
       int q = (acc[r] + half) >> e.shift;      // arithmetic shift: floor, i.e. round half up
       q = e.relu ? min(max(q, 0), 255) : min(max(q, -128), 127);
       qv[r] = q;
-      packed |= ((uint32_t)(q & 0xff)) << (8 * r);
+    }
+#pragma unroll
+    for (int g = 0; g < CW / 4; ++g) {
+      packed[g] = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) packed[g] |= ((uint32_t)(qv[4 * g + r] & 0xff)) << (8 * r);
     }
     uint8_t* o = reinterpret_cast<uint8_t*>(e.out) + m * e.ldo + n;
-    if (e.vec_ok && n + 3 < N) {
-      *reinterpret_cast<uint32_t*>(o) = packed;
+    if (vec) {
+      if constexpr (CW == 8) *reinterpret_cast<uint2*>(o) = make_uint2(packed[0], packed[1]);
+      else *reinterpret_cast<uint32_t*>(o) = packed[0];
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int r = 0; r < CW; ++r)
         if (n + r < N) o[r] = (uint8_t)(qv[r] & 0xff);
     }
   } else {  // EPI_DQ_*: ((float)acc * sx[m]) * sw[n] (+ bias[n]), each step rounded once
-    float v[4];
+    float v[CW];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if (n + r < N) {
-        float t = (float)acc[r];
-        t = t * sxm;
-        t = t * cols.sw[r];
-        if (e.bias) t = t + cols.b[r];
-        v[r] = t;
-      } else {
-        v[r] = 0.0f;
-      }
+    for (int r = 0; r < CW; ++r) {
+      float t = (float)acc[r];
+      t = t * sxm;
+      t = t * cols.sw[r];
+      if (e.bias) t = t + cols.b[r];           // uniform test: the bias pointer is a kernel argument
+      v[r] = t;
     }
     const int64_t off = m * e.ldo + n;
     if constexpr (EPI == EPI_DQ_F32) {
       float* y = reinterpret_cast<float*>(e.out) + off;
-      if (e.vec_ok && n + 3 < N) {
-        *reinterpret_cast<f32x4*>(y) = f32x4{v[0], v[1], v[2], v[3]};
+      if (vec) {
+#pragma unroll
+        for (int q = 0; q < CW / 4; ++q)
+          *reinterpret_cast<f32x4*>(y + 4 * q) = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
       } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < CW; ++r)
           if (n + r < N) y[r] = v[r];
       }
     } else {
-      uint16_t h[4];
+      uint32_t h[CW / 2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) h[r] = EPI == EPI_DQ_BF16 ? f32_to_bf16_bits(v[r]) : f32_to_f16_bits(v[r]);
+      for (int q = 0; q < CW / 2; ++q)
+        h[q] = EPI == EPI_DQ_BF16 ? f32x2_to_bf16x2_bits(v[2 * q], v[2 * q + 1])
+                                  : f32x2_to_f16x2_bits(v[2 * q], v[2 * q + 1]);
       uint16_t* y = reinterpret_cast<uint16_t*>(e.out) + off;
-      if (e.vec_ok && n + 3 < N) {
-        *reinterpret_cast<uint2*>(y) = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16),
-                                                  (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+      if (vec) {
+        if constexpr (CW == 8) *reinterpret_cast<uint4*>(y) = make_uint4(h[0], h[1], h[2], h[3]);
+        else *reinterpret_cast<uint2*>(y) = make_uint2(h[0], h[1]);
       } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (n + r < N) y[r] = h[r];
+        for (int r = 0; r < CW; ++r)
+          if (n + r < N) y[r] = (uint16_t)(h[r / 2] >> (16 * (r & 1)));
       }
     }
   }
+}
+
+// Four columns held as one i32x4 (the small-M kernel's accumulator).
+template <int EPI>
+__device__ __forceinline__ void epilogue4(const EpiArgs& e, int64_t m, int64_t n, int64_t M, int64_t N,
+                                          const i32x4& acc, int& calib, const EpiCols<EPI, 4>& cols, float sxm) {
+  const int32_t a[4] = {acc[0], acc[1], acc[2], acc[3]};
+  epilogue_w<EPI, false, 4>(e, m, n, M, N, a, calib, cols, sxm);
 }
 
 template <int EPI>
@@ -238,29 +213,33 @@ __device__ __forceinline__ void calib_flush(const EpiArgs& e, int calib) {
 // XCD-aware order: consecutive workgroup ids go round-robin over the 8 XCDs, so ids are remapped
 // to give each XCD a contiguous run of tiles, and runs are walked GROUP_M tile-rows at a time so
 // that the workgroups sharing an XCD's L2 share A rows and W columns.
-__device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_t tiles_n, int64_t& tm, int64_t& tn) {
-  constexpr int XCDS = 8;
-  constexpr int GROUP_M = 8;
-  const int64_t total = tiles_m * tiles_n;
-  const int64_t q = total / XCDS, r = total % XCDS;
-  const int64_t xcd = pid % XCDS, local = pid / XCDS;
-  const int64_t tile = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + local;
-  const int64_t in_group = (int64_t)GROUP_M * tiles_n;
-  const int64_t g = tile / in_group;
-  const int64_t first_m = g * GROUP_M;
-  const int64_t gsz = min((int64_t)GROUP_M, tiles_m - first_m);
-  const int64_t rem = tile % in_group;
-  tm = first_m + rem % gsz;
-  tn = rem / gsz;
+__device__ __forceinline__ void tile_coords(uint32_t pid, uint32_t tiles_m, uint32_t tiles_n, int64_t& tm,
+                                            int64_t& tn) {
+  // 32-bit arithmetic (the launcher keeps tile counts below 2^31): 64-bit divisions cost thousands
+  // of cycles on the scalar unit
+  constexpr uint32_t XCDS = 8;
+  constexpr uint32_t GROUP_M = 8;
+  const uint32_t total = tiles_m * tiles_n;
+  const uint32_t q = total / XCDS, r = total % XCDS;
+  const uint32_t xcd = pid % XCDS, local = pid / XCDS;
+  const uint32_t tile = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + local;
+  const uint32_t in_group = GROUP_M * tiles_n;
+  const uint32_t g = tile / in_group;
+  const uint32_t first_m = g * GROUP_M;
+  const uint32_t gsz = min(GROUP_M, tiles_m - first_m);
+  const uint32_t rem = tile - g * in_group;
+  const uint32_t rdiv = rem / gsz;
+  tm = first_m + (rem - rdiv * gsz);
+  tn = rdiv;
 }
 
-// LDS rows are 128 bytes (one K slice of a row); chunk c of row r sits at chunk c ^ f(r) with
-// f(r) = (r & 7) ^ ((r >> 3) & 1). A fragment read touches 16 consecutive rows at one logical chunk:
-// rows r..r+7 land in 8 distinct 16-byte bank groups (LDS serving 8 lanes of 16 bytes per pass), and
-// the 8 rows of equal parity among r..r+15 land in 8 distinct groups of a 256-byte line (16 lanes per
-// pass). f depends only on r & 15, so fragments 16 rows apart differ by a constant LDS offset.
-__device__ __forceinline__ int swz_f(int row) { return (row & 7) ^ ((row >> 3) & 1); }
-__device__ __forceinline__ int swz(int row, int chunk) { return (row << 7) + ((chunk ^ swz_f(row)) << 4); }
+// LDS rows are 64 bytes (one 64-deep K slice of a tile row); the 16-byte chunk c (0..3) of row r sits
+// at chunk c ^ f(r) with f(r) = ((r >> 1) ^ (r >> 3)) & 3. A fragment read touches 32 consecutive rows
+// at one logical chunk: each 8 of them (LDS serving 8 lanes of 16 bytes per pass) land in 8 distinct
+// 16-byte bank groups of a 128-byte line, and each 16 in 16 distinct groups of a 256-byte line (16
+// lanes per pass). f depends only on r & 31, so fragments 32 rows apart differ by a constant offset.
+__device__ __forceinline__ int swz_f(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+__device__ __forceinline__ int swz(int row, int chunk) { return (row << 6) + ((chunk ^ swz_f(row)) << 4); }
 
 // Raw buffer loads: a 16-byte load at a byte offset >= the resource's size returns zeros, which is how
 // rows past M / N, chunks past K and conv taps outside the image read as zero without a branch.
@@ -275,6 +254,20 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // 16 bytes per lane from global memory straight into LDS: lane l's bytes land at lds + 16 * l.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t off, int8_t* lds, uint32_t soff = 0) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, (int)off, (int)soff, 0, 0);
+}
+
+// s_waitcnt with a compile-time count (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8): wait until at most N vector memory loads of this wave are outstanding (they complete
+// in issue order), optionally also for every LDS access.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
 // Scheduling groups for __builtin_amdgcn_sched_group_barrier.
@@ -295,33 +288,46 @@ struct PinGroups {
 };
 
 
-// Tile engine. Each K slice (128 bytes of K) of the A and W tiles is brought into LDS by the DMA
-// form of the buffer load: one wave instruction fills 8 whole 128-byte LDS rows, and each lane
-// fetches the global chunk that belongs at its LDS position under the swizzle. Two LDS stages; per
-// slice kt (two 64-deep MFMA steps):
-//   step 0: MFMAs of the step-0 fragments, with the step-1 fragment reads in between;
-//   step 1, first half of the MFMAs; wait for this wave's DMA of slice kt+1; barrier;
-//   step 1, second half, with the DMA of slice kt+2 (into the stage just freed) and the reads of
-//   slice kt+1's step-0 fragments in between.
-// One barrier per slice; the DMA has a whole slice of MFMAs to land.
-template <int BM, int BN, int WM, int WN, int CONVM, int EPI, bool KFULL>
+// Emits NA groups "1 instruction of kind XA + its share of the first half of NM MFMAs", then NB
+// groups "1 instruction of kind XB + its share of the second half".
+template <int XA, int NA, int XB, int NB, int NM>
+struct PinTwo {
+  __device__ __forceinline__ static void emit() {
+    PinGroups<XA, NA, NM / 2, 0>::emit();
+    PinGroups<XB, NB, NM - NM / 2, 0>::emit();
+  }
+};
+
+// Tile engine. Each 64-deep K slice of the A and W tiles is brought into LDS by the DMA form of the
+// buffer load: one wave instruction fills 16 whole 64-byte LDS rows, and each lane fetches the global
+// chunk that belongs at its LDS position under the swizzle. S LDS stages hold slices kt .. kt+S-1, so
+// the loads of a slice have S - 1 slices of MFMAs to land. Per slice kt (two 32-deep MFMA steps):
+//   step 0: MFMAs of the step-0 fragments, with the reads of the step-1 fragments in between;
+//   wait for this wave's DMA of slice kt+1; barrier (every wave has read all of slice kt, and slice
+//   kt+1 is complete);
+//   step 1: MFMAs of the step-1 fragments, with the DMA of slice kt+S into slice kt's stage and the
+//   reads of slice kt+1's step-0 fragments in between.
+// Slices past the end of K are loaded as out-of-range (zero) reads, which keeps the wait counts and
+// the loop uniform.
+template <int BM, int BN, int WM, int WN, int S, int CONVM, int EPI, bool KFULL>
 __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __restrict__ a, int64_t lda,
                                                                const int8_t* __restrict__ w, int64_t ldw, int64_t M,
                                                                int64_t N, int64_t K, ConvGeom cg, EpiArgs e) {
-  constexpr bool CONV = CONVM != 0;      // CONVM: 0 GEMM, 1 conv with C_pad % 128 == 0, 2 any C_pad
-  constexpr int BK = 128;
+  constexpr bool CONV = CONVM != 0;      // CONVM: 0 GEMM, 1 conv with C_pad % 64 == 0, 2 any C_pad
+  constexpr int BK = 64;
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;  // 32 x 32 MFMA tiles per wave
-  constexpr int IA = BM / 8 / NW;        // DMA instructions per wave per slice (8 rows each)
-  constexpr int IW = BN / 8 / NW;
+  constexpr int IA = BM / 16 / NW;       // DMA instructions per wave per slice (16 rows each)
+  constexpr int IW = BN / 16 / NW;
   static_assert(FM >= 1 && FN >= 1, "wave tile below 32 x 32");
-  static_assert(IA >= 1 && IW >= 1 && BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile / wave mismatch");
+  static_assert(IA >= 1 && IW >= 1 && BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "tile / wave mismatch");
   constexpr int STAGE = (BM + BN) * BK;
+  static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS stages");
+  constexpr int NDMA = IA + IW;
+  static_assert((S - 1) * NDMA <= 63, "vmcnt range");
 
-  __shared__ __attribute__((aligned(1024))) int8_t lds[2 * STAGE];
-  int8_t* const lds0 = lds;
-  int8_t* const lds1 = lds + STAGE;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -330,7 +336,7 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
 
   const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int64_t tm, tn;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_coords(blockIdx.x, (uint32_t)tiles_m, (uint32_t)tiles_n, tm, tn);
   const int64_t m0 = tm * BM, n0 = tn * BN;
 
   // The epilogue's per-row and per-column scales do not depend on K: load them now, so they arrive
@@ -344,17 +350,21 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
       sx_pre[rr] = m < M ? e.sx[m] : 0.0f;
     }
   }
-  EpiCols<EPI> cols_pre[FN];
+  // Epilogue read-back width: CB 32-column blocks side by side, CW columns per lane (8 lanes per row)
+  constexpr int CB = FN >= 2 ? 2 : 1;
+  constexpr int CW = 4 * CB;
+  EpiCols<EPI, CW> cols_pre[FN / CB];
 #pragma unroll
-  for (int j = 0; j < FN; ++j) cols_pre[j] = EpiCols<EPI>(e, n0 + wn * TN + j * 32 + (lane & 7) * 4, N);
+  for (int jp = 0; jp < FN / CB; ++jp)
+    cols_pre[jp] = EpiCols<EPI, CW>(e, n0 + wn * TN + jp * 32 * CB + (lane & 7) * CW, N);
 
   const __amdgpu_buffer_rsrc_t ra_rsrc = make_rsrc(a, (uint32_t)(CONV ? (M * cg.c_pad) : (M * lda)));
   const __amdgpu_buffer_rsrc_t rw_rsrc = make_rsrc(w, (uint32_t)(N * ldw));
 
-  // This lane's rows: DMA instruction j of this wave covers tile rows r0 = (wave * I + j) * 8 .. +8,
-  // and lane l fills LDS chunk l % 8 of row r0 + l / 8, i.e. logical chunk (l % 8) ^ f(row).
-  const int lrow = lane >> 3;
-  const int pch = lane & 7;
+  // This lane's rows: DMA instruction j of this wave covers tile rows r0 = (wave * I + j) * 16 .. +16,
+  // and lane l fills LDS chunk l % 4 of row r0 + l / 4, i.e. logical chunk (l % 4) ^ f(row).
+  const int lrow = lane >> 2;
+  const int pch = lane & 3;
   uint32_t oa[IA], ow[IW];
   int ca[IA], cw[IW];                    // logical chunk per slot
   int py[IA], px[IA];
@@ -362,52 +372,63 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
   (void)px;
 #pragma unroll
   for (int j = 0; j < IA; ++j) {
-    const int row = (wave * IA + j) * 8 + lrow;
+    const int row = (wave * IA + j) * 16 + lrow;
     ca[j] = pch ^ swz_f(row);
     const int64_t m = m0 + row;
     if constexpr (CONV) {
-      const int64_t hw = cg.h * cg.w;
-      const int64_t mm = m < M ? m : 0;
-      const int64_t img = mm / hw, p = mm - img * hw;
-      const int yy = (int)(p / cg.w);
-      py[j] = m < M ? yy : -1000000;       // an invalid row fails every bounds test
-      px[j] = (int)(p - (int64_t)yy * cg.w);
-      oa[j] = (uint32_t)(mm * cg.c_pad);
+      // 32-bit: M * c_pad stays below 2^30 (the launcher splits larger batches)
+      const uint32_t hw = (uint32_t)(cg.h * cg.w);
+      const uint32_t mm = m < M ? (uint32_t)m : 0u;
+      const uint32_t p = mm % hw;
+      const uint32_t yy = p / (uint32_t)cg.w;
+      py[j] = m < M ? (int)yy : -1000000;  // an invalid row fails every bounds test
+      px[j] = (int)(p - yy * (uint32_t)cg.w);
+      oa[j] = mm * (uint32_t)cg.c_pad;
     } else {
       oa[j] = m < M ? (uint32_t)(m * lda + ca[j] * 16) : OOB;
     }
   }
 #pragma unroll
   for (int j = 0; j < IW; ++j) {
-    const int row = (wave * IW + j) * 8 + lrow;
+    const int row = (wave * IW + j) * 16 + lrow;
     cw[j] = pch ^ swz_f(row);
     const int64_t n = n0 + row;
     ow[j] = n < N ? (uint32_t)(n * ldw + cw[j] * 16) : OOB;
   }
 
+  const int64_t nk = (K + BK - 1) / BK;
+  // CONVM 1: the slices are issued in order, so the tap and channel offset of the next slice to load
+  // are kept as running counters instead of being divided out of k.
+  int dtap = 0, dc0 = 0;
+  (void)dtap;
+  (void)dc0;
   auto dma_slice = [&](int64_t kt, int8_t* stage) {
     const int64_t k0 = kt * BK;
+    const bool live = kt < nk;           // uniform; dead slices read zeros without memory traffic
     int8_t* sa = stage;
     int8_t* sw = stage + BM * BK;
     if constexpr (CONVM == 1) {
-      // C_pad % 128 == 0: the whole slice is one tap
-      const int64_t tap = k0 / cg.c_pad;
-      const int64_t c0 = k0 - tap * cg.c_pad;
-      const int dy = (int)(tap / 3) - 1, dx = (int)(tap % 3) - 1;
-      const int64_t delta = ((int64_t)dy * cg.w + dx) * cg.c_pad + c0;
-      const bool kin = k0 < K;
+      // C_pad % 64 == 0: the whole slice is one tap
+      const int dy = (dtap >= 3) + (dtap >= 6) - 1;
+      const int dx = dtap - 3 * (dy + 1) - 1;
+      const int64_t delta = ((int64_t)dy * cg.w + dx) * cg.c_pad + dc0;
 #pragma unroll
       for (int j = 0; j < IA; ++j) {
         const int sy = py[j] + dy, sx = px[j] + dx;
-        const bool ok = kin && sy >= 0 && sy < cg.h && sx >= 0 && sx < cg.w;
+        const bool ok = live && sy >= 0 && sy < cg.h && sx >= 0 && sx < cg.w;
         dma16(ra_rsrc, ok ? (uint32_t)(oa[j] + delta + ca[j] * 16) : OOB, sa + ((wave * IA + j) << 10));
+      }
+      dc0 += BK;
+      if (dc0 == cg.c_pad) {
+        dc0 = 0;
+        ++dtap;
       }
     } else if constexpr (CONVM == 2) {
 #pragma unroll
       for (int j = 0; j < IA; ++j) {
-        const int64_t kb = k0 + ca[j] * 16;
-        const int64_t tap = kb / cg.c_pad;
-        const int64_t c = kb - tap * cg.c_pad;
+        const uint32_t kb = (uint32_t)k0 + ca[j] * 16;
+        const uint32_t tap = kb / (uint32_t)cg.c_pad;
+        const uint32_t c = kb - tap * (uint32_t)cg.c_pad;
         const int dy = (int)(tap / 3) - 1, dx = (int)(tap % 3) - 1;
         const int sy = py[j] + dy, sx = px[j] + dx;
         const bool ok = kb < K && sy >= 0 && sy < cg.h && sx >= 0 && sx < cg.w;
@@ -415,9 +436,10 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
         dma16(ra_rsrc, ok ? (uint32_t)(oa[j] + delta) : OOB, sa + ((wave * IA + j) << 10));
       }
     } else {
-      if (KFULL) {                         // K % 128 == 0: the per-slot offsets are constant
+      if (KFULL) {                         // K % 64 == 0: the per-slot offsets are constant
 #pragma unroll
-        for (int j = 0; j < IA; ++j) dma16(ra_rsrc, oa[j], sa + ((wave * IA + j) << 10), (uint32_t)k0);
+        for (int j = 0; j < IA; ++j)
+          dma16(ra_rsrc, live ? oa[j] : OOB, sa + ((wave * IA + j) << 10), live ? (uint32_t)k0 : 0u);
       } else {
 #pragma unroll
         for (int j = 0; j < IA; ++j) {
@@ -428,7 +450,8 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
     }
     if (KFULL) {
 #pragma unroll
-      for (int j = 0; j < IW; ++j) dma16(rw_rsrc, ow[j], sw + ((wave * IW + j) << 10), (uint32_t)k0);
+      for (int j = 0; j < IW; ++j)
+        dma16(rw_rsrc, live ? ow[j] : OOB, sw + ((wave * IW + j) << 10), live ? (uint32_t)k0 : 0u);
     } else {
 #pragma unroll
       for (int j = 0; j < IW; ++j) {
@@ -438,9 +461,9 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
     }
   };
 
-  // Fragments of one 32-deep k sub-step ks (4 per slice): lane l holds 16 bytes of row
+  // Fragments of one 32-deep k step ks (2 per slice): lane l holds 16 bytes of row
   // (frag base + l % 32) at logical chunk 2 * ks + l / 32. Two register sets alternate: while the
-  // MFMAs of sub-step ks run, the fragments of sub-step ks + 1 are read into the other set.
+  // MFMAs of one step run, the fragments of the next are read into the other set.
   const int frow = lane & 31;
   const int fk = lane >> 5;
   i32x4 fa[2][FM], fw[2][FN];
@@ -465,95 +488,83 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
       for (int i = 0; i < FM; ++i) acc[j][i] = mfma32x32x32(fw[set][j], fa[set][i], acc[j][i]);
   };
 
-  const int64_t nk = (K + BK - 1) / BK;
-  dma_slice(0, lds0);
-  if (nk > 1) dma_slice(1, lds1);
-  if (nk > 1) {
-    // slice 0 landed (the DMA completes in order): wait for all but slice 1's loads
-    if constexpr (IA + IW == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if constexpr (IA + IW == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else if constexpr (IA + IW == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  } else {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  }
-  __syncthreads();
-  read_frags(lds0, 0, 0);
+  // prologue: slices 0 .. S-1 into stages 0 .. S-1, then wait for slice 0
+#pragma unroll
+  for (int s = 0; s < S; ++s) dma_slice(s, lds + s * STAGE);
+  // bare barrier: __syncthreads() would also fence, i.e. wait for every load of the prologue
+  wait_vmcnt<(S - 1) * NDMA>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  read_frags(lds, 0, 0);
 
-  // Pinned order inside each sub-step: the next sub-step's fragment reads are spread between this
-  // sub-step's MFMAs (one read per NMF / NRD MFMAs), so no MFMA waits on LDS.
-  constexpr int NMF = FM * FN, NRD = FM + FN, NDMA = IA + IW;
-  auto pin_reads = [&]() { PinGroups<SG_DS_READ, NRD, NMF, 0>::emit(); };
-  auto substep = [&](const int8_t* stage, int ks_next, int set_next, int set) {
-    read_frags(stage, ks_next, set_next);
-    mfmas(set);
-    pin_reads();
+  constexpr int NMF = FM * FN, NRD = FM + FN;
+  int cur_s = 0;
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    int8_t* cur = lds + cur_s * STAGE;
+    const int nxt_s = cur_s + 1 == S ? 0 : cur_s + 1;
+    const int8_t* nxt = lds + nxt_s * STAGE;
+    // step 0
+    read_frags(cur, 1, 1);
+    mfmas(0);
+    PinGroups<SG_DS_READ, NRD, NMF, 0>::emit();
     __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // One slice = sub-steps 0..3 (sets 0,1,0,1). The barrier sits between sub-steps 2 and 3: by then
-  // every wave has read all of this slice's fragments, so its stage can take the DMA of slice kt+2,
-  // and slice kt+1 (waited for just before) is complete for the reads during sub-step 3. The loop
-  // body is branch-free; the last two slices (no DMA left to issue) are peeled.
-  auto slice = [&](int64_t kt, auto dma_tag, auto next_tag) {
-    constexpr bool DMA = decltype(dma_tag)::value, NEXT = decltype(next_tag)::value;
-    int8_t* cur = lds + (kt & 1) * STAGE;
-    const int8_t* nxt = lds + ((kt + 1) & 1) * STAGE;
-    substep(cur, 1, 1, 0);
-    substep(cur, 2, 0, 1);
-    substep(cur, 3, 1, 0);
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    // slice kt+1 landed (this wave's part), this wave's reads of slice kt done; then all waves
+    wait_vmcnt_lgkm0<(S - 2) * NDMA>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (DMA) dma_slice(kt + 2, cur);
-    if constexpr (NEXT) read_frags(nxt, 0, 0);
+    // step 1
+    dma_slice(kt + S, cur);
+    read_frags(nxt, 0, 0);
     mfmas(1);
-    // DMA issue spread over the last sub-step's MFMAs
-    if constexpr (DMA) PinGroups<SG_VMEM_READ, NDMA, NMF, 0>::emit();
+    PinTwo<SG_VMEM_READ, NDMA, SG_DS_READ, NRD, NMF>::emit();
     __builtin_amdgcn_sched_barrier(0);
-  };
-  using T_ = std::integral_constant<bool, true>;
-  using F_ = std::integral_constant<bool, false>;
-  int64_t kt = 0;
-  for (; kt + 2 < nk; ++kt) slice(kt, T_{}, T_{});
-  if (kt + 1 < nk) slice(kt++, F_{}, T_{});
-  slice(kt, F_{}, F_{});
+    cur_s = nxt_s;
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Epilogue through LDS. The 32x32 accumulator of tile (j, i) holds, in lane l, output row
   // m = i * 32 + l % 32 of the wave tile and, in element 4 * g + r, column 8 * g + 4 * (l / 32) + r of
-  // column block j. Each accumulator block goes to a per-wave LDS staging area as 32 int32 rows of
-  // 32 columns (pitch 144 bytes: conflict-free for these 16-byte writes and reads), and is read back
-  // four consecutive columns per lane, eight lanes per row, for the epilogue: every store instruction
-  // writes whole contiguous row pieces instead of 4 columns of 64 different rows.
-  constexpr int PITCH = 144;
-  static_assert(NW * 32 * PITCH <= 2 * STAGE, "staging does not fit in LDS");
+  // column block j. CB accumulator blocks of one row block go to a per-wave LDS staging area as 32
+  // int32 rows of 32 * CB columns (pitch 32 * CB * 4 + 16 bytes: conflict-free 16-byte writes and
+  // reads), read back CW consecutive columns per lane, eight lanes per row: each store instruction
+  // writes whole 8-row pieces of 32 * CB contiguous columns (full 128-byte lines for bf16 with CB 2).
+  constexpr int PITCH = 32 * CB * 4 + 16;
+  static_assert(NW * 32 * PITCH <= S * STAGE, "staging does not fit in LDS");
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();                       // every wave is done with the K-loop's LDS stages
-  int8_t* stg = lds0 + wave * 32 * PITCH;
+  int8_t* stg = lds + wave * 32 * PITCH;
   int calib = 0;
-  // uniform: the whole tile is inside M x N and the output rows take 4-wide vector stores
+  // uniform: the whole tile is inside M x N and the output rows take CW-wide vector stores
   const bool full = m0 + BM <= M && n0 + BN <= N && (EPI == EPI_CALIB || e.vec_ok);
-  const int rsub = lane >> 3;            // read-back: row rr * 8 + rsub, columns 4 * (lane & 7) .. +3
+  const int rsub = lane >> 3;            // read-back: row rr * 8 + rsub, columns CW * (lane & 7) ..
   const int cq = lane & 7;
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int64_t n = n0 + wn * TN + j * 32 + cq * 4;
+  for (int jp = 0; jp < FN / CB; ++jp) {
+    const int64_t n = n0 + wn * TN + jp * 32 * CB + cq * CW;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const i32x4 v = {acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]};
-        *reinterpret_cast<i32x4*>(stg + (lane & 31) * PITCH + (8 * g + 4 * (lane >> 5)) * 4) = v;
+      for (int jj = 0; jj < CB; ++jj) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const i32x16& c = acc[jp * CB + jj][i];
+          *reinterpret_cast<i32x4*>(stg + (lane & 31) * PITCH + (jj * 32 + 8 * g + 4 * (lane >> 5)) * 4) =
+              i32x4{c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
+        }
       }
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int row = rr * 8 + rsub;
-        const i32x4 v = *reinterpret_cast<const i32x4*>(stg + row * PITCH + cq * 16);
+        int32_t v[CW];
+#pragma unroll
+        for (int q = 0; q < CB; ++q) {
+          const i32x4 t = *reinterpret_cast<const i32x4*>(stg + row * PITCH + cq * CW * 4 + q * 16);
+          v[4 * q] = t[0], v[4 * q + 1] = t[1], v[4 * q + 2] = t[2], v[4 * q + 3] = t[3];
+        }
         const int64_t m = m0 + wm * TM + i * 32 + row;
         const float sxm = sx_pre[DQ ? i * 4 + rr : 0];
-        if (full) epilogue4<EPI, true>(e, m, n, M, N, v, calib, cols_pre[j], sxm);
-        else epilogue4<EPI, false>(e, m, n, M, N, v, calib, cols_pre[j], sxm);
+        if (full) epilogue_w<EPI, true, CW>(e, m, n, M, N, v, calib, cols_pre[jp], sxm);
+        else epilogue_w<EPI, false, CW>(e, m, n, M, N, v, calib, cols_pre[jp], sxm);
       }
     }
   }
@@ -561,10 +572,18 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
 }
 
 // ------------------------------------------------------------------------------ small M
-// Workgroup = WAVES waves owning output columns [n0, n0+16) and rows [m0, m0+16); wave v sums
-// k in its own K range. Per step a lane loads 32 bytes of weight row n0 + (lane & 15) at
-// k = kb + (lane >> 4) * 32 and the matching 32 bytes of activation row m0 + (lane & 15), and
-// issues two MFMAs (bytes 0..15 and 16..31).
+// Weight streaming for M <= 64 (decode): a workgroup of WAVES waves owns output columns
+// [n0, n0 + 16) and rows [m0, m0 + 16); wave v sums k over its own range [kbeg, kend) (a multiple of
+// 64 bytes). Per 64-deep step a lane loads 16 bytes of weight row n0 + (lane & 15) and of activation
+// row m0 + (lane & 15) at k + 16 * (lane >> 4), and one 16x16x64 MFMA consumes them. Steps go in
+// batches of U with two register sets, so the loads of the next batch are in flight while the MFMAs of
+// this one run. Rows past M / N and bytes past the wave's range read as zeros (out-of-range buffer
+// loads). The waves' partial sums meet in LDS; wave 0 runs the epilogue.
+__device__ __forceinline__ i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+}
+
 template <int WAVES, int U, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __restrict__ a, int64_t lda,
                                                               const int8_t* __restrict__ w, int64_t ldw, int64_t M,
@@ -576,31 +595,42 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
   const int64_t m0 = (int64_t)blockIdx.y * 16;
   const int64_t n = n0 + (lane & 15);
   const int64_t m = m0 + (lane & 15);
-  const bool nv = n < N, mv = m < M;
-  const int8_t* pw = w + (nv ? n : 0) * ldw + (lane >> 4) * 32;
-  const int8_t* pa = a + (mv ? m : 0) * lda + (lane >> 4) * 32;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(N * ldw));
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a, (uint32_t)(M * lda));
+  const uint32_t wrow = n < N ? (uint32_t)(n * ldw) : OOB;
+  const uint32_t arow = m < M ? (uint32_t)(m * lda) : OOB;
   const int64_t kbeg = (int64_t)wave * kper;
   const int64_t kend = min(K, kbeg + kper);
+  const int cq = (lane >> 4) * 16;
 
-  i32x4 acc = {0, 0, 0, 0};
-  for (int64_t kb = kbeg; kb < kend; kb += 128 * U) {
-    i32x4 wv[U][2], av[U][2];
+  auto load = [&](int64_t kb, i32x4 (&wv)[U], i32x4 (&av)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t k = kb + u * 128 + (lane >> 4) * 32;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const bool kin = k + h * 16 < kend;
-        wv[u][h] = (nv && kin) ? *reinterpret_cast<const i32x4*>(pw + kb + u * 128 + h * 16) : i32x4{0, 0, 0, 0};
-        av[u][h] = (mv && kin) ? *reinterpret_cast<const i32x4*>(pa + kb + u * 128 + h * 16) : i32x4{0, 0, 0, 0};
-      }
+      const int64_t k = kb + u * 64 + cq;
+      const bool kin = k < kend;
+      wv[u] = buf_load16(rw, kin && wrow != OOB ? wrow + (uint32_t)k : OOB);
+      av[u] = buf_load16(ra, kin && arow != OOB ? arow + (uint32_t)k : OOB);
     }
+  };
+  // two accumulators alternate so consecutive MFMAs do not wait on each other
+  i32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+  auto mfmas = [&](const i32x4 (&wv)[U], const i32x4 (&av)[U]) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      acc = mfma16x16x64(wv[u][0], av[u][0], acc);
-      acc = mfma16x16x64(wv[u][1], av[u][1], acc);
+    for (int u = 0; u < U; u += 2) {
+      acc0 = mfma16x16x64(wv[u], av[u], acc0);
+      if (u + 1 < U) acc1 = mfma16x16x64(wv[u + 1], av[u + 1], acc1);
     }
+  };
+  i32x4 w0[U], a0[U], w1[U], a1[U];
+  load(kbeg, w0, a0);
+  for (int64_t kb = kbeg; kb < kend; kb += 2 * U * 64) {
+    load(kb + U * 64, w1, a1);
+    mfmas(w0, a0);
+    if (kb + U * 64 >= kend) break;
+    load(kb + 2 * U * 64, w0, a0);
+    mfmas(w1, a1);
   }
+  i32x4 acc = acc0 + acc1;
   red[wave][lane] = acc;
   __syncthreads();
   if (wave != 0) return;
@@ -670,23 +700,25 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
     return XDNA_EINVAL;
   }
   dim3 grid((unsigned)tiles, 1, 1);
-  const bool kfull = K % 128 == 0;
-#define XDNA_TILE_W(BM_, BN_, WM_, WN_)                                                                       \
-  if (kfull) mm_tile_kernel<BM_, BN_, WM_, WN_, CONVM, EPI, true><<<grid, WM_ * WN_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e); \
-  else mm_tile_kernel<BM_, BN_, WM_, WN_, CONVM, EPI, false><<<grid, WM_ * WN_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
-#define XDNA_TILE(BM_, BN_) XDNA_TILE_W(BM_, BN_, 2, 2)
+  const bool kfull = K % 64 == 0;
+  // LDS stages per tile shape: 4 for the large tiles (128 KB at 256 x 256; 64 KB at 128 x 128, two
+  // workgroups per CU), 8 for 64 x 64 tiles, whose problems are too small to hide HBM latency otherwise
+#define XDNA_TILE_W(BM_, BN_, WM_, WN_, S_)                                                                   \
+  if (kfull) mm_tile_kernel<BM_, BN_, WM_, WN_, S_, CONVM, EPI, true><<<grid, WM_ * WN_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e); \
+  else mm_tile_kernel<BM_, BN_, WM_, WN_, S_, CONVM, EPI, false><<<grid, WM_ * WN_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
+#define XDNA_TILE(BM_, BN_, S_) XDNA_TILE_W(BM_, BN_, 2, 2, S_)
   if (t.bm == 256 && t.bn == 256 && t.waves == 8) {
-    XDNA_TILE_W(256, 256, 2, 4)
+    XDNA_TILE_W(256, 256, 2, 4, 4)
   } else if (t.bm == 256 && t.bn == 256) {
-    XDNA_TILE(256, 256)
+    XDNA_TILE(256, 256, 4)
   } else if (t.bm == 256) {
-    XDNA_TILE(256, 128)
+    XDNA_TILE(256, 128, 4)
   } else if (t.bn == 256) {
-    XDNA_TILE(128, 256)
+    XDNA_TILE(128, 256, 4)
   } else if (t.bm == 128) {
-    XDNA_TILE(128, 128)
+    XDNA_TILE(128, 128, 4)
   } else {
-    XDNA_TILE(64, 64)
+    XDNA_TILE(64, 64, 8)
   }
 #undef XDNA_TILE
 #undef XDNA_TILE_W
@@ -712,13 +744,21 @@ template <int EPI>
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                 const EpiArgs& e, hipStream_t st) {
   if (M <= 64) {
-    // weight streaming: waves split K into 128-byte multiples
-    constexpr int WAVES = 8, U = 2;
-    const int64_t slices = (K + 127) / 128;
-    const int64_t kper = ((slices + WAVES - 1) / WAVES) * 128;
-    dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16), 1);
-    mm_small_kernel<WAVES, U, EPI><<<grid, WAVES * 64, 0, st>>>(a, lda, w, ldw, M, N, K, kper, e);
-    return launch_status("mm_small");
+    // weight streaming: the waves of a workgroup split K into multiples of 64 bytes; the weight is
+    // processed in row chunks that one buffer resource can address
+    constexpr int WAVES = 8, U = 8;
+    const int64_t steps = (K + 63) / 64;
+    const int64_t kper = ((steps + WAVES - 1) / WAVES) * 64;
+    const int64_t nrows = std::max<int64_t>(16, (MAX_BUF / ldw) / 16 * 16);
+    for (int64_t n0 = 0; n0 < N; n0 += nrows) {
+      const int64_t nc = std::min(nrows, N - n0);
+      dim3 grid((unsigned)((nc + 15) / 16), (unsigned)((M + 15) / 16), 1);
+      mm_small_kernel<WAVES, U, EPI><<<grid, WAVES * 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper,
+                                                                 shift_epi(e, out_bytes<EPI>(), 0, n0));
+      const int rc = launch_status("mm_small");
+      if (rc) return rc;
+    }
+    return XDNA_OK;
   }
   const int64_t mrows = std::max<int64_t>(256, (MAX_BUF / lda) / 256 * 256);
   const int64_t nrows = std::max<int64_t>(256, (MAX_BUF / ldw) / 256 * 256);
@@ -748,7 +788,7 @@ int launch_conv(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad
     const int64_t bc = std::min(imgs, nb - b0);
     const EpiArgs eb = shift_epi(e, 1, b0 * h * w, 0);
     const int8_t* xb = x + b0 * per_img;
-    int rc = (c_pad % 128 == 0) ? launch_tiles<1, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, st)
+    int rc = (c_pad % 64 == 0) ? launch_tiles<1, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, st)
                                 : launch_tiles<2, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, st);
     if (rc) return rc;
   }
@@ -773,7 +813,7 @@ int xdna_gemm_i8_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
   EpiArgs e{};
   e.out = c;
   e.ldo = ldc;
-  e.vec_ok = (ldc % 4 == 0) && aligned(c, 16);
+  e.vec_ok = (ldc % 8 == 0) && aligned(c, 16);
   return launch_gemm<EPI_I32>(a, lda, w, ldw, m, n, k, e, as_stream(stream));
 }
 
@@ -792,8 +832,7 @@ int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const in
   e.sx = sx;
   e.sw = sw;
   e.bias = bias;
-  const int esz = y_dtype == XDNA_F32 ? 4 : 2;
-  e.vec_ok = (ldy % 4 == 0) && aligned(y, 4 * esz);
+  e.vec_ok = (ldy % 8 == 0) && aligned(y, 16);
   hipStream_t st = as_stream(stream);
   if (y_dtype == XDNA_F32) return launch_gemm<EPI_DQ_F32>(a, lda, w, ldw, m, n, k, e, st);
   if (y_dtype == XDNA_BF16) return launch_gemm<EPI_DQ_BF16>(a, lda, w, ldw, m, n, k, e, st);
@@ -819,7 +858,7 @@ int xdna_conv3x3_i8(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c
   e.out = y;
   e.ldo = co;
   e.shift = shift;
-  e.vec_ok = (co % 4 == 0) && aligned(y, 4);
+  e.vec_ok = (co % 8 == 0) && aligned(y, 16);
   return launch_conv<EPI_REQUANT>(x, nb, h, w, c_pad, wq, co, e, st);
 }
 

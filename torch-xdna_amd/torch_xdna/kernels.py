@@ -12,6 +12,7 @@ A non-zero status from the library raises RuntimeError with the library's messag
 CPU fallback in this module: if the library is missing, the launchers raise.
 """
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -123,7 +124,21 @@ def _ptr(t):
 
 
 def _stream(dev):
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    """torch's current stream on dev, as the raw HIP stream handle the library launches on."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(idx))
+
+
+_NOCTX = contextlib.nullcontext()
+
+
+def _on(dev):
+    """Device context for a launch on dev: none when dev is already the current device (the common
+    case, and switching costs microseconds per launch)."""
+    idx = dev.index
+    if idx is None or idx == torch.cuda.current_device():
+        return _NOCTX
+    return torch.cuda.device(idx)
 
 
 def _need_gpu(*ts):
@@ -187,7 +202,7 @@ def quant_rows(x2d, k_pad=None, out=None):
         if xq.shape != (R, k_pad) or xq.stride(1) != 1 or sx.shape != (R,) or not sx.is_contiguous():
             raise ValueError("quant_rows: bad out tensors")
     if R:
-        with torch.cuda.device(dev):
+        with _on(dev):
             _check(lib().xdna_quant_rows(_ptr(x2d), _DTYPE_CODE[x2d.dtype], R, K, x2d.stride(0), _ptr(xq),
                                          xq.stride(0), k_pad, _ptr(sx), _stream(dev)), "quant_rows")
     return xq, sx
@@ -203,7 +218,7 @@ def pad_k(xq, k_pad):
         xq = xq.contiguous()
     out = torch.empty((R, k_pad), dtype=torch.int8, device=dev)
     if R:
-        with torch.cuda.device(dev):
+        with _on(dev):
             _check(lib().xdna_pad_rows_i8(_ptr(xq), R, K, xq.stride(0), _ptr(out), k_pad, k_pad, _stream(dev)),
                    "pad_rows_i8")
     return out
@@ -219,7 +234,7 @@ def mm_i8(a, w, out=None):
         raise ValueError(f"mm_i8: K mismatch {a.shape} vs {w.shape}")
     c = torch.empty((M, N), dtype=torch.int32, device=dev) if out is None else out
     if M and N:
-        with torch.cuda.device(dev):
+        with _on(dev):
             _check(lib().xdna_gemm_i8_i32(_ptr(a), a.stride(0), _ptr(w), w.stride(0), _ptr(c), c.stride(0), M, N, K,
                                           _stream(dev)), "gemm_i8_i32")
     return c
@@ -234,7 +249,7 @@ def mm_i8_dequant(a, sx, w, sw, bias, out_dtype):
         raise ValueError(f"mm_i8_dequant: K mismatch {a.shape} vs {w.shape}")
     y = torch.empty((M, N), dtype=out_dtype, device=dev)
     if M and N:
-        with torch.cuda.device(dev):
+        with _on(dev):
             _check(lib().xdna_gemm_i8_dequant(_ptr(a), a.stride(0), _ptr(sx), _ptr(w), w.stride(0), _ptr(sw),
                                               _ptr(bias), _ptr(y), _DTYPE_CODE[out_dtype], y.stride(0), M, N, K,
                                               _stream(dev)), "gemm_i8_dequant")
@@ -250,7 +265,7 @@ def conv_quant(x, c_pad):
     sx = torch.empty((n,), dtype=torch.float32, device=dev)
     ws = torch.empty((n,), dtype=torch.float32, device=dev)
     if n:
-        with torch.cuda.device(dev):
+        with _on(dev):
             _check(lib().xdna_conv_quant_nhwc(_ptr(x), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(xq), c_pad, _ptr(sx),
                                               _ptr(ws), _stream(dev)), "conv_quant_nhwc")
     return xq, sx
@@ -265,7 +280,7 @@ def conv_weight_pack(weight, ci_pad):
     co, ci = wt.shape[:2]
     wq = torch.empty((co, 9, ci_pad), dtype=torch.int8, device=dev)
     sw = torch.empty((co,), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _on(dev):
         _check(lib().xdna_conv_weight_pack(_ptr(wt), _DTYPE_CODE[wt.dtype], co, ci, _ptr(wq), ci_pad, _ptr(sw),
                                            _stream(dev)), "conv_weight_pack")
     return wq, sw
@@ -279,7 +294,7 @@ def conv3x3(xq, wq, shift, relu):
     co = wq.shape[0]
     y = torch.empty((n, h, w, co), dtype=torch.uint8 if relu else torch.int8, device=dev)
     if n:
-        with torch.cuda.device(dev):
+        with _on(dev):
             _check(lib().xdna_conv3x3_i8(_ptr(xq), n, h, w, c_pad, _ptr(wq), co, int(shift), int(bool(relu)),
                                          _ptr(y), None, _stream(dev)), "conv3x3_i8")
     return y
@@ -291,7 +306,7 @@ def conv3x3_calibrate(xq, wq, relu):
     n, h, w, c_pad = xq.shape
     co = wq.shape[0]
     top = torch.empty((1,), dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _on(dev):
         _check(lib().xdna_conv3x3_i8(_ptr(xq), n, h, w, c_pad, _ptr(wq), co, 1, int(bool(relu)), None, _ptr(top),
                                      _stream(dev)), "conv3x3_i8 (calibrate)")
     return int(top.item())
@@ -303,7 +318,7 @@ def conv_dequant(q, relu, scale, sx, bias, out_dtype):
     n, h, w, co = q.shape
     y = torch.empty((n, co, h, w), dtype=out_dtype, device=dev)
     if n:
-        with torch.cuda.device(dev):
+        with _on(dev):
             _check(lib().xdna_conv_dequant(_ptr(q), int(bool(relu)), n, h, w, co, _ptr(scale), _ptr(sx), _ptr(bias),
                                            _ptr(y), _DTYPE_CODE[out_dtype], _stream(dev)), "conv_dequant")
     return y
@@ -316,7 +331,7 @@ def nchw_to_nhwc(xq, c_pad):
     n, c, h, w = xq.shape
     out = torch.empty((n, h, w, c_pad), dtype=torch.int8, device=dev)
     if n:
-        with torch.cuda.device(dev):
+        with _on(dev):
             _check(lib().xdna_nchw_to_nhwc_i8(_ptr(xq), n, c, h, w, _ptr(out), c_pad, _stream(dev)), "nchw_to_nhwc")
     return out
 
@@ -328,6 +343,6 @@ def nhwc_to_nchw(q):
     n, h, w, c = q.shape
     out = torch.empty((n, c, h, w), dtype=q.dtype, device=dev)
     if n:
-        with torch.cuda.device(dev):
+        with _on(dev):
             _check(lib().xdna_nhwc_to_nchw_i8(_ptr(q), n, c, h, w, _ptr(out), _stream(dev)), "nhwc_to_nchw")
     return out
