@@ -7,13 +7,13 @@
 // columns n of one row m. Tiles: 256x256 with 8 waves (two per SIMD), 256x128 / 128x256 /
 // 128x128 with 4 waves, 64x64 with 4 waves; the host picks one per shape.
 //
-// K is staged through LDS in 128-byte slices, two stages deep, by the LDS-DMA form of the raw
-// buffer load: each lane's 16 bytes land at M0 + 16 * lane, so no VGPRs carry the tile. The DMA
-// of slice kt + 2 is issued after the one barrier per slice and overlaps the MFMAs of kt + 1.
-// LDS rows are 128 bytes; the 16-byte chunk c of row r sits at chunk c ^ f(r) with
-// f(r) = (r & 7) ^ ((r >> 3) & 1), which keeps the 8- and 16-lane phases of a fragment read on
-// distinct bank groups and is periodic in 16 rows, so fragment offsets are immediates.
-// Out-of-range rows, K chunks and conv halo pixels are out-of-range buffer loads, which read 0.
+// K is staged through S LDS stages of 64-byte slices by the LDS-DMA form of the raw buffer load:
+// each lane's 16 bytes land at M0 + 16 * lane, so no VGPRs carry the tile, and S - 1 slices are in
+// flight while one is consumed. LDS rows are 64 bytes; the 16-byte chunk c of row r sits at chunk
+// c ^ f(r) with f(r) = ((r >> 1) ^ (r >> 3)) & 3, which keeps the 8- and 16-lane phases of a
+// fragment read on distinct bank groups and depends only on r & 31, so fragment offsets are
+// immediates. Out-of-range rows, K chunks and conv halo pixels are out-of-range buffer loads, which
+// read 0.
 //
 // Integer sums are exact, so the order in which K is split between lanes, MFMAs or waves does not
 // change the result: the only requirement is that the A and W fragments of one MFMA pair the same
