@@ -114,6 +114,6 @@ def install(monkeypatch):
     monkeypatch.setitem(kernels._state, "ok", True)       # mark_broken() can still retire it
     monkeypatch.setitem(kernels._state, "error", None)
     monkeypatch.setattr(kernels, "gpu_device", lambda t: torch.device("cpu"))
-    monkeypatch.setattr(kernels, "gemm_variant", lambda dev, M, N: "fake")
+    monkeypatch.setattr(kernels, "gemm_variant", lambda dev, M, N, K: "fake")
     for name in LAUNCHERS:
         monkeypatch.setattr(kernels, name, getattr(me, name))

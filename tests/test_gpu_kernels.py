@@ -43,7 +43,7 @@ def _i8(shape, seed, lo=-127, hi=128):
 # ------------------------------------------------------------------------------ quantize
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,k", [(1, 16), (5, 200), (7, 300), (64, 1024), (33, 4096), (3, 14336), (2, 40000),
-                                    (9, 1)])
+                                    (9, 1), (2000, 8192), (1500, 14336)])
 def test_quant_rows(gpu, dtype, rows, k):
     x = _rand((rows, k), DT[dtype], seed=rows * 1000 + k, outliers=1e-3)
     from torch_xdna import kernels
@@ -161,8 +161,8 @@ def _conv_case(n, ci, co, h, w, seed):
 
 @pytest.mark.parametrize("n,ci,co,h,w", [(2, 3, 48, 13, 37), (1, 64, 128, 16, 64), (2, 16, 20, 5, 7),
                                          (1, 256, 256, 8, 64), (3, 40, 64, 9, 9),
-                                         (1, 32, 256, 64, 256),      # 128x128 tiles
-                                         (1, 16, 256, 256, 256)])    # 256x256 tiles
+                                         (1, 32, 256, 64, 256),      # larger tiles (every tile shape:
+                                         (1, 16, 256, 256, 256)])    # test_tiles_forced)
 @pytest.mark.parametrize("relu", [False, True])
 def test_conv3x3(gpu, n, ci, co, h, w, relu):
     from torch_xdna import kernels
@@ -240,3 +240,32 @@ def test_graph_replay(gpu):
         torch.cuda.synchronize()
         for got, ref in zip(outs, want):
             assert torch.equal(got, ref), f"replay {rep} differs from the eager result"
+
+
+# ------------------------------------------------------------------------------ every tile shape
+@pytest.mark.parametrize("tile", ["256x256w8", "256x256", "256x128", "128x256", "128x128", "64x64"])
+def test_tiles_forced(gpu, tile, monkeypatch):
+    """Each tile configuration of the engine, forced through XDNA_GEMM_TILE (read per call): int32
+    and fused bf16 GEMMs with partial tiles and K both a multiple of 64 and not, and the conv with
+    both A loaders (C_pad % 64 == 0 and not), against the oracle."""
+    from torch_xdna import kernels
+
+    monkeypatch.setenv("XDNA_GEMM_TILE", tile)
+    for m, n, k in [(700, 1000, 4160), (333, 520, 208)]:
+        a, w = _i8((m, k), seed=m + k), _i8((n, k), seed=n + k)
+        acc = c_oracle.gemm_i32(a.numpy(), w.numpy())
+        assert np.array_equal(_np(kernels.mm_i8(a.to(gpu), w.to(gpu))), acc), (m, n, k)
+        sx = torch.rand(m) + 0.01
+        sw = torch.rand(n) + 0.01
+        y = kernels.mm_i8_dequant(a.to(gpu), sx.to(gpu), w.to(gpu), sw.to(gpu), None, torch.bfloat16)
+        assert np.array_equal(_f32(y), O.to_bf16(O.dequant(acc, sx.numpy(), sw.numpy()))), (m, n, k)
+    for n, ci, co, h, w_ in [(2, 64, 96, 16, 20), (1, 48, 40, 13, 37)]:
+        xq = _i8((n, ci, h, w_), seed=ci + h)
+        wq = _i8((co, ci, 3, 3), seed=co + w_)
+        c_pad = -(-ci // 16) * 16
+        packed = torch.zeros(co, 9, c_pad, dtype=torch.int8)
+        packed[:, :, :ci] = wq.permute(0, 2, 3, 1).reshape(co, 9, ci)
+        x_nhwc = kernels.nchw_to_nhwc(xq.to(gpu), c_pad)
+        acc = c_oracle.conv3x3_acc(xq.numpy(), wq.numpy())
+        q = kernels.conv3x3(x_nhwc, packed.to(gpu), 9, False)
+        assert np.array_equal(_np(q).transpose(0, 3, 1, 2), O.requant(acc, 9, False)), (n, ci, co, h, w_)

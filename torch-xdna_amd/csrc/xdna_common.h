@@ -24,6 +24,8 @@ void set_error(const std::string& msg);
 
 // Status of the launches just made on this thread (hipGetLastError), as an ABI status.
 int launch_status(const char* where);
+// Compute units of the current device (cached per device).
+int device_cus();
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

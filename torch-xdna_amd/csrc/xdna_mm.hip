@@ -28,8 +28,8 @@
 // shift / round-half-up / saturate (xdna::conv3x3), and the calibration max (first conv call).
 //
 // Small M (decode, M <= 64) uses a separate weight-streaming kernel: each workgroup owns 16 output
-// columns, its waves split K, each lane streams 32 contiguous weight bytes per step (so every
-// weight row is read as whole 128-byte lines), and the partial sums meet in LDS.
+// columns, its 4 / 8 / 16 waves split K, each wave keeps a batch of 16-byte weight loads in flight
+// while it runs the MFMAs of the previous batch, and the partial sums meet in LDS.
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -650,26 +650,16 @@ struct TileCfg {
   int bm, bn, waves;
 };
 
-int g_num_cus = 0;
 
-int num_cus() {
-  if (g_num_cus == 0) {
-    int dev = 0;
-    hipDeviceProp_t prop;
-    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
-      g_num_cus = prop.multiProcessorCount;
-    else
-      g_num_cus = 256;
-  }
-  return g_num_cus;
-}
-
-// Tile choice, from a sweep of every tile shape over the BASELINE shapes on MI355X: 256 x 256 tiles
-// with 8 waves (two per SIMD, one workgroup per CU) win from about 1.75 rounds of such tiles; 128 x 128
-// tiles (two workgroups per CU) win whenever they fill the CUs once; 64 x 64 tiles win for smaller
-// problems and for N <= 64.
-TileCfg pick_tile(int64_t M, int64_t N) {
-  // XDNA_GEMM_TILE=<bm>x<bn> forces a tile shape (tile sweeps); ignored unless it names a built one
+// Tile choice, from a back-to-back timed sweep of every tile shape over the BASELINE GEMM and conv
+// shapes on MI355X (t128 / t256: tiles of that size the problem needs):
+//   * 256 x 256 with 8 waves (one workgroup per CU) from 1.5 rounds of such tiles;
+//   * otherwise, once 128 x 128 tiles fill three quarters of the CUs: 128 x 256 (four waves) for deep K
+//     (>= 4096) when there are at least half a round of 256-wide tiles, else 128 x 128 (three
+//     workgroups per CU);
+//   * 64 x 64 for smaller problems and N <= 64.
+TileCfg pick_tile(int64_t M, int64_t N, int64_t K) {
+  // XDNA_GEMM_TILE=<bm>x<bn>[w8] forces a tile shape (tile sweeps); ignored unless it names a built one
   if (const char* env = std::getenv("XDNA_GEMM_TILE")) {
     int bm = 0, bn = 0, waves = 4;
     const int got = std::sscanf(env, "%dx%dw%d", &bm, &bn, &waves);
@@ -678,12 +668,12 @@ TileCfg pick_tile(int64_t M, int64_t N) {
                                      (bm == 64 && bn == 64)))))
       return {bm, bn, waves};
   }
-  const int64_t cus = num_cus();
+  const int64_t cus = device_cus();
   if (M <= 64 || N <= 64) return {64, 64, 4};
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-  if (4 * t256 >= 7 * cus) return {256, 256, 8};
-  if (t128 >= cus) return {128, 128, 4};
+  if (2 * t256 >= 3 * cus) return {256, 256, 8};
+  if (4 * t128 >= 3 * cus) return (K >= 4096 && 2 * t256 >= cus) ? TileCfg{128, 256, 4} : TileCfg{128, 128, 4};
   return {64, 64, 4};
 }
 
@@ -693,7 +683,7 @@ constexpr int64_t MAX_BUF = 0x40000000;   // 1 GB per resource
 template <int CONVM, int EPI>
 int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                  ConvGeom cg, const EpiArgs& e, hipStream_t st) {
-  const TileCfg t = pick_tile(M, N);
+  const TileCfg t = pick_tile(M, N, K);
   const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   if (tiles >= (1ll << 31)) {
     set_error("launch_mm: too many tiles");
@@ -701,14 +691,14 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
   }
   dim3 grid((unsigned)tiles, 1, 1);
   const bool kfull = K % 64 == 0;
-  // LDS stages per tile shape: 4 for the large tiles (128 KB at 256 x 256; 64 KB at 128 x 128, two
-  // workgroups per CU), 8 for 64 x 64 tiles, whose problems are too small to hide HBM latency otherwise
+  // LDS stages per tile shape, from a measured sweep of 3 / 4 / 5 (and 4 / 8 / 12 for 64 x 64): 3 for
+  // the large tiles (96 KB at 256 x 256; 48 KB at 128 x 128, three workgroups per CU), 4 for 64 x 64
 #define XDNA_TILE_W(BM_, BN_, WM_, WN_, S_)                                                                   \
   if (kfull) mm_tile_kernel<BM_, BN_, WM_, WN_, S_, CONVM, EPI, true><<<grid, WM_ * WN_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e); \
   else mm_tile_kernel<BM_, BN_, WM_, WN_, S_, CONVM, EPI, false><<<grid, WM_ * WN_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
 #define XDNA_TILE(BM_, BN_, S_) XDNA_TILE_W(BM_, BN_, 2, 2, S_)
   if (t.bm == 256 && t.bn == 256 && t.waves == 8) {
-    XDNA_TILE_W(256, 256, 2, 4, 4)
+    XDNA_TILE_W(256, 256, 2, 4, 3)
   } else if (t.bm == 256 && t.bn == 256) {
     XDNA_TILE(256, 256, 4)
   } else if (t.bm == 256) {
@@ -716,9 +706,9 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
   } else if (t.bn == 256) {
     XDNA_TILE(128, 256, 4)
   } else if (t.bm == 128) {
-    XDNA_TILE(128, 128, 4)
+    XDNA_TILE(128, 128, 3)
   } else {
-    XDNA_TILE(64, 64, 8)
+    XDNA_TILE(64, 64, 4)
   }
 #undef XDNA_TILE
 #undef XDNA_TILE_W
@@ -745,16 +735,23 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
                 const EpiArgs& e, hipStream_t st) {
   if (M <= 64) {
     // weight streaming: the waves of a workgroup split K into multiples of 64 bytes; the weight is
-    // processed in row chunks that one buffer resource can address
-    constexpr int WAVES = 8, U = 8;
+    // processed in row chunks that one buffer resource can address. Waves per workgroup: the largest
+    // of 4 / 8 / 16 that keeps all workgroups resident at once (about 16 waves per CU at this
+    // kernel's register use), so the whole weight streams in one round with every wave's loads in flight.
+    constexpr int U = 8;
     const int64_t steps = (K + 63) / 64;
-    const int64_t kper = ((steps + WAVES - 1) / WAVES) * 64;
+    const int64_t strips = ((N + 15) / 16) * ((M + 15) / 16);
+    const int64_t per_strip = (16 * (int64_t)device_cus()) / std::max<int64_t>(strips, 1);
+    const int waves = per_strip >= 16 ? 16 : per_strip >= 8 ? 8 : 4;
+    const int64_t kper = ((steps + waves - 1) / waves) * 64;
     const int64_t nrows = std::max<int64_t>(16, (MAX_BUF / ldw) / 16 * 16);
     for (int64_t n0 = 0; n0 < N; n0 += nrows) {
       const int64_t nc = std::min(nrows, N - n0);
       dim3 grid((unsigned)((nc + 15) / 16), (unsigned)((M + 15) / 16), 1);
-      mm_small_kernel<WAVES, U, EPI><<<grid, WAVES * 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper,
-                                                                 shift_epi(e, out_bytes<EPI>(), 0, n0));
+      const EpiArgs en = shift_epi(e, out_bytes<EPI>(), 0, n0);
+      if (waves == 16) mm_small_kernel<16, U, EPI><<<grid, 16 * 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper, en);
+      else if (waves == 8) mm_small_kernel<8, U, EPI><<<grid, 8 * 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper, en);
+      else mm_small_kernel<4, U, EPI><<<grid, 4 * 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper, en);
       const int rc = launch_status("mm_small");
       if (rc) return rc;
     }

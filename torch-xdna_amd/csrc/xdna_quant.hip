@@ -11,6 +11,7 @@
 //
 // All floating-point arithmetic here is compiled without contraction (-ffp-contract=off), so
 // every product and sum rounds once as in torch's CPU kernels.
+#include <algorithm>
 #include <mutex>
 #include <string>
 
@@ -23,6 +24,17 @@ thread_local std::string g_last_error;
 }
 
 void set_error(const std::string& msg) { g_last_error = msg; }
+
+int device_cus() {
+  static int cache[64] = {0};              // per device; concurrent first calls store the same value
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    hipDeviceProp_t prop;
+    cache[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 256;
+  }
+  return cache[dev];
+}
 
 int launch_status(const char* where) {
   hipError_t e = hipGetLastError();
@@ -145,6 +157,79 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const void* __restr
   for (int64_t c = k + t; c < k_pad; c += TPR) qr[c] = 0;
 }
 
+// Long rows (more than 512 vectors): persistent blocks of 256 threads walk rows with a grid stride;
+// each thread holds up to MAXV 16-byte vectors of a row, and the loads of the block's next row are
+// issued before this row's reduction and quantize, so HBM sees a continuous stream. The partial
+// maxima go through a double-buffered LDS slot: one barrier per row.
+template <int DT, int MAXV>
+__global__ __launch_bounds__(256) void quant_rows_stream_kernel(const void* __restrict__ x, int64_t rows, int64_t k,
+                                                                int64_t ld_x, int8_t* __restrict__ q, int64_t ld_q,
+                                                                int64_t k_pad, float* __restrict__ s) {
+  using V = Vec16<DT>;
+  constexpr int VEC = V::N;
+  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
+  __shared__ float red[2][4];
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int64_t nvec = k / VEC;
+  const int64_t stride = gridDim.x;
+
+  auto load = [&](int64_t row, V (&v)[MAXV]) {
+    const char* xr = reinterpret_cast<const char*>(x) + (row < rows ? row : 0) * ld_x * ESZ;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int64_t iv = t + (int64_t)j * 256;
+      v[j].raw = (row < rows && iv < nvec) ? *reinterpret_cast<const uint4*>(xr + iv * 16) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto process = [&](int64_t row, const V (&v)[MAXV], int buf) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) amax = fmaxf(amax, fabsf(v[j].get(e)));
+    amax = wave_max(amax);
+    if (lane == 0) red[buf][wave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[buf][0], red[buf][1]), fmaxf(red[buf][2], red[buf][3]));
+    const float sc = scale_from_amax(amax);
+    const float rc = 1.0f / sc;
+    if (t == 0) s[row] = sc;
+    int8_t* qr = q + row * ld_q;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int64_t iv = t + (int64_t)j * 256;
+      if (iv < nvec) {
+        uint32_t w[VEC / 4];
+#pragma unroll
+        for (int g = 0; g < VEC / 4; ++g) {
+          uint32_t packed = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            packed |= ((uint32_t)(uint8_t)(int8_t)quant1(v[j].get(g * 4 + e), sc, rc)) << (8 * e);
+          w[g] = packed;
+        }
+        if constexpr (VEC == 8) *reinterpret_cast<uint2*>(qr + iv * VEC) = make_uint2(w[0], w[1]);
+        else *reinterpret_cast<uint32_t*>(qr + iv * VEC) = w[0];
+      }
+    }
+    for (int64_t c = k + t; c < k_pad; c += 256) qr[c] = 0;
+  };
+
+  V va[MAXV], vb[MAXV];
+  int64_t row = blockIdx.x;
+  load(row, va);
+  while (row < rows) {
+    load(row + stride, vb);
+    process(row, va, 0);
+    row += stride;
+    if (row >= rows) break;
+    load(row + stride, va);
+    process(row, vb, 1);
+    row += stride;
+  }
+}
+
 // Scalar path for any k / stride / alignment: one block per row, the row read twice.
 template <int DT>
 __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(const void* __restrict__ x, int64_t rows, int64_t k,
@@ -164,6 +249,20 @@ __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(const void* __re
   for (int64_t i = k + threadIdx.x; i < k_pad; i += 256) qr[i] = 0;
 }
 
+// Blocks of a persistent streaming kernel: as many as are resident at once (the runtime's occupancy
+// for 256 threads, cached per kernel and device), at most one per row.
+template <typename F>
+unsigned stream_blocks(F kernel, int64_t rows) {
+  static int per_cu[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (per_cu[dev] == 0) {
+    int n = 0;
+    per_cu[dev] = (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) == hipSuccess && n > 0) ? n : 1;
+  }
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(rows, (int64_t)per_cu[dev] * device_cus()));
+}
+
 template <int DT>
 int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8_t* q, int64_t ld_q, int64_t k_pad,
                       float* s, hipStream_t st) {
@@ -176,7 +275,13 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
   const int64_t nvec = k / VEC;
   if (nvec <= 64 * 8) {  // one wavefront per row, four rows per block
     quant_rows_vec_kernel<DT, 64, 8><<<dim3((unsigned)cdiv(rows, 4)), 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
-  } else {               // one block per row
+  } else if (nvec <= 256 * 8) {
+    quant_rows_stream_kernel<DT, 8><<<dim3(stream_blocks(quant_rows_stream_kernel<DT, 8>, rows)), 256, 0, st>>>(
+        x, rows, k, ld_x, q, ld_q, k_pad, s);
+  } else if (nvec <= 256 * 16) {
+    quant_rows_stream_kernel<DT, 16><<<dim3(stream_blocks(quant_rows_stream_kernel<DT, 16>, rows)), 256, 0, st>>>(
+        x, rows, k, ld_x, q, ld_q, k_pad, s);
+  } else {               // one block per row, the row read twice
     quant_rows_vec_kernel<DT, 256, 16><<<dim3((unsigned)rows), 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
   }
   return launch_status("quant_rows");

@@ -165,18 +165,20 @@ def num_cus(dev) -> int:
     return _cus[idx]
 
 
-def gemm_variant(dev, M, N) -> str:
-    """Which GEMM kernel the library runs for M x N (mirrors the library's pick_tile): one NPU-program
-    key of the reference (runtime.py:207) corresponds to one (variant, N, K) here."""
+def gemm_variant(dev, M, N, K) -> str:
+    """Which GEMM kernel the library runs for M x N x K (mirrors the library's pick_tile): one
+    NPU-program key of the reference (runtime.py:207) corresponds to one (variant, N, K) here."""
     if M <= 64:
         return "small"
     cus = num_cus(dev)
     if N <= 64:
         return "t64x64"
-    if 4 * (-(-M // 256) * -(-N // 256)) >= 7 * cus:
+    t256 = -(-M // 256) * -(-N // 256)
+    t128 = -(-M // 128) * -(-N // 128)
+    if 2 * t256 >= 3 * cus:
         return "t256x256w8"
-    if -(-M // 128) * -(-N // 128) >= cus:
-        return "t128x128"
+    if 4 * t128 >= 3 * cus:
+        return "t128x256" if K >= 4096 and 2 * t256 >= cus else "t128x128"
     return "t64x64"
 
 

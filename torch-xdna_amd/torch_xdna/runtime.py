@@ -219,7 +219,7 @@ def _gpu_linear(x2d, qw, bias, dtype):
     b = None if bias is None else bias.to(dev, torch.float32).contiguous()
     y = kernels.mm_i8_dequant(xq, sx, wq, sw, b, dtype)
     stats.launches += 1
-    key = ("dq", kernels.gemm_variant(dev, x2d.shape[0], qw.N), qw.N, qw.K, str(dtype))
+    key = ("dq", kernels.gemm_variant(dev, x2d.shape[0], qw.N, qw.Kp), qw.N, qw.K, str(dtype))
     _check(key, y, lambda: _cpu_linear(x2d, qw, bias, dtype))
     return y
 
@@ -231,7 +231,7 @@ def _gpu_acc(xq, qw):
     a = kernels.pad_k(xq.to(dev), qw.Kp)
     acc = kernels.mm_i8(a, wq)
     stats.launches += 1
-    key = ("i8", kernels.gemm_variant(dev, xq.shape[0], qw.N), qw.N, qw.K)
+    key = ("i8", kernels.gemm_variant(dev, xq.shape[0], qw.N, qw.Kp), qw.N, qw.K)
     _check(key, acc, lambda: _cpu_acc(xq, qw))
     return acc
 
