@@ -107,16 +107,45 @@ __device__ __forceinline__ void store_from_f32<XDNA_F16>(void* base, int64_t i, 
 // product lies within 2^-14 of a half-integer; only then is the IEEE division done.
 __device__ __forceinline__ float round_div(float x, float s, float r) {
   float t = x * r;
-  float f = t - floorf(t);
+  const float f = __builtin_amdgcn_fractf(t);   // t - floor(t) in one instruction (v_fract_f32)
   if (fabsf(f - 0.5f) < 6.103515625e-05f) t = x / s;
   return rintf(t);
 }
 
 // Quantized value of x for a row scale s (with r = 1 / s): clamp(round(x / s), -127, 127).
-__device__ __forceinline__ int quant1(float x, float s, float r) {
-  float q = round_div(x, s, r);
-  q = fminf(fmaxf(q, -127.0f), 127.0f);
-  return (int)q;
+__device__ __forceinline__ float quantf(float x, float s, float r) {
+  return fminf(fmaxf(round_div(x, s, r), -127.0f), 127.0f);
+}
+__device__ __forceinline__ int quant1(float x, float s, float r) { return (int)quantf(x, s, r); }
+
+// N values quantized and packed as N int8 bytes (value e in byte e % 4 of word e / 4), the vector form
+// of quant1. The products with the reciprocal are rounded first; only when some lane of the wave
+// holds a product within 2^-14 of a half-integer (rare) does the wave take the IEEE-division branch,
+// which is wave-uniform so the divisions are not computed speculatively for every element. q + 128
+// is an exact integer in [1, 255], which v_cvt_pk_u8_f32 writes into its byte lane; flipping bit 7
+// of every byte then gives the two's-complement int8.
+template <int N>
+__device__ __forceinline__ void quant_pack(const float (&x)[N], float s, float r, uint32_t (&w)[N / 4]) {
+  float t[N];
+  bool near = false;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    t[i] = x[i] * r;
+    near |= fabsf(__builtin_amdgcn_fractf(t[i]) - 0.5f) < 6.103515625e-05f;
+  }
+  if (__builtin_amdgcn_ballot_w64(near)) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (fabsf(__builtin_amdgcn_fractf(t[i]) - 0.5f) < 6.103515625e-05f) t[i] = x[i] / s;
+  }
+#pragma unroll
+  for (int g = 0; g < N / 4; ++g) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v = __builtin_amdgcn_cvt_pk_u8_f32(fminf(fmaxf(rintf(t[4 * g + e]), -127.0f), 127.0f) + 128.0f, e, v);
+    w[g] = v ^ 0x80808080u;
+  }
 }
 
 // The row scale from the row's max |x|: max(amax, 1e-8f) / 127 with IEEE division.

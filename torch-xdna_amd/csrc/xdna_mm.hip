@@ -28,7 +28,7 @@
 // shift / round-half-up / saturate (xdna::conv3x3), and the calibration max (first conv call).
 //
 // Small M (decode, M <= 64) uses a separate weight-streaming kernel: each workgroup owns 16 output
-// columns, its 4 / 8 / 16 waves split K, each wave keeps a batch of 16-byte weight loads in flight
+// columns, its waves (2, or 4 for K above 8 KB) split K, each wave keeps a batch of 16-byte weight loads in flight
 // while it runs the MFMAs of the previous batch, and the partial sums meet in LDS.
 #include <algorithm>
 #include <cmath>
@@ -735,14 +735,16 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
                 const EpiArgs& e, hipStream_t st) {
   if (M <= 64) {
     // weight streaming: the waves of a workgroup split K into multiples of 64 bytes; the weight is
-    // processed in row chunks that one buffer resource can address. Waves per workgroup: the largest
-    // of 4 / 8 / 16 that keeps all workgroups resident at once (about 16 waves per CU at this
-    // kernel's register use), so the whole weight streams in one round with every wave's loads in flight.
+    // processed in row chunks that one buffer resource can address. Waves per workgroup, from a
+    // measured sweep of 1 / 2 / 4 / 8 / 16 over the decode shapes: long per-wave streams through the
+    // double-buffered loop beat wide workgroups; 2 waves, 4 once K exceeds 8 KB.
     constexpr int U = 8;
     const int64_t steps = (K + 63) / 64;
-    const int64_t strips = ((N + 15) / 16) * ((M + 15) / 16);
-    const int64_t per_strip = (16 * (int64_t)device_cus()) / std::max<int64_t>(strips, 1);
-    const int waves = per_strip >= 16 ? 16 : per_strip >= 8 ? 8 : 4;
+    int waves = steps > 128 ? 4 : 2;
+    if (const char* env = std::getenv("XDNA_SMALL_WAVES")) {   // sweeps: 1, 2, 4, 8 or 16
+      const int v = std::atoi(env);
+      if (v == 1 || v == 2 || v == 4 || v == 8 || v == 16) waves = v;
+    }
     const int64_t kper = ((steps + waves - 1) / waves) * 64;
     const int64_t nrows = std::max<int64_t>(16, (MAX_BUF / ldw) / 16 * 16);
     for (int64_t n0 = 0; n0 < N; n0 += nrows) {
@@ -751,7 +753,9 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
       const EpiArgs en = shift_epi(e, out_bytes<EPI>(), 0, n0);
       if (waves == 16) mm_small_kernel<16, U, EPI><<<grid, 16 * 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper, en);
       else if (waves == 8) mm_small_kernel<8, U, EPI><<<grid, 8 * 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper, en);
-      else mm_small_kernel<4, U, EPI><<<grid, 4 * 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper, en);
+      else if (waves == 4) mm_small_kernel<4, U, EPI><<<grid, 4 * 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper, en);
+      else if (waves == 2) mm_small_kernel<2, U, EPI><<<grid, 2 * 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper, en);
+      else mm_small_kernel<1, U, EPI><<<grid, 64, 0, st>>>(a, lda, w + n0 * ldw, ldw, M, nc, K, kper, en);
       const int rc = launch_status("mm_small");
       if (rc) return rc;
     }

@@ -130,14 +130,11 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const void* __restr
   if (t == 0) s[row] = sc;
 
   auto emit = [&](const V& u, int64_t iv) {
+    float f[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) f[e] = u.get(e);
     uint32_t w[VEC / 4];
-#pragma unroll
-    for (int g = 0; g < VEC / 4; ++g) {
-      uint32_t packed = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) packed |= ((uint32_t)(uint8_t)(int8_t)quant1(u.get(g * 4 + e), sc, rc)) << (8 * e);
-      w[g] = packed;
-    }
+    quant_pack<VEC>(f, sc, rc, w);
     if constexpr (VEC == 8) *reinterpret_cast<uint2*>(qr + iv * VEC) = make_uint2(w[0], w[1]);
     else *reinterpret_cast<uint32_t*>(qr + iv * VEC) = w[0];
   };
@@ -200,15 +197,11 @@ __global__ __launch_bounds__(256) void quant_rows_stream_kernel(const void* __re
     for (int j = 0; j < MAXV; ++j) {
       const int64_t iv = t + (int64_t)j * 256;
       if (iv < nvec) {
+        float f[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) f[e] = v[j].get(e);
         uint32_t w[VEC / 4];
-#pragma unroll
-        for (int g = 0; g < VEC / 4; ++g) {
-          uint32_t packed = 0;
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            packed |= ((uint32_t)(uint8_t)(int8_t)quant1(v[j].get(g * 4 + e), sc, rc)) << (8 * e);
-          w[g] = packed;
-        }
+        quant_pack<VEC>(f, sc, rc, w);
         if constexpr (VEC == 8) *reinterpret_cast<uint2*>(qr + iv * VEC) = make_uint2(w[0], w[1]);
         else *reinterpret_cast<uint32_t*>(qr + iv * VEC) = w[0];
       }
