@@ -15,6 +15,7 @@ configs; seed 0), with inputs and device-resident int8 weights already in HBM:
   c5            W8A8 GEMM, bf16 in/out with bias, K 4096 N 14336 M 8192 (the largest config).
   decode        the C5 decode GEMMs (M 1 and 16), HBM-bound: roofline in GB/s of algorithmic bytes.
   quant         the activation quantize kernel alone, bf16 [8192, 14336].
+  bf16          precision "bf16" on the C2 shapes: the bf16 MFMA GEMM (bf16 in / out, float32 sums).
   copy          calibration of the HBM byte counters (a 1 GiB read + 1 GiB write elementwise kernel).
 
 Weight / activation sets are rotated so a step's working set exceeds the 256 MB MALL. Timing:
@@ -43,6 +44,7 @@ for _p in (ROOT, os.path.join(ROOT, "torch-xdna_amd")):
 from torch_xdna import kernels  # noqa: E402
 
 PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, TOP/s (5.0 POP/s)
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, TFLOP/s
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
 MALL_BYTES = 256 << 20
 
@@ -52,7 +54,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "decode", "quant", "copy"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "decode", "quant", "bf16", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -213,7 +215,7 @@ def main():
            "unit": "TOPS", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic (seed 0, randn)"}
     bench = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
-             "decode": bench_decode, "quant": bench_quant, "copy": bench_copy}[a.workload]
+             "decode": bench_decode, "quant": bench_quant, "bf16": bench_bf16, "copy": bench_copy}[a.workload]
     res.update(bench(a, dev))
     print(json.dumps(res), flush=True)
 
@@ -385,6 +387,61 @@ def bench_c1(a, dev):
 def bench_c5(a, dev):
     return gemm_result(a, dev, [(8192, 14336, 4096)], torch.bfloat16, True,
                        "C5 W8A8 GEMM M=8192 N=14336 K=4096 bf16 + bias", "C5")
+
+
+def bench_bf16(a, dev):
+    """precision "bf16" on the C2 shapes: bf16 x and weights, the bf16 MFMA GEMM with float32
+    accumulation, bf16 out (no quantize); one step = the 12 GEMMs between two events."""
+    shapes = []
+    for M in (128, 512, 1024, 3000):
+        shapes += [(M, 4096, 1024), (M, 6144, 1024), (M, 1024, 3072)]
+    g = gen(0)
+    per_set = sum(2 * (M * K + N * K + M * N) for M, N, K in shapes)
+    nsets = max(1, -(-(MALL_BYTES + (64 << 20)) // per_set))
+    sets = [[(torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev),
+              (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)) for M, N, K in shapes]
+            for _ in range(nsets)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(a.steps)]
+
+    def step(i, t):
+        if t:
+            ev[i][0].record()
+        for x, w in sets[i % nsets]:
+            kernels.mm_bf16(x, w, None, torch.bfloat16)
+        if t:
+            ev[i][1].record()
+
+    for i in range(a.warmup):
+        step(i, None)
+    host = eager_seconds(a, step)
+    sec = gated_timed_steps(a, step, True, host * 1e3)
+    g_sec = sum(e[0].elapsed_time(e[1]) for e in ev) / 1e3
+    flops = sum(2 * M * N * K for M, N, K in shapes)
+    ach = flops * a.steps / g_sec / 1e12
+    out = {"metric": "bf16 GEMM TFLOP/s (precision bf16) on 1 MI355X", "unit": "TFLOP/s", "dtype": "bf16",
+           "value": round(flops / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
+           "host_ms_per_step": round(host * 1e3, 4),
+           "config": {"workload": "precision bf16 on the C2 shapes: 12 bf16 GEMMs per step, bf16 out",
+                      "shapes_mnk": shapes, "rotating_sets": nsets},
+           "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic("bf16"),
+                        "kernel": "mm_tile_kernel (EPI_BF_BF16)",
+                        "avg_launch_us": round(g_sec / (len(shapes) * a.steps) * 1e6, 2)}}
+    if not a.no_cpu_baseline:
+        xs = [(torch.randn(M, K, generator=g), torch.randn(N, K, generator=g) * 0.02) for M, N, K in shapes]
+        ts = []
+        t_end = time.perf_counter() + 15.0
+        while len(ts) < 30 and (time.perf_counter() < t_end or len(ts) < 2):
+            t = time.perf_counter()
+            for x, w in xs:          # the reference's CPU route of precision bf16 (runtime.py:306-313)
+                (x.float() @ w.float().t()).to(torch.bfloat16)
+            ts.append(time.perf_counter() - t)
+        best = min(ts)
+        out["cpu_baseline"] = {"value": round(flops / best / 1e12, 3), "unit": "TFLOP/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"full step, min of {len(ts)} reps ({best * 1e3:.1f} ms): torch CPU "
+                                         "float32 matmul, the reference's CPU route of precision bf16"}
+    return out
 
 
 def bench_decode(a, dev):

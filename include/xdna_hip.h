@@ -82,6 +82,18 @@ int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const in
                          const float* sw, const float* bias, void* y, int y_dtype, int64_t ldy,
                          int64_t m, int64_t n, int64_t k, void* stream);
 
+/* The bf16 GEMM of precision "bf16": y[m, n] = sum_k a[m, k] * w[n, k] with bf16 operands and float32
+ * accumulation (+ bias[n] in float32), converted to y_dtype (XDNA_F32/BF16/F16, round to nearest
+ * even). Replaces kernels.mm_bf16 (torch_xdna/kernels.py:167-169) behind runtime._npu_bf16 /
+ * _gemm_bf16 (torch_xdna/runtime.py:212-237, :299-313) with the bf16 weight copy of
+ * QWeight.npu_bf16 (:80-86). Float sums are not bit-exact across summation orders: the result is
+ * the float32 sum of the exact bf16 products to within K float32 roundings (the reference checks
+ * its NPU to a 5e-2 relative norm, runtime.py:179-182). a: [m, k] bf16, row stride lda; w: [n, k]
+ * bf16, row stride ldw; k % 8 == 0 (zero-pad), lda and ldw multiples of 8, 16-byte aligned; bias
+ * may be NULL. */
+int xdna_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const float* bias, void* y, int y_dtype,
+                   int64_t ldy, int64_t m, int64_t n, int64_t k, void* stream);
+
 /* dst[r, :cols] = src[r, :cols], dst[r, cols:cols_pad] = 0 for int8 rows (aligning an int8
  * activation handed to xdna::linear_i8, torch_xdna/ops.py:49-55, to the 16-byte K rule). */
 int xdna_pad_rows_i8(const int8_t* src, int64_t rows, int64_t cols, int64_t ld_src, int8_t* dst,

@@ -25,6 +25,9 @@ How each function is pinned (tests/test_oracle.py):
 * requant: closed form floor(acc / 2^s + 1/2) with Python integers, including negative ties,
   which separate round-half-up from round-half-away.
 * calibrate: closed-form boundaries (top * 1.25 / 127 at exact powers of two).
+* gemm_bf16: exact rational arithmetic (Python fractions) on tiny inputs; the bound is checked to
+  contain numpy's float32 matmul of the same operands and to be violated by a wrong operand
+  (a transposed or unrounded weight).
 """
 
 import math
@@ -108,6 +111,33 @@ def to_bf16(y):
     nan = np.isnan(y)
     out[nan] = np.nan
     return out
+
+
+def gemm_bf16(x, w, bias=None):
+    """precision "bf16": y = bf16(x) @ bf16(w)^T (+ bias), the math of the reference's bf16 route
+    (runtime.py:218-236: operands rounded to bf16 in the staging copies, float32 accumulation;
+    :299-313 and :340-344 for the bias).
+
+    Float32 accumulation is not associative, so instead of one float32 result this returns
+    (y, bound): y is the sum of the bf16 products in float64 (each product is exact; the float64
+    summation error, at most K 2^-53 sum |x w|, is 2^-29 of the float32 bound below), and
+    bound[m, n] = gamma_K * sum_k |x_mk w_nk| (+ 2^-24 |y| for the bias addition), with
+    gamma_K = K u / (1 - K u), u = 2^-24: the worst-case error of any float32 summation order
+    (Higham, Accuracy and Stability of Numerical Algorithms, 2nd ed., sec. 3.1). A float32 result
+    must satisfy |y32 - y| <= bound; a bf16 / fp16 output may also differ by its final rounding.
+    """
+    xb = to_bf16(np.asarray(x, dtype=F32)).astype(np.float64)
+    wb = to_bf16(np.asarray(w, dtype=F32)).astype(np.float64)
+    K = xb.shape[1]
+    y = xb @ wb.T
+    mag = np.abs(xb) @ np.abs(wb).T
+    u = 2.0 ** -24
+    gamma = K * u / (1 - K * u)
+    bound = gamma * mag
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=F32).astype(np.float64)[None, :]
+        bound = bound + u * (np.abs(y) + bound)
+    return y, bound
 
 
 def to_dtype(y, dtype):

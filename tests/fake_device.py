@@ -47,6 +47,17 @@ def mm_i8_dequant(a, sx, w, sw, bias, out_dtype):
     return _to_torch(O.to_dtype(y, _NP_OF[out_dtype]), out_dtype)
 
 
+def bf16_rows(x2d, k_pad):
+    out = torch.zeros((x2d.shape[0], k_pad), dtype=torch.bfloat16)
+    out[:, :x2d.shape[1]] = x2d
+    return out
+
+
+def mm_bf16(a, w, bias, out_dtype):
+    y, _ = O.gemm_bf16(a.float().numpy(), w.float().numpy(), None if bias is None else bias.float().numpy())
+    return _to_torch(O.to_dtype(y.astype(np.float32), _NP_OF[out_dtype]), out_dtype)
+
+
 def conv_weight_pack(weight, ci_pad):
     wq, sw = O.conv_weight_quant(weight.float().numpy())
     co, ci = wq.shape[:2]
@@ -100,7 +111,7 @@ def nhwc_to_nchw(q):
     return q.permute(0, 3, 1, 2).contiguous()
 
 
-LAUNCHERS = ("quant_rows", "pad_k", "mm_i8", "mm_i8_dequant", "conv_weight_pack", "conv_quant", "conv3x3",
+LAUNCHERS = ("quant_rows", "pad_k", "mm_i8", "mm_i8_dequant", "bf16_rows", "mm_bf16", "conv_weight_pack", "conv_quant", "conv3x3",
              "conv3x3_calibrate", "conv_dequant", "nchw_to_nhwc", "nhwc_to_nchw")
 
 

@@ -207,3 +207,20 @@ def test_ops_direct(gpu):
         layer = next(L for _, L in xconv._layers.values() if L.relu == relu)
         assert q.dtype == (torch.uint8 if relu else torch.int8) and q.shape == (2, 48, 13, 37)
         assert torch.equal(q.cpu(), layer.cpu(xc)) and torch.equal(scale.cpu(), layer.scale(torch.device("cpu")))
+
+
+def test_precision_bf16(gpu):
+    """precision="bf16" (runtime.py:299-313): the bf16 GEMM kernel runs on the GPU (verified on its
+    first launch against the bf16 operands multiplied in float32, the reference's check) and agrees
+    with the float32 CPU route to the reference's 5e-2 norm (here far closer)."""
+    torch.manual_seed(11)
+    net = Net().eval().to(gpu)
+    x = torch.randn(300, 200, device=gpu)
+    with torch.no_grad():
+        ref = net(x)
+    y = run(net, x, policy="gpu", fallback="eager", precision="bf16")
+    s = _stats()
+    assert s["calls"] == {"gpu": 3} and not s["fallbacks"] and s["gpu_launches"] == 3, s
+    y_cpu = run(net, x, policy="cpu", fallback="eager", precision="bf16")
+    assert _stats()["calls"] == {"cpu": 3}
+    assert rel_err(y, y_cpu) < 1e-2 and rel_err(y, ref) < 1e-2

@@ -152,6 +152,37 @@ def test_gemm_dequant_range(gpu, out):
     assert not bad.any(), f"{bad.sum()} of {got.size} differ, e.g. {got[bad][:4]} vs {want[bad][:4]}"
 
 
+# ------------------------------------------------------------------------------ bf16 GEMM (precision "bf16")
+def _bf16_bracket(got, want, bound, out):
+    """got (the output dtype's values, as float32) must be the rounding of some v with
+    |v - want| <= bound; rounding is monotonic, so it lies between the roundings of the two ends
+    (widened by 2^-20 relative for the float64 -> float32 step)."""
+    pad = bound * 1.0001 + np.abs(want) * 2.0 ** -20 + 1e-38
+    lo = O.to_dtype((want - pad).astype(np.float32), out)
+    hi = O.to_dtype((want + pad).astype(np.float32), out)
+    bad = ~((got >= lo) & (got <= hi))
+    assert not bad.any(), f"{bad.sum()} of {got.size} outside the bound, e.g. {got[bad][:3]} vs {want[bad][:3]}"
+
+
+@pytest.mark.parametrize("out", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("m,n,k,bias", [(1, 4096, 1024, True), (16, 1000, 520, False), (64, 300, 200, True),
+                                        (128, 3072, 1024, True), (300, 520, 1032, False), (700, 1000, 4096, True),
+                                        (2048, 1024, 256, False)])
+def test_gemm_bf16(gpu, out, m, n, k, bias):
+    """xdna_gemm_bf16 against the oracle's bf16 GEMM within the float32-accumulation bound, through
+    the small-M kernel (m <= 64) and the tile engine, K a multiple of 64 and not."""
+    from torch_xdna import kernels
+
+    x = _rand((m, k), torch.float32, seed=m + n + k)
+    w = _rand((n, k), torch.float32, seed=m + n + k + 1, scale=0.05)
+    b = _rand((n,), torch.float32, seed=m + n + k + 2, scale=0.1) if bias else None
+    xb = kernels.bf16_rows(x.to(gpu), k)
+    wb = kernels.bf16_rows(w.to(gpu), k)
+    y = kernels.mm_bf16(xb, wb, None if b is None else b.to(gpu), DT[out])
+    want, bound = O.gemm_bf16(x.numpy(), w.numpy(), None if b is None else b.numpy())
+    _bf16_bracket(_f32(y), want, bound, out)
+
+
 # ------------------------------------------------------------------------------ conv
 def _conv_case(n, ci, co, h, w, seed):
     x = _rand((n, ci, h, w), torch.float32, seed=seed)
@@ -259,6 +290,12 @@ def test_tiles_forced(gpu, tile, monkeypatch):
         sw = torch.rand(n) + 0.01
         y = kernels.mm_i8_dequant(a.to(gpu), sx.to(gpu), w.to(gpu), sw.to(gpu), None, torch.bfloat16)
         assert np.array_equal(_f32(y), O.to_bf16(O.dequant(acc, sx.numpy(), sw.numpy()))), (m, n, k)
+    for m, n, k in [(700, 1000, 2080), (333, 520, 104)]:          # the bf16 GEMM (K bytes = 2 k)
+        x = _rand((m, k), torch.float32, seed=m + k)
+        w = _rand((n, k), torch.float32, seed=n + k, scale=0.05)
+        y = kernels.mm_bf16(kernels.bf16_rows(x.to(gpu), k), kernels.bf16_rows(w.to(gpu), k), None, torch.float32)
+        want, bound = O.gemm_bf16(x.numpy(), w.numpy())
+        _bf16_bracket(_f32(y), want, bound, "f32")
     for n, ci, co, h, w_ in [(2, 64, 96, 16, 20), (1, 48, 40, 13, 37)]:
         xq = _i8((n, ci, h, w_), seed=ci + h)
         wq = _i8((co, ci, 3, 3), seed=co + w_)

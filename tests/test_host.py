@@ -180,6 +180,27 @@ def test_silent_wrong_fake(fake):
     assert s["calls"] == {"gpu": 2, "cpu": 1}, s["calls"]
 
 
+def test_precision_bf16_fake(fake):
+    """precision="bf16" routes the linears to the bf16 GEMM launcher, verified on its first launch
+    to the reference's 5e-2 norm against the bf16 operands in float32; a launch that disagrees moves
+    that shape to the float32 CPU route (runtime.py:299-313)."""
+    from torch_xdna import kernels, runtime
+
+    net = Net().eval()
+    x = torch.randn(300, 200)
+    y = run(net, x, policy="gpu", fallback="eager", precision="bf16")
+    s = runtime.stats.as_dict()
+    assert s["calls"] == {"gpu": 3} and not s["fallbacks"], s
+    y_cpu = run(net, x, policy="cpu", fallback="eager", precision="bf16")
+    assert rel_err(y, y_cpu) < 1e-2
+    real = kernels.mm_bf16
+    fake.setattr(kernels, "mm_bf16", lambda a, w, b, dt: real(a, w, b, dt) * (2 if w.shape[0] == 300 else 1))
+    y2 = run(net, x, policy="gpu", fallback="eager", precision="bf16", verify="always")   # shapes verified above
+    s = runtime.stats.as_dict()
+    assert len(s["fallbacks"]) == 1 and "disagrees with the CPU" in s["fallbacks"][0][1], s["fallbacks"]
+    assert s["calls"] == {"gpu": 2, "cpu": 1} and rel_err(y2, y_cpu) < 1e-2, s
+
+
 def test_verify_off_lets_wrong_values_through(fake):
     from torch_xdna import kernels
 

@@ -296,3 +296,38 @@ def test_golden_fixtures():
     for relu in (0, 1):
         assert np.array_equal(O.requant(cacc, int(d["c_shift"][relu]), bool(relu)), d[f"c_q{relu}"])
         assert O.calibrate_shift(cacc[0], bool(relu)) == int(d["c_shift"][relu])
+
+
+# ------------------------------------------------------------------------------ bf16 GEMM (precision "bf16")
+def test_gemm_bf16_exact_rationals_tiny():
+    """y against exact rational sums of the bf16-rounded operands (Python fractions)."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((3, 9)) * [[1e-3], [1.0], [50.0]]).astype(np.float32)
+    w = rng.standard_normal((4, 9)).astype(np.float32)
+    b = rng.standard_normal(4).astype(np.float32)
+    y, bound = O.gemm_bf16(x, w, b)
+    xb, wb = O.to_bf16(x), O.to_bf16(w)
+    for m in range(3):
+        for n in range(4):
+            exact = sum(Fraction(float(xb[m, k])) * Fraction(float(wb[n, k])) for k in range(9)) + Fraction(float(b[n]))
+            mag = sum(abs(Fraction(float(xb[m, k])) * Fraction(float(wb[n, k]))) for k in range(9))
+            assert abs(Fraction(float(y[m, n])) - exact) <= mag * Fraction(9, 2 ** 53) + abs(exact) * Fraction(1, 2 ** 52)
+            assert bound[m, n] > 0
+
+
+def test_gemm_bf16_bound_contains_float32_and_rejects_wrong_operands():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((64, 1000)).astype(np.float32)
+    w = (rng.standard_normal((300, 1000)) * 0.02).astype(np.float32)
+    y, bound = O.gemm_bf16(x, w)
+    y32 = O.to_bf16(x) @ O.to_bf16(w).T                  # a float32 summation of the same products
+    assert (np.abs(y32.astype(np.float64) - y) <= bound).all()
+    wrong = x.astype(np.float64) @ w.astype(np.float64).T  # operands not rounded to bf16
+    assert (np.abs(wrong - y) > bound).mean() > 0.5        # the worst-case bound is loose; half still fail
+    sq = rng.standard_normal((50, 50)).astype(np.float32)
+    ws = rng.standard_normal((50, 50)).astype(np.float32)
+    ys, bs = O.gemm_bf16(sq, ws)
+    yt = O.to_bf16(sq).astype(np.float64) @ O.to_bf16(ws).astype(np.float64)   # x @ w instead of x @ w^T
+    assert (np.abs(yt - ys) > bs).mean() > 0.5

@@ -42,7 +42,13 @@
 namespace xdna {
 
 // EPI_DEQUANT_* carry the output dtype in the kernel's type so each epilogue is straight-line code.
-enum Epi { EPI_I32 = 0, EPI_REQUANT = 2, EPI_CALIB = 3, EPI_DQ_F32 = 4, EPI_DQ_BF16 = 5, EPI_DQ_F16 = 6 };
+// EPI_BF_*: the bf16 GEMM (precision "bf16"): float accumulators, + bias, cast to the output dtype.
+enum Epi {
+  EPI_I32 = 0, EPI_REQUANT = 2, EPI_CALIB = 3, EPI_DQ_F32 = 4, EPI_DQ_BF16 = 5, EPI_DQ_F16 = 6,
+  EPI_BF_F32 = 7, EPI_BF_BF16 = 8, EPI_BF_F16 = 9
+};
+constexpr bool epi_dq(int e) { return e == EPI_DQ_F32 || e == EPI_DQ_BF16 || e == EPI_DQ_F16; }
+constexpr bool epi_bf(int e) { return e == EPI_BF_F32 || e == EPI_BF_BF16 || e == EPI_BF_F16; }
 
 struct EpiArgs {
   void* out;            // int32 C, float y, or int8/uint8 q (NHWC)
@@ -61,6 +67,8 @@ struct ConvGeom {
 };
 
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ i32x4 mfma16x16x64(const i32x4& a, const i32x4& b, const i32x4& c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -72,6 +80,16 @@ __device__ __forceinline__ i32x16 mfma32x32x32(const i32x4& a, const i32x4& b, c
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
+// The bf16 forms take the same 16 bytes per lane (8 bf16 values instead of 16 int8) and the same
+// lane layouts, so the byte-level staging of the int8 engine carries them unchanged: one MFMA covers
+// 16 k-values (32 x 32) or 32 (16 x 16) instead of 32 / 64.
+__device__ __forceinline__ f32x16 mfma32x32x16bf(const i32x4& a, const i32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x32bf(const i32x4& a, const i32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
 // ------------------------------------------------------------------------------ epilogue
 // Per-column values of CW consecutive output columns n .. n+CW-1 (weight scales and bias of the
 // dequantize), loaded once per column block and reused for every row.
@@ -80,8 +98,8 @@ struct EpiCols {
   float sw[CW], b[CW];
   __device__ __forceinline__ EpiCols() {}
   __device__ __forceinline__ EpiCols(const EpiArgs& e, int64_t n, int64_t N) {
-    if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16) {
-      load(e.sw, n, N, sw);
+    if constexpr (epi_dq(EPI)) load(e.sw, n, N, sw);
+    if constexpr (epi_dq(EPI) || epi_bf(EPI)) {
 #pragma unroll
       for (int r = 0; r < CW; ++r) b[r] = 0.0f;
       if (e.bias) load(e.bias, n, N, b);
@@ -152,18 +170,25 @@ __device__ __forceinline__ void epilogue_w(const EpiArgs& e, int64_t m, int64_t 
       for (int r = 0; r < CW; ++r)
         if (n + r < N) o[r] = (uint8_t)(qv[r] & 0xff);
     }
-  } else {  // EPI_DQ_*: ((float)acc * sx[m]) * sw[n] (+ bias[n]), each step rounded once
+  } else {
+    // EPI_DQ_*: ((float)acc * sx[m]) * sw[n] (+ bias[n]), each step rounded once;
+    // EPI_BF_*: the float accumulator (its bits arrive in acc) (+ bias[n])
     float v[CW];
 #pragma unroll
     for (int r = 0; r < CW; ++r) {
-      float t = (float)acc[r];
-      t = t * sxm;
-      t = t * cols.sw[r];
+      float t;
+      if constexpr (epi_bf(EPI)) {
+        t = __builtin_bit_cast(float, acc[r]);
+      } else {
+        t = (float)acc[r];
+        t = t * sxm;
+        t = t * cols.sw[r];
+      }
       if (e.bias) t = t + cols.b[r];           // uniform test: the bias pointer is a kernel argument
       v[r] = t;
     }
     const int64_t off = m * e.ldo + n;
-    if constexpr (EPI == EPI_DQ_F32) {
+    if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_BF_F32) {
       float* y = reinterpret_cast<float*>(e.out) + off;
       if (vec) {
 #pragma unroll
@@ -178,8 +203,8 @@ __device__ __forceinline__ void epilogue_w(const EpiArgs& e, int64_t m, int64_t 
       uint32_t h[CW / 2];
 #pragma unroll
       for (int q = 0; q < CW / 2; ++q)
-        h[q] = EPI == EPI_DQ_BF16 ? f32x2_to_bf16x2_bits(v[2 * q], v[2 * q + 1])
-                                  : f32x2_to_f16x2_bits(v[2 * q], v[2 * q + 1]);
+        h[q] = (EPI == EPI_DQ_BF16 || EPI == EPI_BF_BF16) ? f32x2_to_bf16x2_bits(v[2 * q], v[2 * q + 1])
+                                                          : f32x2_to_f16x2_bits(v[2 * q], v[2 * q + 1]);
       uint16_t* y = reinterpret_cast<uint16_t*>(e.out) + off;
       if (vec) {
         if constexpr (CW == 8) *reinterpret_cast<uint4*>(y) = make_uint4(h[0], h[1], h[2], h[3]);
@@ -476,16 +501,21 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
       fw[set][j] = *reinterpret_cast<const i32x4*>(stage + BM * BK + swz(wn * TN + j * 32 + frow, ks * 2 + fk));
   };
 
-  i32x16 acc[FN][FM];
+  constexpr bool BFE = epi_bf(EPI);       // bf16 operands, float accumulators
+  using AccT = std::conditional_t<BFE, f32x16, i32x16>;
+  AccT acc[FN][FM];
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int i = 0; i < FM; ++i) acc[j][i] = i32x16{};
+    for (int i = 0; i < FM; ++i) acc[j][i] = AccT{};
   auto mfmas = [&](int set) {
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int i = 0; i < FM; ++i) acc[j][i] = mfma32x32x32(fw[set][j], fa[set][i], acc[j][i]);
+      for (int i = 0; i < FM; ++i) {
+        if constexpr (BFE) acc[j][i] = mfma32x32x16bf(fw[set][j], fa[set][i], acc[j][i]);
+        else acc[j][i] = mfma32x32x32(fw[set][j], fa[set][i], acc[j][i]);
+      }
   };
 
   // prologue: slices 0 .. S-1 into stages 0 .. S-1, then wait for slice 0
@@ -547,7 +577,7 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
       for (int jj = 0; jj < CB; ++jj) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const i32x16& c = acc[jp * CB + jj][i];
+          const i32x16 c = __builtin_bit_cast(i32x16, acc[jp * CB + jj][i]);   // float bits for BFE
           *reinterpret_cast<i32x4*>(stg + (lane & 31) * PITCH + (jj * 32 + 8 * g + 4 * (lane >> 5)) * 4) =
               i32x4{c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
         }
@@ -588,7 +618,9 @@ template <int WAVES, int U, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __restrict__ a, int64_t lda,
                                                               const int8_t* __restrict__ w, int64_t ldw, int64_t M,
                                                               int64_t N, int64_t K, int64_t kper, EpiArgs e) {
-  __shared__ i32x4 red[WAVES][64];
+  constexpr bool BFE = epi_bf(EPI);       // bf16 operands, float accumulators
+  using Acc4 = std::conditional_t<BFE, f32x4, i32x4>;
+  __shared__ Acc4 red[WAVES][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
@@ -613,12 +645,16 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
     }
   };
   // two accumulators alternate so consecutive MFMAs do not wait on each other
-  i32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+  Acc4 acc0 = {}, acc1 = {};
+  auto mfma = [&](const i32x4& w_, const i32x4& a_, Acc4& c) {
+    if constexpr (BFE) c = mfma16x16x32bf(w_, a_, c);
+    else c = mfma16x16x64(w_, a_, c);
+  };
   auto mfmas = [&](const i32x4 (&wv)[U], const i32x4 (&av)[U]) {
 #pragma unroll
     for (int u = 0; u < U; u += 2) {
-      acc0 = mfma16x16x64(wv[u], av[u], acc0);
-      if (u + 1 < U) acc1 = mfma16x16x64(wv[u + 1], av[u + 1], acc1);
+      mfma(wv[u], av[u], acc0);
+      if (u + 1 < U) mfma(wv[u + 1], av[u + 1], acc1);
     }
   };
   i32x4 w0[U], a0[U], w1[U], a1[U];
@@ -630,7 +666,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
     load(kb + 2 * U * 64, w0, a0);
     mfmas(w1, a1);
   }
-  i32x4 acc = acc0 + acc1;
+  Acc4 acc = acc0 + acc1;
   red[wave][lane] = acc;
   __syncthreads();
   if (wave != 0) return;
@@ -641,7 +677,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
   const int64_t mrow = m0 + (lane & 15);
   float sxm = 0.0f;
   if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16) sxm = mrow < M ? e.sx[mrow] : 0.0f;
-  epilogue4<EPI>(e, mrow, n0 + 4 * (lane >> 4), M, N, acc, calib, cols, sxm);
+  epilogue4<EPI>(e, mrow, n0 + 4 * (lane >> 4), M, N, __builtin_bit_cast(i32x4, acc), calib, cols, sxm);
   calib_flush<EPI>(e, calib);
 }
 
@@ -838,6 +874,28 @@ int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const in
   if (y_dtype == XDNA_F32) return launch_gemm<EPI_DQ_F32>(a, lda, w, ldw, m, n, k, e, st);
   if (y_dtype == XDNA_BF16) return launch_gemm<EPI_DQ_BF16>(a, lda, w, ldw, m, n, k, e, st);
   return launch_gemm<EPI_DQ_F16>(a, lda, w, ldw, m, n, k, e, st);
+}
+
+int xdna_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const float* bias, void* y, int y_dtype,
+                   int64_t ldy, int64_t m, int64_t n, int64_t k, void* stream) {
+  XDNA_REQUIRE(y_dtype == XDNA_F32 || y_dtype == XDNA_BF16 || y_dtype == XDNA_F16, "y_dtype must be F32/BF16/F16");
+  XDNA_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative size");
+  if (m == 0 || n == 0) return XDNA_OK;
+  XDNA_REQUIRE(k % 8 == 0 && k >= 8, "k must be a positive multiple of 8 (16-byte bf16 rows; pad with zeros)");
+  XDNA_REQUIRE(lda >= k && ldw >= k && lda % 8 == 0 && ldw % 8 == 0 && ldy >= n, "bad leading dimensions");
+  XDNA_REQUIRE(a && w && y && aligned(a, 16) && aligned(w, 16), "operands must be 16-byte aligned device pointers");
+  EpiArgs e{};
+  e.out = y;
+  e.ldo = ldy;
+  e.bias = bias;
+  e.vec_ok = (ldy % 8 == 0) && aligned(y, 16);
+  // the engine stages bytes: a bf16 row of k values is 2 * k bytes
+  const int8_t* ab = static_cast<const int8_t*>(a);
+  const int8_t* wb = static_cast<const int8_t*>(w);
+  hipStream_t st = as_stream(stream);
+  if (y_dtype == XDNA_F32) return launch_gemm<EPI_BF_F32>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, st);
+  if (y_dtype == XDNA_BF16) return launch_gemm<EPI_BF_BF16>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, st);
+  return launch_gemm<EPI_BF_F16>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, st);
 }
 
 int xdna_conv3x3_i8(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad, const int8_t* wq, int64_t co,

@@ -95,6 +95,7 @@ def _declare(L):
         "xdna_quant_rows": ([p, i, i64, i64, i64, p, i64, i64, p, p], i),
         "xdna_gemm_i8_i32": ([p, i64, p, i64, p, i64, i64, i64, i64, p], i),
         "xdna_gemm_i8_dequant": ([p, i64, p, p, i64, p, p, p, i, i64, i64, i64, i64, p], i),
+        "xdna_gemm_bf16": ([p, i64, p, i64, p, p, i, i64, i64, i64, i64, p], i),
         "xdna_pad_rows_i8": ([p, i64, i64, i64, p, i64, i64, p], i),
         "xdna_conv_quant_nhwc": ([p, i, i64, i64, i64, i64, p, i64, p, p, p], i),
         "xdna_conv_weight_pack": ([p, i, i64, i64, p, i64, p, p], i),
@@ -109,7 +110,7 @@ def _declare(L):
 
 
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
-           "xdna_gemm_i8_dequant", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc", "xdna_conv_weight_pack",
+           "xdna_gemm_i8_dequant", "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc", "xdna_conv_weight_pack",
            "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_nchw_to_nhwc_i8", "xdna_nhwc_to_nchw_i8")
 
 
@@ -255,6 +256,37 @@ def mm_i8_dequant(a, sx, w, sw, bias, out_dtype):
             _check(lib().xdna_gemm_i8_dequant(_ptr(a), a.stride(0), _ptr(sx), _ptr(w), w.stride(0), _ptr(sw),
                                               _ptr(bias), _ptr(y), _DTYPE_CODE[out_dtype], y.stride(0), M, N, K,
                                               _stream(dev)), "gemm_i8_dequant")
+    return y
+
+
+def bf16_rows(x2d, k_pad):
+    """x2d as bf16 [R, k_pad] rows the bf16 GEMM reads (round to nearest even; zero columns past K,
+    16-byte aligned rows): the tensor itself when it already qualifies, else one copy."""
+    _need_gpu(x2d)
+    R, K = x2d.shape
+    if (x2d.dtype == torch.bfloat16 and K == k_pad and x2d.stride(1) == 1 and x2d.stride(0) % 8 == 0
+            and x2d.data_ptr() % 16 == 0):
+        return x2d
+    out = torch.zeros((R, k_pad), dtype=torch.bfloat16, device=x2d.device) if K != k_pad else \
+        torch.empty((R, k_pad), dtype=torch.bfloat16, device=x2d.device)
+    out[:, :K].copy_(x2d)
+    return out
+
+
+def mm_bf16(a, w, bias, out_dtype):
+    """y [M, N] = (a @ w^T (+ bias)) as out_dtype, bf16 operands a [M, Kp] and w [N, Kp] (Kp % 8 == 0,
+    16-byte aligned rows), float32 accumulation and bias, in one kernel (precision "bf16")."""
+    dev = _need_gpu(a, w, bias)
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K or a.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError(f"mm_bf16: bf16 [M, K] x [N, K] operands, got {a.dtype} {tuple(a.shape)}, "
+                         f"{w.dtype} {tuple(w.shape)}")
+    y = torch.empty((M, N), dtype=out_dtype, device=dev)
+    if M and N:
+        with _on(dev):
+            _check(lib().xdna_gemm_bf16(_ptr(a), a.stride(0), _ptr(w), w.stride(0), _ptr(bias), _ptr(y),
+                                        _DTYPE_CODE[out_dtype], y.stride(0), M, N, K, _stream(dev)), "gemm_bf16")
     return y
 
 
