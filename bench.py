@@ -54,7 +54,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "decode", "quant", "bf16", "copy"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "decode", "quant", "bf16", "vgg16",
+                                                          "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -215,7 +216,8 @@ def main():
            "unit": "TOPS", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic (seed 0, randn)"}
     bench = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
-             "decode": bench_decode, "quant": bench_quant, "bf16": bench_bf16, "copy": bench_copy}[a.workload]
+             "decode": bench_decode, "quant": bench_quant, "bf16": bench_bf16, "vgg16": bench_vgg16,
+             "copy": bench_copy}[a.workload]
     res.update(bench(a, dev))
     print(json.dumps(res), flush=True)
 
@@ -551,7 +553,8 @@ def bench_c3(a, dev):
         y = kernels.conv_dequant(kernels.conv3x3(xq, wq, shift, True), True, scale, sx, None, torch.float32)
     scales = [sw * 2.0 ** s for (wq, sw, _), s in zip(layers, shifts)]
 
-    def step(i, ct=None):
+    def step_parts(i, ct=None):
+        """Each layer as conv3x3_int8 alone: quantize, conv, dequantize to float32."""
         y = x
         for (wq, sw, _), s, sc in zip(layers, shifts, scales):
             xq, sx = kernels.conv_quant(y, c_pad)
@@ -559,14 +562,29 @@ def bench_c3(a, dev):
             y = kernels.conv_dequant(q, True, sc, sx, None, torch.float32)
         return y
 
+    def step(i, ct=None):
+        """The chained layers (xdna::conv3x3_chain): the activation stays NHWC int8 between convs."""
+        xq, sx = kernels.conv_quant(x, c_pad)
+        for j, ((wq, sw, _), s, sc) in enumerate(zip(layers, shifts, scales)):
+            q = ct(kernels.conv3x3, xq, wq, s, True) if ct else kernels.conv3x3(xq, wq, s, True)
+            if j < L - 1:
+                xq, sx = kernels.conv_requant_next(q, True, False, sc, sx, None, torch.float32, c_pad)
+            else:
+                y = kernels.conv_dequant(q, True, sc, sx, None, torch.float32)
+        return y
+
+    if not torch.equal(step(0), step_parts(0)):
+        raise SystemExit("chained and per-layer C3 outputs differ")
+    sec_parts, _ = timed_steps(a, step_parts, None)
     ct = Timer()
     sec, host = timed_steps(a, step, ct)
     ms = ct.ms()
     ops = 2 * n * h * w * c * c * 9
     ach = ops / (sum(ms) / len(ms) / 1e3) / 1e12
     out = {"value": round(ops * L / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
-           "host_ms_per_step": round(host * 1e3, 4),
-           "config": {"workload": "C3 4x (conv3x3 256->256 + ReLU) on 1x256x64x64, quantize/conv/dequantize per layer"},
+           "host_ms_per_step": round(host * 1e3, 4), "unchained_ms_per_step": round(sec_parts * 1e3, 4),
+           "config": {"workload": "C3 4x (conv3x3 256->256 + ReLU) on 1x256x64x64, chained: quantize once, "
+                                  "int8 NHWC requantize between convs, dequantize once"},
            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic("c3"), "kernel": "mm_tile_kernel (conv)",
                         "avg_launch_us": round(sum(ms) / len(ms) * 1e3, 2)}}
@@ -574,6 +592,87 @@ def bench_c3(a, dev):
         tops, nrep, best = cpu_baseline_conv(n, c, h, w, L)
         out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
                                "kind": "port", "sample": f"full C3 step, min of {nrep} reps ({best * 1e3:.1f} ms)"}
+    return out
+
+
+VGG16_CFG = [64, 64, "M", 128, 128, "M", 256, 256, 256, "M", 512, 512, 512, "M", 512, 512, 512, "M"]
+
+
+def vgg16_features():
+    """torchvision's VGG-16 `features` layout: biased 3x3 convs, in-place ReLUs, 2x2 max-pools."""
+    layers, c = [], 3
+    for v in VGG16_CFG:
+        if v == "M":
+            layers.append(torch.nn.MaxPool2d(2, 2))
+        else:
+            layers += [torch.nn.Conv2d(c, v, 3, padding=1), torch.nn.ReLU(inplace=True)]
+            c = v
+    return torch.nn.Sequential(*layers)
+
+
+def bench_vgg16(a, dev):
+    """VGG-16 features at batch 8 (C4's VGG shapes, torchvision's layout with bias, ReLU and pools)
+    through torch.compile(backend="xdna"): the 13 convs become one xdna::conv3x3_chain. The same
+    model with the chaining pass off (each conv quantized from and dequantized to float32) is timed
+    beside it; both must give the same output."""
+    import torch_xdna
+    from torch_xdna import backend, runtime
+
+    n, hw = 8, 224
+    torch.manual_seed(0)
+    net = vgg16_features().eval().to(dev)
+    x = torch.randn(n, 3, hw, hw, generator=gen(0)).to(dev)
+    ops, c, size = 0, 3, hw
+    for v in VGG16_CFG:
+        if v == "M":
+            size //= 2
+        else:
+            ops += 2 * n * size * size * c * v * 9
+            c = v
+
+    def timed_model(chain):
+        """Compile (from a fresh Dynamo cache, the chaining pass on or off), check that every conv ran on
+        the GPU, then time it. Returns (output, GPU s / step, host s / step)."""
+        torch._dynamo.reset()
+        runtime.stats.reset()
+        saved = backend._chain_convs
+        if not chain:
+            backend._chain_convs = lambda gm, cid: 0
+        try:
+            m = torch.compile(net, backend="xdna", options={"policy": "gpu", "fallback": "eager"})
+            with torch.no_grad():
+                y = m(x)
+        finally:
+            backend._chain_convs = saved
+        st = runtime.stats.as_dict()
+        if st["fallbacks"] or set(st["calls"]) != {"gpu"}:
+            raise SystemExit(f"VGG-16 convs did not all run on the GPU: {st}")
+
+        def step(i, ct=None):
+            with torch.no_grad():
+                return m(x)
+
+        return (y,) + timed_steps(a, step, None)
+
+    y_parts, sec_parts, host_parts = timed_model(False)
+    y_chain, sec, host = timed_model(True)
+    if not torch.equal(y_chain, y_parts):
+        raise SystemExit("chained and per-layer VGG-16 outputs differ")
+    ach = ops / sec / 1e12
+    out = {"value": round(ach, 2), "ms_per_step": round(sec * 1e3, 4), "host_ms_per_step": round(host * 1e3, 4),
+           "unchained_ms_per_step": round(sec_parts * 1e3, 4),
+           "unchained_host_ms_per_step": round(host_parts * 1e3, 4),
+           "config": {"workload": "VGG-16 features (13 conv3x3 + bias + ReLU, 5 max-pools) at 8x3x224x224 fp32, "
+                                  "torch.compile(backend='xdna'), convs chained as int8 NHWC on the GPU"},
+           "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                        "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None,
+                        "kernel": "whole step (13 convs, their quantize / requantize passes, the final pool)"}}
+    if not a.no_cpu_baseline:
+        tops, nrep, best = cpu_baseline_conv(1, 256, 56, 56, 1)
+        out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"one VGG-16 conv3 layer 256->256 at 1x256x56x56, min of "
+                               f"{nrep} reps ({best * 1e3:.1f} ms): torch CPU quantize + fp32 conv2d of the int8 "
+                               "values + shift + dequantize"}
     return out
 
 

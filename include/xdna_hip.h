@@ -99,12 +99,16 @@ int xdna_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const
 int xdna_pad_rows_i8(const int8_t* src, int64_t rows, int64_t cols, int64_t ld_src, int8_t* dst,
                      int64_t ld_dst, int64_t cols_pad, void* stream);
 
+/* Floats of caller scratch per image for the per-image max of the two calls below (block maxima,
+ * reduced by the kernel that needs the image's max: no atomics, nothing to clear first). */
+#define XDNA_AMAX_WS_PER_IMAGE 256
+
 /* Per-image quantization of an NCHW activation into the conv's NHWC int8 layout:
  *   sx[b] = max(amax |x[b]|, 1e-8f) / 127 over the whole image (C*H*W values),
  *   q[b, p, c] = clamp(round_half_even(x[b, c, p] / sx[b]), -127, 127) for c < ch, 0 for
  *   ch <= c < c_pad, p = y * w + x,
- * bit-exact with torch_xdna/conv.py:45-46 (`conv3x3_int8`). amax_ws is caller scratch of nb
- * floats (overwritten). */
+ * bit-exact with torch_xdna/conv.py:45-46 (`conv3x3_int8`). amax_ws is caller scratch of
+ * nb * XDNA_AMAX_WS_PER_IMAGE floats (overwritten). */
 int xdna_conv_quant_nhwc(const void* x, int x_dtype, int64_t nb, int64_t ch, int64_t h, int64_t w,
                          int8_t* q, int64_t c_pad, float* sx, float* amax_ws, void* stream);
 
@@ -132,6 +136,20 @@ int xdna_conv3x3_i8(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c
 int xdna_conv_dequant(const void* q, int relu, int64_t nb, int64_t h, int64_t w, int64_t co,
                       const float* scale, const float* sx, const float* bias, void* y, int y_dtype,
                       void* stream);
+
+/* Conv-to-conv chaining (the reference's "What is left", results/conv3x3_cascade.md:216-222): the
+ * previous conv's NHWC output q [nb, h, w, co] (uint8 when relu) goes straight to the next conv's
+ * NHWC int8 input xq_next [nb, h', w', c_pad_next] with its per-image scale sx_next [nb], computing
+ * exactly what the reference's chain computes through float tensors: the dequantize of
+ * torch_xdna/conv.py:48-50 (q * (scale[o] * sx[b]) (+ bias[o]), cast to x_dtype), the 2x2 / stride-2
+ * max-pool between the layers when pool != 0 (h' = h / 2, w' = w / 2), and the next layer's
+ * per-image quantize (conv.py:45-46). relu_y != 0 adds the graph ReLU that follows a biased conv
+ * (torch_xdna/backend.py:161-165 fuses a ReLU only into bias-free convs). Pooling runs on the
+ * integers (the dequantize is non-decreasing in q). amax_ws is caller scratch of
+ * nb * XDNA_AMAX_WS_PER_IMAGE floats (overwritten). */
+int xdna_conv_requant_next(const void* q, int relu, int relu_y, int pool, int64_t nb, int64_t h, int64_t w, int64_t co,
+                           const float* scale, const float* sx, const float* bias, int x_dtype, int8_t* xq_next,
+                           int64_t c_pad_next, float* sx_next, float* amax_ws, void* stream);
 
 /* int8 layout changes for the reference op's NCHW int8 contract (torch_xdna/ops.py:64-76):
  * NCHW [nb, ch, h, w] -> NHWC [nb, h, w, c_pad] (zero channels past ch), and

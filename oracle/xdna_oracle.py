@@ -261,6 +261,16 @@ def conv_dequant(q, scale, sx, bias=None):
     return y
 
 
+def max_pool2(y):
+    """2x2 / stride-2 max-pool of NCHW y, floor mode (torch.nn.functional.max_pool2d(y, 2, 2)), the
+    pool between the convs of a VGG-style chain (examples/conv_xdna.py, vgg16)."""
+    y = np.asarray(y)
+    n, c, h, w = y.shape
+    ho, wo = h // 2, w // 2
+    v = y[:, :, :2 * ho, :2 * wo].reshape(n, c, ho, 2, wo, 2)
+    return v.max(axis=(3, 5))
+
+
 def conv3x3_layer(xq, wq, shift, relu):
     """`ConvLayer.cpu` (torch_xdna/conv.py:89-92): the int8/uint8 output of one layer."""
     return requant(conv3x3_acc(xq, wq), shift, relu)

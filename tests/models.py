@@ -76,6 +76,24 @@ class VGGBlock(torch.nn.Module):
         return x
 
 
+class VGGStack(torch.nn.Module):
+    """A VGG-style stack: biased convs with in-place ReLUs and 2x2 max-pools (torchvision's layout),
+    bias-free convs whose ReLU the rewrite fuses, channel counts that are and are not multiples of 64."""
+
+    def __init__(self):
+        super().__init__()
+        self.features = torch.nn.Sequential(
+            torch.nn.Conv2d(3, 32, 3, padding=1), torch.nn.ReLU(inplace=True),
+            torch.nn.Conv2d(32, 64, 3, padding=1), torch.nn.ReLU(inplace=True), torch.nn.MaxPool2d(2, 2),
+            torch.nn.Conv2d(64, 48, 3, padding=1, bias=False), torch.nn.ReLU(),
+            torch.nn.MaxPool2d(2),
+            torch.nn.Conv2d(48, 64, 3, padding=1), torch.nn.ReLU(inplace=True),
+            torch.nn.Conv2d(64, 40, 3, padding=1))
+
+    def forward(self, x):
+        return torch.relu(self.features(x))
+
+
 def run(net, x, **opts):
     """torch.compile with the xdna backend from a fresh Dynamo cache and fresh stats."""
     from torch_xdna import runtime

@@ -121,9 +121,8 @@ def test_launch_failure(gpu, monkeypatch):
     assert s["fallbacks"] and not s["gpu_available"] and s["calls"].get("cpu") == 3, s
 
 
-def test_conv_pass(gpu):
+def _conv_graph(gpu, net, x):
     import torch_xdna
-    from torch_xdna.conv import conv3x3_int8
 
     graphs = []
 
@@ -134,12 +133,31 @@ def test_conv_pass(gpu):
 
     torch._dynamo.reset()
     with torch.no_grad():
-        torch.compile(CNN().eval().to(gpu), backend=capture)(torch.randn(1, 64, 16, 64, device=gpu))
-    nodes = [n for n in graphs[0].graph.nodes if n.op == "call_function"]
+        torch.compile(net.eval().to(gpu), backend=capture)(x.to(gpu))
+    return [n for n in graphs[0].graph.nodes if n.op == "call_function"]
+
+
+def test_conv_pass(gpu, monkeypatch):
+    """The reference's case_conv_pass (which convs are rewritten, which ReLU is fused), with the
+    conv-to-conv chaining switched off; then the chained graph of the same model."""
+    from torch_xdna import backend
+    from torch_xdna.conv import conv3x3_int8
+
+    x = torch.randn(1, 64, 16, 64)
+    with monkeypatch.context() as m:
+        m.setattr(backend, "_chain_convs", lambda gm, cid: 0)
+        nodes = _conv_graph(gpu, CNN(), x)
     convs = [n for n in nodes if n.target is conv3x3_int8]
     assert [n.args[3] for n in convs] == [False, True, False]
     assert sum(n.target in (torch.relu, torch.nn.functional.relu) for n in nodes) == 1
     assert sum(n.target is torch.conv2d for n in nodes) == 1
+
+    nodes = _conv_graph(gpu, CNN(), x)
+    chains = [n for n in nodes if n.target is torch.ops.xdna.conv3x3_chain.default]
+    assert len(chains) == 1 and not any(n.target is conv3x3_int8 for n in nodes)
+    _, ws, bs, relus, relu_after, pools, _ = chains[0].args
+    assert (len(ws), relus, relu_after, pools) == (3, [False, True, False], [True, False, False], [False] * 3)
+    assert not any(backend._is_relu(n) for n in nodes) and sum(n.target is torch.conv2d for n in nodes) == 1
 
 
 @pytest.mark.parametrize("net_cls,shape,ncalls", [(CNN, (2, 64, 32, 64), 3), (OddCNN, (2, 3, 13, 37), 2)])

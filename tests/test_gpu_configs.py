@@ -93,6 +93,51 @@ def test_c3_conv_chain(gpu):
     assert np.array_equal(y.cpu().numpy(), h)
 
 
+def _oracle_stack(net, x, dtype):
+    """VGGStack through the oracle: per conv quantize -> int32 sums -> shift -> requant -> dequant
+    (+ bias) -> cast, then the graph's ReLU / max-pool, as the unchained layers compute it."""
+    h = x
+    mods = list(net.features) + [torch.nn.ReLU()]
+    i = 0
+    while i < len(mods):
+        m = mods[i]
+        if isinstance(m, torch.nn.Conv2d):
+            fused = m.bias is None and isinstance(mods[i + 1], torch.nn.ReLU)
+            xq, sx = O.conv_quant_images(h)
+            wq, sw = O.conv_weight_quant(m.weight.detach().cpu().numpy())
+            acc = c_oracle.conv3x3_acc(xq, wq)
+            shift = O.calibrate_shift(acc[0], fused)
+            b = None if m.bias is None else m.bias.detach().cpu().numpy()
+            h = O.to_dtype(O.conv_dequant(O.requant(acc, shift, fused), O.conv_scale(sw, shift), sx, b), dtype)
+            i += 2 if fused else 1
+            continue
+        h = np.maximum(h, 0) if isinstance(m, torch.nn.ReLU) else O.max_pool2(h)
+        i += 1
+    return h
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_conv_chain_vgg_stack(gpu, dtype):
+    """A VGG-style stack (biased convs with graph ReLUs, a fused ReLU, 2x2 max-pools, 40 / 48-channel
+    layers) compiled into one xdna::conv3x3_chain: the int8 activation stays on the GPU between the
+    convs, and the output equals the oracle's unchained composition bit for bit."""
+    from models import VGGStack, run
+    from torch_xdna import conv as xconv
+
+    torch.manual_seed(5)
+    net = VGGStack().eval()
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16}[dtype]
+    x = torch.randn(3, 3, 36, 30, generator=_gen(21))
+    xconv._layers.clear()
+    y = run(net.to(gpu, tdt), x.to(gpu, tdt), policy="gpu", fallback="eager")
+    s = _stats()
+    assert s["calls"] == {"gpu": 5} and not s["fallbacks"], s
+    net_f = net.float().cpu()
+    want = _oracle_stack(net_f, O.to_dtype(x.numpy(), dtype), dtype)
+    assert y.shape == want.shape
+    assert np.array_equal(y.float().cpu().numpy(), want)
+
+
 def _sampled_conv_check(xq_nchw, wq, q_nhwc, shift, relu, n_samples, seed):
     rng = np.random.default_rng(seed)
     nb, ci, h, w = xq_nchw.shape

@@ -226,6 +226,36 @@ def test_conv3x3(gpu, n, ci, co, h, w, relu):
     assert np.array_equal(_np(y), O.conv_dequant(want_q, scale, sx_r, bias.numpy()))
 
 
+@pytest.mark.parametrize("relu", [False, True])
+@pytest.mark.parametrize("pool", [False, True])
+@pytest.mark.parametrize("x_dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("n,co,h,w,c_pad", [(2, 64, 14, 10, 64), (1, 20, 9, 7, 32), (3, 48, 6, 6, 48)])
+def test_conv_requant_next(gpu, relu, pool, x_dtype, n, co, h, w, c_pad):
+    """Conv chaining: the previous conv's NHWC q -> the next conv's NHWC int8 input and per-image scale,
+    equal to dequantize -> cast -> [2x2 max-pool] -> per-image quantize through the oracle (bit for
+    bit, padding channels zero)."""
+    from torch_xdna import kernels
+
+    g = torch.Generator().manual_seed(n * 100 + co + h)
+    q = (torch.randint(0, 256, (n, h, w, co), generator=g, dtype=torch.uint8) if relu
+         else torch.randint(-128, 128, (n, h, w, co), generator=g, dtype=torch.int8))
+    scale = torch.rand(co, generator=g) * 1e-3 + 1e-5
+    sx = torch.rand(n, generator=g) + 0.1
+    bias = torch.randn(co, generator=g) * 0.1
+    for b in (None, bias):
+        xq, sxn = kernels.conv_requant_next(q.to(gpu), relu, pool, scale.to(gpu), sx.to(gpu),
+                                            None if b is None else b.to(gpu), DT[x_dtype], c_pad)
+        y = O.to_dtype(O.conv_dequant(_np(q).transpose(0, 3, 1, 2), scale.numpy(), sx.numpy(),
+                                      None if b is None else b.numpy()), x_dtype)
+        if pool:
+            y = O.max_pool2(y)
+        xq_r, sx_r = O.conv_quant_images(y)
+        got = _np(xq)
+        assert got.shape == (n, y.shape[2], y.shape[3], c_pad)
+        assert np.array_equal(got[..., :co].transpose(0, 3, 1, 2), xq_r) and not got[..., co:].any()
+        assert np.array_equal(_np(sxn), sx_r)
+
+
 def test_conv_layouts(gpu):
     from torch_xdna import kernels
 

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import fake_device
-from models import CNN, Attn, Net, OddCNN, rel_err, run
+from models import CNN, Attn, Net, OddCNN, VGGStack, rel_err, run
 
 torch.manual_seed(0)
 
@@ -295,6 +295,109 @@ def test_conv_silent_wrong_fake(fake):
     assert len(s["fallbacks"]) == 1 and "disagrees with the CPU" in s["fallbacks"][0][1], s["fallbacks"]
     assert s["calls"] == {"gpu": 2, "cpu": 1}, s["calls"]
     assert rel_err(y, ref) < 0.05
+
+
+def _compile_capture(net, x):
+    """Compile net with the xdna passes and return (output, the rewritten graph)."""
+    import torch_xdna
+    from torch_xdna import runtime
+
+    graphs = []
+
+    def capture(gm, example_inputs):
+        torch_xdna.offload_gemms(gm, example_inputs, torch_xdna.Config(policy="gpu"))
+        graphs.append(gm)
+        return gm.forward
+
+    torch._dynamo.reset()
+    runtime.stats.reset()
+    with torch.no_grad():
+        y = torch.compile(net, backend=capture)(x)
+    return y, graphs[0]
+
+
+@pytest.fixture
+def chain_fake(fake):
+    """The fake device, with its (CPU) tensors taken for GPU tensors by the conv-chaining pass and op,
+    and a count of the chaining launches."""
+    from torch_xdna import backend, kernels
+    from torch_xdna import conv as xconv
+
+    fake.setattr(backend, "_on_gpu", lambda x: True)
+    fake.setattr(xconv, "_on_gpu", lambda t: True)
+    calls = []
+
+    def counted(*a, **k):
+        calls.append(a[1:3] + (k.get("relu_y", False),))
+        return fake_device.conv_requant_next(*a, **k)
+
+    fake.setattr(kernels, "conv_requant_next", counted)
+    xconv._layers.clear()
+    return calls
+
+
+def test_conv_chain_fake(chain_fake, fake):
+    """conv -> ReLU -> conv -> ReLU -> pool -> conv(ReLU fused) -> pool -> conv -> ReLU -> conv becomes one
+    xdna::conv3x3_chain, which gives the same output as the unchained layers (each calibrated from
+    its own input in a fresh run)."""
+    from torch_xdna import backend, runtime
+    from torch_xdna import conv as xconv
+    from torch_xdna.conv import conv3x3_int8
+
+    torch.manual_seed(3)
+    net = VGGStack().eval()
+    x = torch.randn(2, 3, 20, 18)
+    y, gm = _compile_capture(net, x)
+    nodes = [n for n in gm.graph.nodes if n.op == "call_function"]
+    chains = [n for n in nodes if n.target is torch.ops.xdna.conv3x3_chain.default]
+    assert len(chains) == 1 and not any(n.target is conv3x3_int8 for n in nodes), nodes
+    _, ws, bs, relus, relu_after, pools, _ = chains[0].args
+    assert len(ws) == 5 and [b is not None for b in bs] == [True, True, False, True, True]
+    assert relus == [False, False, True, False, False]
+    assert relu_after == [True, True, False, True, False] and pools == [False, True, True, False, False]
+    assert sum(backend._is_pool2(n) for n in nodes) == 0 and sum(backend._is_relu(n) for n in nodes) == 1
+    s = runtime.stats.as_dict()
+    assert s["calls"] == {"gpu": 5} and not s["fallbacks"], s
+    assert chain_fake == [(False, False, True), (False, True, True), (True, True, False), (False, False, True)]
+    assert y.shape == (2, 40, 5, 4)
+
+    xconv._layers.clear()
+    chain_fake.clear()
+    fake.setattr(backend, "_chain_convs", lambda gm, cid: 0)
+    y_parts, gm = _compile_capture(net, x)
+    assert not chain_fake and sum(n.target is conv3x3_int8 for n in gm.graph.nodes) == 5
+    assert torch.equal(y, y_parts)
+    with torch.no_grad():
+        assert rel_err(y, net(x)) < 0.05
+
+
+def test_conv_chain_layer_failure_fake(chain_fake, fake):
+    """A chain layer whose first launch disagrees with the CPU: it moves to the CPU and the chain runs
+    as its parts, with the same result as the unchained layers."""
+    from torch_xdna import kernels, runtime
+    from torch_xdna import conv as xconv
+
+    real = kernels.conv3x3
+
+    def corrupt(xq, wq, shift, relu):
+        q = real(xq, wq, shift, relu)
+        if wq.shape[0] == 48:
+            q[0, 0, 0, 0] += 1
+        return q
+
+    fake.setattr(kernels, "conv3x3", corrupt)
+    torch.manual_seed(4)
+    net = VGGStack().eval()
+    x = torch.randn(1, 3, 16, 16)
+    y, _ = _compile_capture(net, x)
+    s = runtime.stats.as_dict()
+    assert len(s["fallbacks"]) == 1 and "disagrees with the CPU" in s["fallbacks"][0][1], s["fallbacks"]
+    assert s["calls"] == {"gpu": 4, "cpu": 1}, s["calls"]
+    for _, layer in xconv._layers.values():
+        layer.device = "cpu"
+    fake.setattr(kernels, "conv3x3", real)
+    y_cpu, _ = _compile_capture(net, x)
+    assert torch.equal(y, y_cpu)
 
 
 def test_report_text(fake):

@@ -331,3 +331,11 @@ def test_gemm_bf16_bound_contains_float32_and_rejects_wrong_operands():
     ys, bs = O.gemm_bf16(sq, ws)
     yt = O.to_bf16(sq).astype(np.float64) @ O.to_bf16(ws).astype(np.float64)   # x @ w instead of x @ w^T
     assert (np.abs(yt - ys) > bs).mean() > 0.5
+
+
+def test_max_pool2_matches_torch():
+    rng = np.random.default_rng(9)
+    for shape in [(2, 3, 8, 6), (1, 5, 7, 9)]:
+        y = rng.standard_normal(shape).astype(np.float32)
+        want = torch.nn.functional.max_pool2d(torch.from_numpy(y), 2, 2).numpy()
+        assert np.array_equal(O.max_pool2(y), want)

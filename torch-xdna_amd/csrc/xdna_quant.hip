@@ -294,11 +294,20 @@ __global__ void pad_rows_i8_kernel(const int8_t* __restrict__ src, int64_t rows,
 }
 
 // ------------------------------------------------------------------------------ conv quantize
-// Per-image max |x| over nb images of `per` elements: grid (blocks, nb), atomic max on the float
-// bits (order-preserving for non-negative floats) into amax[b], which starts at 0.
+// Per-image max |x| in two steps without atomics: a first kernel with grid (parts, nb), parts <=
+// AMAX_PARTS, writes each block's max to parts_out[b * AMAX_PARTS + block]; the kernel that needs
+// the image's max reduces those `parts` values (image_amax). The caller's scratch holds nb *
+// AMAX_PARTS floats.
+constexpr int AMAX_PARTS = XDNA_AMAX_WS_PER_IMAGE;
+
+__device__ __forceinline__ float image_amax(const float* __restrict__ parts, int64_t b, int nparts, float* red) {
+  const float m = threadIdx.x < nparts ? parts[b * AMAX_PARTS + threadIdx.x] : 0.0f;
+  return group_max<256>(m, red);
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void image_absmax_kernel(const void* __restrict__ x, int64_t per,
-                                                           uint32_t* __restrict__ amax_bits) {
+                                                           float* __restrict__ parts) {
   __shared__ float red[4];
   const int64_t b = blockIdx.y;
   constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
@@ -319,7 +328,7 @@ __global__ __launch_bounds__(256) void image_absmax_kernel(const void* __restric
       m = fmaxf(m, fabsf(load_as_f32<DT>(xb, i)));
   }
   m = group_max<256>(m, red);
-  if (threadIdx.x == 0) atomicMax(amax_bits + b, __float_as_uint(m));
+  if (threadIdx.x == 0) parts[b * AMAX_PARTS + blockIdx.x] = m;
 }
 
 // Quantize + NCHW -> NHWC: tile of 64 channels x 64 pixels per block (256 threads). Wave w
@@ -328,14 +337,15 @@ __global__ __launch_bounds__(256) void image_absmax_kernel(const void* __restric
 // write-out gives each thread 16 channels of one pixel (a 16-byte store).
 template <int DT>
 __global__ __launch_bounds__(256) void conv_quant_nhwc_kernel(const void* __restrict__ x, int64_t ch, int64_t hw,
-                                                              const uint32_t* __restrict__ amax_bits,
+                                                              const float* __restrict__ parts, int nparts,
                                                               int8_t* __restrict__ q, int64_t c_pad,
                                                               float* __restrict__ sx) {
   __shared__ uint32_t tile[64][17];
+  __shared__ float red[4];
   const int64_t b = blockIdx.z;
   const int64_t p0 = (int64_t)blockIdx.x * 64;
   const int64_t c0 = (int64_t)blockIdx.y * 64;
-  const float sc = scale_from_amax(__uint_as_float(amax_bits[b]));
+  const float sc = scale_from_amax(image_amax(parts, b, nparts, red));
   const float rc = 1.0f / sc;
   if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) sx[b] = sc;
   const int lane = threadIdx.x & 63;
@@ -426,6 +436,163 @@ __global__ __launch_bounds__(256) void conv_dequant_kernel(const void* __restric
     float v = qf * f;
     if (bias) v = v + bias[o];
     store_from_f32<DT>(y, (b * co + o) * hw + p, v);
+  }
+}
+
+// ------------------------------------------------------------------------------ conv chaining
+// Between two convs of a chain: the previous conv's NHWC int8 output q (uint8 with ReLU) is
+// dequantized as conv_dequant does (q * (scale[o] * sx[b]) (+ bias[o]), cast to the activation
+// dtype), optionally 2x2 max-pooled, and quantized per image for the next conv, straight into its
+// NHWC int8 layout: the float activation is never written. Dequantize and cast are non-decreasing
+// in q (scale * sx > 0), so pooling the integers first gives the same values as pooling the floats.
+// relu_y applies a ReLU to the dequantized value (a graph ReLU after a biased conv); a ReLU before
+// or after the cast gives the same quantized integers (the cast is monotone and keeps 0).
+// Item: one output pixel, 16 channels (item = pixel * ng + group, ng = c_pad / 16); indices within
+// an image are 32-bit (the host checks the sizes). PASS 0 (grid (parts, nb), grid-stride over the
+// items) writes each block's max |x| to parts_ws; PASS 1 (one item per thread) reduces the image's
+// parts, then quantizes (scale as conv_quant_nhwc), channels >= co written as 0.
+// PASS 0 keeps, per channel, only the min and max of the (pooled) integers: the dequantize is
+// non-decreasing in q, so max |x| over a channel is max(|x(q_min)|, |x(q_max)|). This needs each
+// thread's items to share one channel group (grid stride a multiple of ng); otherwise PASS 0
+// dequantizes every value.
+struct ChainArgs {
+  const uint8_t* q;
+  uint32_t h, w, co, ho, wo, ng;
+  const float* scale;
+  const float* bias;
+  int relu_y, vec_f;
+};
+
+// The (pooled) integers of channels c0 .. c0+15 of output pixel pix of image b (int domain: uint8
+// with ReLU, else int8); channels >= co read as the domain's minimum.
+template <bool RELU, bool POOL>
+__device__ __forceinline__ void chain_q(const ChainArgs& a, int64_t b, uint32_t pix, uint32_t c0, int (&qv)[16]) {
+  const uint32_t y = pix / a.wo, x = pix - y * a.wo;
+  const uint8_t* img = a.q + (uint64_t)b * a.h * a.w * a.co;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) qv[e] = RELU ? 0 : -128;
+  const bool vec = (a.co % 16 == 0) && (c0 + 16 <= a.co);
+#pragma unroll
+  for (int d = 0; d < (POOL ? 4 : 1); ++d) {
+    const uint32_t sy = POOL ? 2 * y + (d >> 1) : y, sxp = POOL ? 2 * x + (d & 1) : x;
+    const uint8_t* src = img + (sy * a.w + sxp) * a.co + c0;
+    if (vec) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(src);
+      const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t byte = (words[e >> 2] >> (8 * (e & 3))) & 0xffu;
+        qv[e] = max(qv[e], RELU ? (int)byte : (int)(int8_t)byte);
+      }
+    } else if (c0 < a.co) {
+      const uint32_t last = a.co - 1 - c0;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint8_t byte = src[min((uint32_t)e, last)];
+        if ((uint32_t)e <= last) qv[e] = max(qv[e], RELU ? (int)byte : (int)(int8_t)byte);
+      }
+    }
+  }
+}
+
+// scale * sx and bias of channels c0 .. c0+15 (0 past co).
+__device__ __forceinline__ void chain_factors(const ChainArgs& a, uint32_t c0, float sxb, float (&f)[16],
+                                              float (&bv)[16]) {
+  if (a.vec_f && c0 + 16 <= a.co) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 s4 = reinterpret_cast<const float4*>(a.scale + c0)[k];
+      f[4 * k] = s4.x * sxb; f[4 * k + 1] = s4.y * sxb; f[4 * k + 2] = s4.z * sxb; f[4 * k + 3] = s4.w * sxb;
+      float4 b4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (a.bias) b4 = reinterpret_cast<const float4*>(a.bias + c0)[k];
+      bv[4 * k] = b4.x; bv[4 * k + 1] = b4.y; bv[4 * k + 2] = b4.z; bv[4 * k + 3] = b4.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t o = min(c0 + e, a.co - 1);
+      const bool in = c0 + e < a.co;
+      f[e] = in ? a.scale[o] * sxb : 0.0f;
+      bv[e] = (in && a.bias) ? a.bias[o] : 0.0f;
+    }
+  }
+}
+
+// The activation value of integer q: q * f (+ bias), ReLU'd with relu_y, cast to DT (as a float).
+template <int DT>
+__device__ __forceinline__ float chain_value(int q, float f, float bias, bool has_bias, int relu_y) {
+  float t = (float)q * f;
+  if (has_bias) t = t + bias;
+  if (relu_y) t = fmaxf(t, 0.0f);
+  if constexpr (DT == XDNA_BF16) t = bf16_bits_to_f32(f32_to_bf16_bits(t));
+  if constexpr (DT == XDNA_F16) t = f16_bits_to_f32(f32_to_f16_bits(t));
+  return t;
+}
+
+template <int DT, bool RELU, bool POOL, int PASS>
+__global__ __launch_bounds__(256) void conv_chain_kernel(ChainArgs a, const float* __restrict__ sx,
+                                                         float* __restrict__ parts, int nparts,
+                                                         int8_t* __restrict__ xq, float* __restrict__ sx_next) {
+  __shared__ float red[4];
+  const int64_t b = blockIdx.y;
+  const uint32_t items = a.ho * a.wo * a.ng;
+  const float sxb = sx[b];
+  const bool has_bias = a.bias != nullptr;
+  int qv[16];
+  float f[16], bv[16];
+  if constexpr (PASS == 0) {
+    float m = 0.0f;
+    const uint32_t stride = gridDim.x * 256u;
+    uint32_t item = blockIdx.x * 256u + threadIdx.x;
+    if (stride % a.ng == 0) {
+      int hi[16], lo[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) { hi[e] = -1024; lo[e] = 1024; }
+      const uint32_t c0 = (item % a.ng) * 16;
+      const bool any = item < items;
+      for (; item < items; item += stride) {
+        chain_q<RELU, POOL>(a, b, item / a.ng, c0, qv);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) { hi[e] = max(hi[e], qv[e]); lo[e] = min(lo[e], qv[e]); }
+      }
+      if (any) {
+        chain_factors(a, c0, sxb, f, bv);
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (c0 + e < a.co)
+            m = fmaxf(m, fmaxf(fabsf(chain_value<DT>(hi[e], f[e], bv[e], has_bias, a.relu_y)),
+                               fabsf(chain_value<DT>(lo[e], f[e], bv[e], has_bias, a.relu_y))));
+      }
+    } else {
+      for (; item < items; item += stride) {
+        const uint32_t pix = item / a.ng, c0 = (item - pix * a.ng) * 16;
+        chain_q<RELU, POOL>(a, b, pix, c0, qv);
+        chain_factors(a, c0, sxb, f, bv);
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (c0 + e < a.co) m = fmaxf(m, fabsf(chain_value<DT>(qv[e], f[e], bv[e], has_bias, a.relu_y)));
+      }
+    }
+    m = group_max<256>(m, red);
+    if (threadIdx.x == 0) parts[b * AMAX_PARTS + blockIdx.x] = m;
+  } else {
+    const float sc = scale_from_amax(image_amax(parts, b, nparts, red));
+    const float rc = 1.0f / sc;
+    const uint32_t item = blockIdx.x * 256u + threadIdx.x;
+    if (item == 0) sx_next[b] = sc;
+    if (item < items) {
+      const uint32_t pix = item / a.ng, c0 = (item - pix * a.ng) * 16;
+      chain_q<RELU, POOL>(a, b, pix, c0, qv);
+      chain_factors(a, c0, sxb, f, bv);
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        v[e] = c0 + e < a.co ? chain_value<DT>(qv[e], f[e], bv[e], has_bias, a.relu_y) : 0.0f;
+      uint32_t wds[4];
+      quant_pack<16>(v, sc, rc, wds);
+      *reinterpret_cast<uint4*>(xq + (uint64_t)b * items * 16 + (uint64_t)item * 16) =
+          make_uint4(wds[0], wds[1], wds[2], wds[3]);
+    }
   }
 }
 
@@ -548,24 +715,22 @@ int xdna_conv_quant_nhwc(const void* x, int x_dtype, int64_t nb, int64_t ch, int
   XDNA_REQUIRE(aligned(q, 16), "q must be 16-byte aligned");
   hipStream_t st = as_stream(stream);
   const int64_t hw = h * w, per = ch * hw;
-  uint32_t* bits = reinterpret_cast<uint32_t*>(amax_ws);
-  fill_u32_kernel<<<dim3((unsigned)cdiv(nb, 256)), 256, 0, st>>>(bits, nb, 0u);
-  const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(per, 256 * 16), 1024));
-  dim3 g1(blocks, (unsigned)nb, 1);
+  const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(per, 256 * 16), AMAX_PARTS));
+  dim3 g1((unsigned)parts, (unsigned)nb, 1);
   dim3 g2((unsigned)cdiv(hw, 64), (unsigned)cdiv(c_pad, 64), (unsigned)nb);
   XDNA_REQUIRE(cdiv(hw, 64) < (1ll << 31) && cdiv(c_pad, 64) < 65536, "image too large");
   switch (x_dtype) {
     case XDNA_F32:
-      image_absmax_kernel<XDNA_F32><<<g1, 256, 0, st>>>(x, per, bits);
-      conv_quant_nhwc_kernel<XDNA_F32><<<g2, 256, 0, st>>>(x, ch, hw, bits, q, c_pad, sx);
+      image_absmax_kernel<XDNA_F32><<<g1, 256, 0, st>>>(x, per, amax_ws);
+      conv_quant_nhwc_kernel<XDNA_F32><<<g2, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);
       break;
     case XDNA_BF16:
-      image_absmax_kernel<XDNA_BF16><<<g1, 256, 0, st>>>(x, per, bits);
-      conv_quant_nhwc_kernel<XDNA_BF16><<<g2, 256, 0, st>>>(x, ch, hw, bits, q, c_pad, sx);
+      image_absmax_kernel<XDNA_BF16><<<g1, 256, 0, st>>>(x, per, amax_ws);
+      conv_quant_nhwc_kernel<XDNA_BF16><<<g2, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);
       break;
     default:
-      image_absmax_kernel<XDNA_F16><<<g1, 256, 0, st>>>(x, per, bits);
-      conv_quant_nhwc_kernel<XDNA_F16><<<g2, 256, 0, st>>>(x, ch, hw, bits, q, c_pad, sx);
+      image_absmax_kernel<XDNA_F16><<<g1, 256, 0, st>>>(x, per, amax_ws);
+      conv_quant_nhwc_kernel<XDNA_F16><<<g2, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);
   }
   return launch_status("conv_quant_nhwc");
 }
@@ -604,6 +769,43 @@ int xdna_conv_dequant(const void* q, int relu, int64_t nb, int64_t h, int64_t w,
   }
 #undef XDNA_DQ
   return launch_status("conv_dequant");
+}
+
+int xdna_conv_requant_next(const void* q, int relu, int relu_y, int pool, int64_t nb, int64_t h, int64_t w, int64_t co,
+                           const float* scale, const float* sx, const float* bias, int x_dtype, int8_t* xq_next,
+                           int64_t c_pad_next, float* sx_next, float* amax_ws, void* stream) {
+  XDNA_REQUIRE(float_dtype(x_dtype), "x_dtype must be XDNA_F32, XDNA_BF16 or XDNA_F16");
+  XDNA_REQUIRE(nb >= 0 && h >= 1 && w >= 1 && co >= 1 && nb < 65536, "bad sizes");
+  XDNA_REQUIRE(c_pad_next >= co && c_pad_next % 16 == 0, "c_pad_next must be a multiple of 16 and >= co");
+  XDNA_REQUIRE(!pool || (h >= 2 && w >= 2), "a 2x2 pool needs h, w >= 2");
+  if (nb == 0) return XDNA_OK;
+  XDNA_REQUIRE(q && scale && sx && xq_next && sx_next && amax_ws, "null pointer");
+  XDNA_REQUIRE(aligned(xq_next, 16) && (co % 16 != 0 || aligned(q, 16)), "misaligned buffers");
+  const int64_t ho = pool ? h / 2 : h, wo = pool ? w / 2 : w;
+  const int64_t items = ho * wo * (c_pad_next / 16);
+  XDNA_REQUIRE(h * w * co < (1ll << 31) && items * 16 < (1ll << 31), "image too large");
+  hipStream_t st = as_stream(stream);
+  const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(items, 256), AMAX_PARTS));
+  dim3 g0((unsigned)parts, (unsigned)nb), g1((unsigned)cdiv(items, 256), (unsigned)nb);
+  ChainArgs ca{static_cast<const uint8_t*>(q), (uint32_t)h, (uint32_t)w, (uint32_t)co, (uint32_t)ho, (uint32_t)wo,
+               (uint32_t)(c_pad_next / 16), scale, bias, relu_y ? 1 : 0,
+               (aligned(scale, 16) && (!bias || aligned(bias, 16))) ? 1 : 0};
+#define XDNA_CH(DT, R, P)                                                                                 \
+  conv_chain_kernel<DT, R, P, 0><<<g0, 256, 0, st>>>(ca, sx, amax_ws, parts, xq_next, sx_next);          \
+  conv_chain_kernel<DT, R, P, 1><<<g1, 256, 0, st>>>(ca, sx, amax_ws, parts, xq_next, sx_next);
+#define XDNA_CH_RP(DT)                 \
+  if (relu && pool) { XDNA_CH(DT, true, true) }        \
+  else if (relu) { XDNA_CH(DT, true, false) }          \
+  else if (pool) { XDNA_CH(DT, false, true) }          \
+  else { XDNA_CH(DT, false, false) }
+  switch (x_dtype) {
+    case XDNA_F32: XDNA_CH_RP(XDNA_F32) break;
+    case XDNA_BF16: XDNA_CH_RP(XDNA_BF16) break;
+    default: XDNA_CH_RP(XDNA_F16)
+  }
+#undef XDNA_CH_RP
+#undef XDNA_CH
+  return launch_status("conv_requant_next");
 }
 
 int xdna_nchw_to_nhwc_i8(const int8_t* src, int64_t nb, int64_t ch, int64_t h, int64_t w, int8_t* dst, int64_t c_pad,

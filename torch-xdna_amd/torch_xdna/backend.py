@@ -116,6 +116,8 @@ def offload_gemms(gm: torch.fx.GraphModule, example_inputs, cfg) -> int:
     if cfg.precision == "int8" and cfg.cpu_kernel == "int8":
         _quantize_in_graph(gm, cid)
     count += _offload_convs(gm, static, cid, attr, cfg)
+    if cfg.fuse:
+        _chain_convs(gm, cid)
     gm.graph.lint()
     gm.recompile()
     return count
@@ -173,6 +175,103 @@ def _offload_convs(gm, static, cid, attr, cfg):
         if relu is not None:
             gm.graph.erase_node(relu)
         gm.graph.erase_node(node)
+        count += 1
+    return count
+
+
+MAXPOOL2D = {F.max_pool2d, torch.max_pool2d}
+
+
+def _is_pool2(n):
+    """A 2x2 / stride-2 max-pool without padding, dilation, ceil mode or returned indices."""
+    if n.op != "call_function" or n.target not in MAXPOOL2D:
+        return False
+    names = ("input", "kernel_size", "stride", "padding", "dilation", "ceil_mode", "return_indices")
+    args = dict(zip(names, n.args), **n.kwargs)
+    k = args.get("kernel_size")
+    s = args.get("stride")
+    if s is None or (isinstance(s, (list, tuple)) and len(s) == 0):
+        s = k
+    try:
+        return (_pair(k) == (2, 2) and _pair(s) == (2, 2) and _pair(args.get("padding", 0)) == (0, 0)
+                and _pair(args.get("dilation", 1)) == (1, 1) and not args.get("ceil_mode", False)
+                and not args.get("return_indices", False))
+    except TypeError:
+        return False
+
+
+def _on_gpu(x):
+    """Whether graph value x is a GPU tensor (its example value's device)."""
+    xt = x.meta.get("example_value") if isinstance(x, torch.fx.Node) else None
+    return isinstance(xt, torch.Tensor) and xt.device.type == "cuda"
+
+
+def _chain_convs(gm, cid):
+    """conv3x3_int8 -> [ReLU] [2x2 max-pool] -> conv3x3_int8 -> ... where every intermediate has that
+    one use -> one xdna::conv3x3_chain, on GPU graphs: the activation stays NHWC int8 from conv to conv
+    (the reference lists this as its next step, results/conv3x3_cascade.md:216-222). The ReLU is the
+    graph ReLU after a biased conv, which the conv rewrite does not fuse (backend.py:161-165)."""
+    from .conv import conv3x3_int8
+
+    def is_conv(n):
+        return n.op == "call_function" and n.target is conv3x3_int8
+
+    def following(n):
+        """(next conv, ReLU between, pool between, the nodes between) when n's value reaches a conv's
+        input through single-use ReLU / 2x2 max-pool nodes (at most one of each)."""
+        relu = pool = False
+        between = []
+        cur = n
+        while True:
+            users = list(cur.users)
+            if len(users) != 1 or not users[0].args or users[0].args[0] is not cur:
+                return None
+            u = users[0]
+            if is_conv(u):
+                return u, relu, pool, between
+            if _is_relu(u) and not relu and len(u.args) <= 2 and set(u.kwargs) <= {"inplace"}:
+                relu = True
+            elif _is_pool2(u) and not pool:
+                pool = True
+            else:
+                return None
+            between.append(u)
+            cur = u
+
+    taken = set()
+    count = 0
+    for node in list(gm.graph.nodes):
+        if not is_conv(node) or node in taken or not _on_gpu(node.args[0]):
+            continue
+        chain, relus_after, pools, between = [node], [], [], []
+        cur = node
+        while True:
+            nxt = following(cur)
+            if nxt is None:
+                break
+            conv_node, relu, pooled, mid = nxt
+            if relu and cur.args[3]:        # a fused ReLU already: a second one changes nothing
+                relu = False
+            relus_after.append(relu)
+            pools.append(pooled)
+            between.extend(mid)
+            chain.append(conv_node)
+            cur = conv_node
+        if len(chain) < 2:
+            continue
+        relus_after.append(False)
+        pools.append(False)
+        taken.update(chain)
+        last = chain[-1]
+        args = (chain[0].args[0], [c.args[1] for c in chain], [c.args[2] for c in chain],
+                [c.args[3] for c in chain], relus_after, pools, cid)
+        with gm.graph.inserting_after(last):
+            new = gm.graph.call_function(torch.ops.xdna.conv3x3_chain.default, args)
+        new.meta.update(last.meta)
+        last.replace_all_uses_with(new)
+        order = {n: i for i, n in enumerate(gm.graph.nodes)}
+        for dead in sorted(chain + between, key=lambda n: -order[n]):
+            gm.graph.erase_node(dead)
         count += 1
     return count
 

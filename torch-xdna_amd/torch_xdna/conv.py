@@ -264,3 +264,80 @@ def conv3x3_fused(cfg, x, weight, bias, relu):
             y = y.to(x.dtype).to(x.device)
     _account(device, t0, n, layer)
     return y
+
+
+def _on_gpu(t):
+    return t.device.type == "cuda"
+
+
+def _unfused_chain(cfg_id, x, weights, biases, relus, relu_after, pools):
+    """The chain as its parts: conv3x3_int8 per layer, then relu and max_pool2d(2) where they sit."""
+    y = x
+    last = len(weights) - 1
+    for i, (wt, b, r) in enumerate(zip(weights, biases, relus)):
+        y = conv3x3_int8(y, wt, b, r, cfg_id)
+        if i < last and relu_after[i]:
+            y = torch.relu(y)
+        if i < last and pools[i]:
+            y = torch.nn.functional.max_pool2d(y, 2, 2)
+    return y
+
+
+def conv3x3_chain(cfg, cfg_id, x, weights, biases, relus, relu_after, pools):
+    """conv3x3_int8 layers, with 2x2 max-pools between some of them, run with the activation kept as
+    NHWC int8 on the GPU from one conv to the next (the reference's "What is left",
+    results/conv3x3_cascade.md:216-222). Between two layers one HIP pass pair does what the reference
+    does through float tensors (conv.py:48-50 dequantize, the ReLU and pool, conv.py:45-46 quantize),
+    so every layer sees the same integers as in the unfused chain. Each layer keeps its own shift calibration,
+    first-launch check and device choice; the chain falls back to its parts when a layer cannot run
+    on the GPU."""
+    if not _on_gpu(x):
+        return _unfused_chain(cfg_id, x, weights, biases, relus, relu_after, pools)
+    n, _, h, w = x.shape
+    last = len(weights) - 1
+    with _lock:
+        layers, hh, ww = [], h, w
+        for i, (wt, r) in enumerate(zip(weights, relus)):
+            layers.append(_layer(wt, hh, ww, r))
+            if i < last and pools[i]:
+                hh, ww = hh // 2, ww // 2
+        if not all(_gpu_route(cfg, L, True) for L in layers):
+            y = None
+        else:
+            y = _gpu_chain(cfg, x, layers, biases, relu_after, pools)
+    if y is None:
+        return _unfused_chain(cfg_id, x, weights, biases, relus, relu_after, pools)
+    return y
+
+
+def _gpu_chain(cfg, x, layers, biases, relu_after, pools):
+    """The GPU chain, or None when a layer fails or must run on the CPU (its state is kept)."""
+    dev = x.device
+    last = len(layers) - 1
+    t0 = time.perf_counter()
+    done = 0
+    try:
+        xq, sx = kernels.conv_quant(x, layers[0].ci_pad)
+        for i, L in enumerate(layers):
+            if L.shift is None:
+                L.calibrate_gpu(xq[:1])
+            if L.device is None:
+                _first_call(cfg, L, lambda v, L=L, xq=xq: L.gpu_nhwc(xq, verify=v), None, True)
+            if L.device != "gpu":
+                return None
+            q = L.gpu_nhwc(xq, verify=cfg.verify == "always")
+            b = None if biases[i] is None else biases[i].to(dev, torch.float32).contiguous()
+            if i < last:
+                xq, sx = kernels.conv_requant_next(q, L.relu, pools[i], L.scale(dev), sx, b, x.dtype,
+                                                   layers[i + 1].ci_pad, relu_y=relu_after[i])
+            else:
+                y = kernels.conv_dequant(q, L.relu, L.scale(dev), sx, b, x.dtype)
+            done += 1
+    except Exception as e:
+        _failed(layers[done], e)
+        return None
+    n = x.shape[0]
+    for L in layers:
+        _account("gpu", t0, n, L)
+        t0 = time.perf_counter()
+    return y

@@ -101,6 +101,7 @@ def _declare(L):
         "xdna_conv_weight_pack": ([p, i, i64, i64, p, i64, p, p], i),
         "xdna_conv3x3_i8": ([p, i64, i64, i64, i64, p, i64, i, i, p, p, p], i),
         "xdna_conv_dequant": ([p, i, i64, i64, i64, i64, p, p, p, p, i, p], i),
+        "xdna_conv_requant_next": ([p, i, i, i, i64, i64, i64, i64, p, p, p, i, p, i64, p, p, p], i),
         "xdna_nchw_to_nhwc_i8": ([p, i64, i64, i64, i64, p, i64, p], i),
         "xdna_nhwc_to_nchw_i8": ([p, i64, i64, i64, i64, p, p], i),
     }
@@ -111,7 +112,7 @@ def _declare(L):
 
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
            "xdna_gemm_i8_dequant", "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc", "xdna_conv_weight_pack",
-           "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_nchw_to_nhwc_i8", "xdna_nhwc_to_nchw_i8")
+           "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8", "xdna_nhwc_to_nchw_i8")
 
 
 def _check(status, what):
@@ -290,6 +291,9 @@ def mm_bf16(a, w, bias, out_dtype):
     return y
 
 
+AMAX_WS_PER_IMAGE = 256        # XDNA_AMAX_WS_PER_IMAGE: scratch floats per image of the per-image max
+
+
 def conv_quant(x, c_pad):
     """Per-image int8 of an NCHW float x -> (xq NHWC [N, H, W, c_pad] int8, sx float32 [N])."""
     dev = _need_gpu(x)
@@ -297,7 +301,7 @@ def conv_quant(x, c_pad):
     n, c, h, w = x.shape
     xq = torch.empty((n, h, w, c_pad), dtype=torch.int8, device=dev)
     sx = torch.empty((n,), dtype=torch.float32, device=dev)
-    ws = torch.empty((n,), dtype=torch.float32, device=dev)
+    ws = torch.empty((n, AMAX_WS_PER_IMAGE), dtype=torch.float32, device=dev)
     if n:
         with _on(dev):
             _check(lib().xdna_conv_quant_nhwc(_ptr(x), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(xq), c_pad, _ptr(sx),
@@ -356,6 +360,24 @@ def conv_dequant(q, relu, scale, sx, bias, out_dtype):
             _check(lib().xdna_conv_dequant(_ptr(q), int(bool(relu)), n, h, w, co, _ptr(scale), _ptr(sx), _ptr(bias),
                                            _ptr(y), _DTYPE_CODE[out_dtype], _stream(dev)), "conv_dequant")
     return y
+
+
+def conv_requant_next(q, relu, pool, scale, sx, bias, x_dtype, c_pad_next, relu_y=False):
+    """Conv chaining: NHWC q [N, H, W, Co] of one conv -> (NHWC int8 [N, H', W', c_pad_next], sx [N])
+    for the next, equal to dequantize (cast to x_dtype) -> [ReLU if relu_y] -> [2x2 max-pool] ->
+    per-image quantize."""
+    dev = _need_gpu(q, scale, sx, bias)
+    n, h, w, co = q.shape
+    ho, wo = (h // 2, w // 2) if pool else (h, w)
+    xq = torch.empty((n, ho, wo, c_pad_next), dtype=torch.int8, device=dev)
+    sxn = torch.empty((n,), dtype=torch.float32, device=dev)
+    ws = torch.empty((n, AMAX_WS_PER_IMAGE), dtype=torch.float32, device=dev)
+    if n:
+        with _on(dev):
+            _check(lib().xdna_conv_requant_next(_ptr(q), int(bool(relu)), int(bool(relu_y)), int(bool(pool)), n, h, w,
+                                                co, _ptr(scale), _ptr(sx), _ptr(bias), _DTYPE_CODE[x_dtype], _ptr(xq),
+                                                c_pad_next, _ptr(sxn), _ptr(ws), _stream(dev)), "conv_requant_next")
+    return xq, sxn
 
 
 def nchw_to_nhwc(xq, c_pad):

@@ -90,3 +90,24 @@ def conv3x3_fused(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Te
 @conv3x3_fused.register_fake
 def _(x, weight, bias, relu, cfg_id):
     return x.new_empty((x.shape[0], weight.shape[0], x.shape[2], x.shape[3]))
+
+
+@torch.library.custom_op("xdna::conv3x3_chain", mutates_args=())
+def conv3x3_chain(x: torch.Tensor, weights: list[torch.Tensor], biases: list[Optional[torch.Tensor]],
+                  relus: list[bool], relu_after: list[bool], pools: list[bool], cfg_id: int) -> torch.Tensor:
+    """Consecutive conv3x3_int8 layers as one op: layer i's output, through a ReLU when relu_after[i]
+    and a 2x2 max-pool when pools[i], feeds layer i + 1. On the GPU the activation stays NHWC int8
+    between the convs, with the same integers as the unfused layers (results/conv3x3_cascade.md:216-222
+    in the reference). relus[i] is conv3x3_int8's fused ReLU; relu_after[i] is a graph ReLU after a
+    biased conv."""
+    return conv.conv3x3_chain(_configs[cfg_id], cfg_id, x, list(weights), list(biases), list(relus),
+                              list(relu_after), list(pools))
+
+
+@conv3x3_chain.register_fake
+def _(x, weights, biases, relus, relu_after, pools, cfg_id):
+    h, w = x.shape[2], x.shape[3]
+    for p in pools[:-1]:
+        if p:
+            h, w = h // 2, w // 2
+    return x.new_empty((x.shape[0], weights[-1].shape[0], h, w))
