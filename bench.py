@@ -210,6 +210,7 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     kernels.lib()   # fails loudly if the HIP library is not built
+    kernels.use_tuned(True)     # the shipped tile table, as Config.tuned_tilings (default) applies it
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     res = {"metric": "W8A8 GEMM & int8 conv3x3 TOPS on 1 MI355X; % of int8 MFMA peak / HBM BW",

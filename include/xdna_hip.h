@@ -44,6 +44,26 @@ extern "C" {
 #define XDNA_EUNSUPPORTED (-2)
 #define XDNA_ENODEV (-3)
 
+/* GEMM / conv kinds of the tile table (xdna_tile_set). */
+#define XDNA_KIND_I8 0   /* xdna_gemm_i8_i32 / xdna_gemm_i8_dequant: (m, n, k) as passed */
+#define XDNA_KIND_BF16 1 /* xdna_gemm_bf16: (m, n, k) as passed (k in bf16 elements) */
+#define XDNA_KIND_CONV 2 /* xdna_conv3x3_i8: m = nb * h * w, n = co, k = 9 * c_pad */
+
+/* Tile ids: the tile engine's workgroup tiles (rows x columns of the output, waves), then the
+ * small-M (weight-streaming) kernel by waves per workgroup. */
+#define XDNA_TILE_AUTO 0
+#define XDNA_TILE_256x256W8 1
+#define XDNA_TILE_256x256W4 2
+#define XDNA_TILE_256x128 3
+#define XDNA_TILE_128x256 4
+#define XDNA_TILE_128x128 5
+#define XDNA_TILE_64x64 6
+#define XDNA_TILE_SMALL_W1 7
+#define XDNA_TILE_SMALL_W2 8
+#define XDNA_TILE_SMALL_W4 9
+#define XDNA_TILE_SMALL_W8 10
+#define XDNA_TILE_SMALL_W16 11
+
 /* Library version (XDNA_ABI_VERSION). Replaces the import probe of kernels.available()
  * (torch_xdna/kernels.py:43-56): a loader checks it before trusting the other symbols. */
 int xdna_abi_version(void);
@@ -55,6 +75,17 @@ const char* xdna_last_error(void);
 /* Number of compute units and the gfx architecture of the current device, for launch shaping
  * and for reports (replaces kernels.unavailable_reason(), torch_xdna/kernels.py:59-60). */
 int xdna_device_info(int* num_cus, int* gfx_major, int* gfx_minor);
+
+/* Per-shape tile table (replaces the reference's tuned NPU tilings: kernels.tuned_table /
+ * tiling_for, torch_xdna/kernels.py:123-149, filled from tools/sweep.py). xdna_tile_set makes
+ * every later launch of exactly (kind, m, n, k) use `tile` (XDNA_TILE_AUTO removes the entry);
+ * any tile computes the same results, only the speed differs. The table is process-wide and
+ * thread-safe. xdna_tile_get returns the tile the next such launch uses (the table's, else the
+ * built-in rule's, which needs the current device) or a negative status; xdna_tile_clear empties
+ * the table. */
+int xdna_tile_set(int kind, int64_t m, int64_t n, int64_t k, int tile);
+int xdna_tile_get(int kind, int64_t m, int64_t n, int64_t k);
+int xdna_tile_clear(void);
 
 /* Per-row symmetric int8 quantization of activations or weights:
  *   s[r] = max(amax_k |x[r,k]|, 1e-8f) / 127  (IEEE float32 division),

@@ -135,6 +135,7 @@ def install(monkeypatch):
     monkeypatch.setitem(kernels._state, "ok", True)       # mark_broken() can still retire it
     monkeypatch.setitem(kernels._state, "error", None)
     monkeypatch.setattr(kernels, "gpu_device", lambda t: torch.device("cpu"))
-    monkeypatch.setattr(kernels, "gemm_variant", lambda dev, M, N, K: "fake")
+    monkeypatch.setattr(kernels, "gemm_variant", lambda dev, M, N, K, kind=0: "fake")
+    monkeypatch.setattr(kernels, "use_tuned", lambda on: None)
     for name in LAUNCHERS:
         monkeypatch.setattr(kernels, name, getattr(me, name))

@@ -304,14 +304,32 @@ def test_graph_replay(gpu):
 
 
 # ------------------------------------------------------------------------------ every tile shape
-@pytest.mark.parametrize("tile", ["256x256w8", "256x256", "256x128", "128x256", "128x128", "64x64"])
-def test_tiles_forced(gpu, tile, monkeypatch):
-    """Each tile configuration of the engine, forced through XDNA_GEMM_TILE (read per call): int32
-    and fused bf16 GEMMs with partial tiles and K both a multiple of 64 and not, and the conv with
-    both A loaders (C_pad % 64 == 0 and not), against the oracle."""
+@pytest.fixture
+def tile_table():
+    """The library's tile table, emptied before and after the test."""
     from torch_xdna import kernels
 
-    monkeypatch.setenv("XDNA_GEMM_TILE", tile)
+    kernels.use_tuned(False)
+    kernels.tile_clear()
+    yield kernels
+    kernels.tile_clear()
+    kernels._tuned_applied = None
+
+
+@pytest.mark.parametrize("tile", ["t256x256w8", "t256x256w4", "t256x128", "t128x256", "t128x128", "t64x64"])
+def test_tiles_forced(gpu, tile, tile_table):
+    """Each tile configuration of the engine, forced through the library's tile table: int32 and
+    fused bf16 GEMMs with partial tiles and K both a multiple of 64 and not, and the conv with both
+    A loaders (C_pad % 64 == 0 and not), against the oracle."""
+    from torch_xdna import kernels
+
+    for m, n, k in [(700, 1000, 4160), (333, 520, 208), (700, 1000, 2080), (333, 520, 104)]:
+        kernels.tile_set("i8", m, n, k, tile)
+        kernels.tile_set("bf16", m, n, k, tile)
+        assert kernels.tile_get(gpu, "i8", m, n, k) == tile
+    for n, ci, co, h, w_ in [(2, 64, 96, 16, 20), (1, 48, 40, 13, 37)]:
+        kernels.tile_set("conv", n * h * w_, co, 9 * -(-ci // 16) * 16, tile)
+        assert kernels.tile_get(gpu, "conv", n * h * w_, co, 9 * -(-ci // 16) * 16) == tile
     for m, n, k in [(700, 1000, 4160), (333, 520, 208)]:
         a, w = _i8((m, k), seed=m + k), _i8((n, k), seed=n + k)
         acc = c_oracle.gemm_i32(a.numpy(), w.numpy())
@@ -336,3 +354,63 @@ def test_tiles_forced(gpu, tile, monkeypatch):
         acc = c_oracle.conv3x3_acc(xq.numpy(), wq.numpy())
         q = kernels.conv3x3(x_nhwc, packed.to(gpu), 9, False)
         assert np.array_equal(_np(q).transpose(0, 3, 1, 2), O.requant(acc, 9, False)), (n, ci, co, h, w_)
+
+
+@pytest.mark.parametrize("tile", ["small_w1", "small_w2", "small_w4", "small_w8", "small_w16", "t64x64", "t128x128"])
+def test_tiles_forced_decode(gpu, tile, tile_table):
+    """Decode-sized and mid-sized GEMMs with a forced tile: the small-M kernel at every width (also
+    above 64 rows) and the tile engine below 64 rows; int32 sums, the fused bf16 dequant and the
+    bf16 GEMM against the oracle. An entry for another shape leaves the rule in place."""
+    from torch_xdna import kernels
+
+    for m, n, k in [(1, 520, 4160), (16, 1000, 208), (100, 264, 1040)]:
+        kernels.tile_set("i8", m, n, k, tile)
+        kernels.tile_set("bf16", m, n, k // 2, tile)
+        a, w = _i8((m, k), seed=m + k), _i8((n, k), seed=n + k)
+        acc = c_oracle.gemm_i32(a.numpy(), w.numpy())
+        assert np.array_equal(_np(kernels.mm_i8(a.to(gpu), w.to(gpu))), acc), (tile, m, n, k)
+        sx, sw = torch.rand(m) + 0.01, torch.rand(n) + 0.01
+        b = torch.randn(n)
+        y = kernels.mm_i8_dequant(a.to(gpu), sx.to(gpu), w.to(gpu), sw.to(gpu), b.to(gpu), torch.bfloat16)
+        assert np.array_equal(_f32(y), O.to_bf16(O.dequant(acc, sx.numpy(), sw.numpy(), b.numpy()))), (tile, m, n, k)
+        x = _rand((m, k // 2), torch.float32, seed=m + k)
+        wf = _rand((n, k // 2), torch.float32, seed=n + k, scale=0.05)
+        yb = kernels.mm_bf16(kernels.bf16_rows(x.to(gpu), k // 2), kernels.bf16_rows(wf.to(gpu), k // 2), None,
+                             torch.float32)
+        want, bound = O.gemm_bf16(x.numpy(), wf.numpy())
+        _bf16_bracket(_f32(yb), want, bound, "f32")
+    assert kernels.tile_get(gpu, "i8", 1, 520, 4160) == tile
+    assert kernels.tile_get(gpu, "i8", 1, 520, 4176).startswith("small_w")     # not in the table: the rule
+    kernels.tile_set("i8", 1, 520, 4160, "auto")
+    assert kernels.tile_get(gpu, "i8", 1, 520, 4160) == "small_w2"
+
+
+def test_sweep_tool(gpu, tile_table, tmp_path):
+    """python -m torch_xdna.sweep on small shapes of each kind: one exact, timed JSONL line per
+    candidate tile; resuming skips finished lines; --summary writes a table the runtime can load."""
+    import json
+
+    from torch_xdna import sweep
+
+    out = str(tmp_path / "sweep.jsonl")
+    sweep.main(["--kind", "i8", "--rows", "16", "300", "--shapes", "520x256", "--out", out])
+    sweep.main(["--kind", "bf16", "--rows", "300", "--shapes", "520x256", "--out", out])
+    sweep.main(["--kind", "conv", "--convs", "2x48x40x13x37", "--out", out])
+    n_lines = sum(1 for _ in open(out))
+    sweep.main(["--kind", "i8", "--rows", "16", "300", "--shapes", "520x256", "--out", out])   # resumed: no-op
+    recs = [json.loads(line) for line in open(out)]
+    assert len(recs) == n_lines == 11 + 6 + 6 + 6
+    assert all(r["status"] == "ok" and r["exact"] and r["gpu_us"] > 0 for r in recs), recs
+    assert {r["checked_against"] for r in recs} == {"cpu"}
+    table_path = str(tmp_path / "tuned.json")
+    sweep.main(["--summary", out, "--table", table_path])
+    doc = json.load(open(table_path))
+    for kind in ("i8", "bf16", "conv"):
+        for key, v in doc.get(kind, {}).items():
+            assert v["tiling"] in kernels_tiles() and v["gpu_us"] < v["rule_us"]
+
+
+def kernels_tiles():
+    from torch_xdna import kernels
+
+    return kernels.TILES

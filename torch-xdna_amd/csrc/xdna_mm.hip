@@ -34,8 +34,11 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <atomic>
+#include <mutex>
 #include <string>
 #include <type_traits>
+#include <unordered_map>
 
 #include "xdna_common.h"
 
@@ -686,31 +689,78 @@ struct TileCfg {
   int bm, bn, waves;
 };
 
+// Tile ids (XDNA_TILE_* in the header): the tile engine's shapes, then the small-M kernel by waves.
+constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128x256 = 4, T_128x128 = 5,
+              T_64x64 = 6, T_SMALL1 = 7, T_SMALL2 = 8, T_SMALL4 = 9, T_SMALL8 = 10, T_SMALL16 = 11, T_COUNT = 12;
 
-// Tile choice, from a back-to-back timed sweep of every tile shape over the BASELINE GEMM and conv
-// shapes on MI355X (t128 / t256: tiles of that size the problem needs):
-//   * 256 x 256 with 8 waves (one workgroup per CU) from 1.5 rounds of such tiles;
-//   * otherwise, once 128 x 128 tiles fill three quarters of the CUs: 128 x 256 (four waves) for deep K
-//     (>= 4096) when there are at least half a round of 256-wide tiles, else 128 x 128 (three
-//     workgroups per CU);
-//   * 64 x 64 for smaller problems and N <= 64.
-TileCfg pick_tile(int64_t M, int64_t N, int64_t K) {
-  // XDNA_GEMM_TILE=<bm>x<bn>[w8] forces a tile shape (tile sweeps); ignored unless it names a built one
-  if (const char* env = std::getenv("XDNA_GEMM_TILE")) {
-    int bm = 0, bn = 0, waves = 4;
-    const int got = std::sscanf(env, "%dx%dw%d", &bm, &bn, &waves);
-    if (got >= 2 && ((bm == 256 && bn == 256 && (waves == 4 || waves == 8)) ||
-                     (waves == 4 && ((bm == 256 && bn == 128) || (bm == 128 && (bn == 256 || bn == 128)) ||
-                                     (bm == 64 && bn == 64)))))
-      return {bm, bn, waves};
+inline bool is_small(int t) { return t >= T_SMALL1 && t <= T_SMALL16; }
+inline int small_waves(int t) { return 1 << (t - T_SMALL1); }
+
+inline TileCfg tile_cfg(int t) {
+  switch (t) {
+    case T_256x256W8: return {256, 256, 8};
+    case T_256x256W4: return {256, 256, 4};
+    case T_256x128: return {256, 128, 4};
+    case T_128x256: return {128, 256, 4};
+    case T_128x128: return {128, 128, 4};
+    default: return {64, 64, 4};
   }
+}
+
+// Per-shape tile choices registered by the host (a tuned table, or a sweep forcing each tile in
+// turn), keyed by (kind, m, n, k) in the caller's units; consulted before the rule below.
+struct TileKey {
+  int kind;
+  int64_t m, n, k;
+  bool operator==(const TileKey& o) const { return kind == o.kind && m == o.m && n == o.n && k == o.k; }
+};
+struct TileKeyHash {
+  size_t operator()(const TileKey& t) const {
+    uint64_t h = (uint64_t)t.kind * 0x9E3779B97F4A7C15ull;
+    h ^= (uint64_t)t.m + 0x9E3779B97F4A7C15ull + (h << 6) + (h >> 2);
+    h ^= (uint64_t)t.n + 0x9E3779B97F4A7C15ull + (h << 6) + (h >> 2);
+    h ^= (uint64_t)t.k + 0x9E3779B97F4A7C15ull + (h << 6) + (h >> 2);
+    return (size_t)h;
+  }
+};
+std::mutex g_tile_mu;
+std::unordered_map<TileKey, int, TileKeyHash> g_tiles;
+std::atomic<int> g_tile_count{0};
+
+int tile_lookup(int kind, int64_t m, int64_t n, int64_t k) {
+  if (g_tile_count.load(std::memory_order_acquire) == 0) return T_AUTO;
+  std::lock_guard<std::mutex> lock(g_tile_mu);
+  const auto it = g_tiles.find(TileKey{kind, m, n, k});
+  return it == g_tiles.end() ? T_AUTO : it->second;
+}
+
+// The built-in rule, from back-to-back timed sweeps of every tile shape over the BASELINE GEMM and
+// conv shapes on MI355X (t128 / t256: tiles of that size the problem needs; kbytes: K in bytes):
+//   * M <= 64 (decode): the small-M kernel, 2 waves per workgroup, 4 once K exceeds 8 KB;
+//   * 64 x 64 for N <= 64; for N <= 128 no 256-wide tile (half of it would be idle);
+//   * 256 x 256 with 8 waves (one workgroup per CU) from 1.5 rounds of such tiles, or from three
+//     quarters of a round for deep K (>= 4096 bytes), where its lower LDS traffic per MAC outweighs
+//     the idle CUs;
+//   * otherwise, once 128 x 128 tiles fill three quarters of the CUs: 128 x 256 (four waves) for deep K
+//     when there are at least half a round of 256-wide tiles, else 128 x 128 (three workgroups per CU);
+//   * 64 x 64 for smaller problems.
+// A shape the tuned table lists uses the table's tile instead.
+int rule_tile(int64_t M, int64_t N, int64_t kbytes, bool small_ok) {
+  if (small_ok && M <= 64) return (kbytes + 63) / 64 > 128 ? T_SMALL4 : T_SMALL2;
   const int64_t cus = device_cus();
-  if (M <= 64 || N <= 64) return {64, 64, 4};
+  if (M <= 64 || N <= 64) return T_64x64;
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-  if (2 * t256 >= 3 * cus) return {256, 256, 8};
-  if (4 * t128 >= 3 * cus) return (K >= 4096 && 2 * t256 >= cus) ? TileCfg{128, 256, 4} : TileCfg{128, 128, 4};
-  return {64, 64, 4};
+  const bool deep = kbytes >= 4096;
+  if (N > 128 && (2 * t256 >= 3 * cus || (deep && 4 * t256 >= 3 * cus))) return T_256x256W8;
+  if (4 * t128 >= 3 * cus) return (N > 128 && deep && 2 * t256 >= cus) ? T_128x256 : T_128x128;
+  return T_64x64;
+}
+
+// kind / (m, n, k): the table key; kbytes: K as the engine counts it (bytes of an operand row).
+int choose_tile(int kind, int64_t m, int64_t n, int64_t k, int64_t kbytes) {
+  const int t = tile_lookup(kind, m, n, k);
+  return t != T_AUTO ? t : rule_tile(m, n, kbytes, kind != XDNA_KIND_CONV);
 }
 
 // Buffer resources address at most 2 GB; larger operands are processed in row chunks.
@@ -718,8 +768,8 @@ constexpr int64_t MAX_BUF = 0x40000000;   // 1 GB per resource
 
 template <int CONVM, int EPI>
 int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
-                 ConvGeom cg, const EpiArgs& e, hipStream_t st) {
-  const TileCfg t = pick_tile(M, N, K);
+                 ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
+  const TileCfg t = tile_cfg(tile);
   const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   if (tiles >= (1ll << 31)) {
     set_error("launch_mm: too many tiles");
@@ -768,19 +818,17 @@ constexpr int out_bytes() {
 
 template <int EPI>
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
-                const EpiArgs& e, hipStream_t st) {
-  if (M <= 64) {
+                const EpiArgs& e, int tile, hipStream_t st) {
+  // the small-M kernel addresses the whole activation with one buffer resource, 16 rows per grid row
+  if (is_small(tile) && (M * lda > MAX_BUF || (M + 15) / 16 >= 65536)) tile = rule_tile(M, N, K, false);
+  if (is_small(tile)) {
     // weight streaming: the waves of a workgroup split K into multiples of 64 bytes; the weight is
     // processed in row chunks that one buffer resource can address. Waves per workgroup, from a
     // measured sweep of 1 / 2 / 4 / 8 / 16 over the decode shapes: long per-wave streams through the
-    // double-buffered loop beat wide workgroups; 2 waves, 4 once K exceeds 8 KB.
+    // double-buffered loop beat wide workgroups (the rule takes 2, or 4 once K exceeds 8 KB).
     constexpr int U = 8;
     const int64_t steps = (K + 63) / 64;
-    int waves = steps > 128 ? 4 : 2;
-    if (const char* env = std::getenv("XDNA_SMALL_WAVES")) {   // sweeps: 1, 2, 4, 8 or 16
-      const int v = std::atoi(env);
-      if (v == 1 || v == 2 || v == 4 || v == 8 || v == 16) waves = v;
-    }
+    const int waves = small_waves(tile);
     const int64_t kper = ((steps + waves - 1) / waves) * 64;
     const int64_t nrows = std::max<int64_t>(16, (MAX_BUF / ldw) / 16 * 16);
     for (int64_t n0 = 0; n0 < N; n0 += nrows) {
@@ -803,7 +851,7 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
     for (int64_t n0 = 0; n0 < N; n0 += nrows) {
       const int64_t mc = std::min(mrows, M - m0), nc = std::min(nrows, N - n0);
       int rc = launch_tiles<0, EPI>(a + m0 * lda, lda, w + n0 * ldw, ldw, mc, nc, K, ConvGeom{},
-                                    shift_epi(e, out_bytes<EPI>(), m0, n0), st);
+                                    shift_epi(e, out_bytes<EPI>(), m0, n0), tile, st);
       if (rc) return rc;
     }
   }
@@ -820,13 +868,14 @@ int launch_conv(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad
     return XDNA_EUNSUPPORTED;
   }
   const int64_t K = 9 * c_pad;
+  const int tile = choose_tile(XDNA_KIND_CONV, nb * h * w, co, K, K);
   ConvGeom cg{h, w, c_pad};
   for (int64_t b0 = 0; b0 < nb; b0 += imgs) {
     const int64_t bc = std::min(imgs, nb - b0);
     const EpiArgs eb = shift_epi(e, 1, b0 * h * w, 0);
     const int8_t* xb = x + b0 * per_img;
-    int rc = (c_pad % 64 == 0) ? launch_tiles<1, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, st)
-                                : launch_tiles<2, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, st);
+    int rc = (c_pad % 64 == 0) ? launch_tiles<1, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st)
+                                : launch_tiles<2, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st);
     if (rc) return rc;
   }
   return XDNA_OK;
@@ -851,7 +900,8 @@ int xdna_gemm_i8_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
   e.out = c;
   e.ldo = ldc;
   e.vec_ok = (ldc % 8 == 0) && aligned(c, 16);
-  return launch_gemm<EPI_I32>(a, lda, w, ldw, m, n, k, e, as_stream(stream));
+  const int tile = choose_tile(XDNA_KIND_I8, m, n, k, k);
+  return launch_gemm<EPI_I32>(a, lda, w, ldw, m, n, k, e, tile, as_stream(stream));
 }
 
 int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const int8_t* w, int64_t ldw, const float* sw,
@@ -871,9 +921,10 @@ int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const in
   e.bias = bias;
   e.vec_ok = (ldy % 8 == 0) && aligned(y, 16);
   hipStream_t st = as_stream(stream);
-  if (y_dtype == XDNA_F32) return launch_gemm<EPI_DQ_F32>(a, lda, w, ldw, m, n, k, e, st);
-  if (y_dtype == XDNA_BF16) return launch_gemm<EPI_DQ_BF16>(a, lda, w, ldw, m, n, k, e, st);
-  return launch_gemm<EPI_DQ_F16>(a, lda, w, ldw, m, n, k, e, st);
+  const int tile = choose_tile(XDNA_KIND_I8, m, n, k, k);
+  if (y_dtype == XDNA_F32) return launch_gemm<EPI_DQ_F32>(a, lda, w, ldw, m, n, k, e, tile, st);
+  if (y_dtype == XDNA_BF16) return launch_gemm<EPI_DQ_BF16>(a, lda, w, ldw, m, n, k, e, tile, st);
+  return launch_gemm<EPI_DQ_F16>(a, lda, w, ldw, m, n, k, e, tile, st);
 }
 
 int xdna_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const float* bias, void* y, int y_dtype,
@@ -893,9 +944,10 @@ int xdna_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const
   const int8_t* ab = static_cast<const int8_t*>(a);
   const int8_t* wb = static_cast<const int8_t*>(w);
   hipStream_t st = as_stream(stream);
-  if (y_dtype == XDNA_F32) return launch_gemm<EPI_BF_F32>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, st);
-  if (y_dtype == XDNA_BF16) return launch_gemm<EPI_BF_BF16>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, st);
-  return launch_gemm<EPI_BF_F16>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, st);
+  const int tile = choose_tile(XDNA_KIND_BF16, m, n, k, 2 * k);
+  if (y_dtype == XDNA_F32) return launch_gemm<EPI_BF_F32>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, tile, st);
+  if (y_dtype == XDNA_BF16) return launch_gemm<EPI_BF_BF16>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, tile, st);
+  return launch_gemm<EPI_BF_F16>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, tile, st);
 }
 
 int xdna_conv3x3_i8(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad, const int8_t* wq, int64_t co,
@@ -919,6 +971,32 @@ int xdna_conv3x3_i8(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c
   e.shift = shift;
   e.vec_ok = (co % 8 == 0) && aligned(y, 16);
   return launch_conv<EPI_REQUANT>(x, nb, h, w, c_pad, wq, co, e, st);
+}
+
+int xdna_tile_set(int kind, int64_t m, int64_t n, int64_t k, int tile) {
+  XDNA_REQUIRE(kind == XDNA_KIND_I8 || kind == XDNA_KIND_BF16 || kind == XDNA_KIND_CONV, "unknown kind");
+  XDNA_REQUIRE(m >= 1 && n >= 1 && k >= 1, "bad sizes");
+  XDNA_REQUIRE(tile >= T_AUTO && tile < T_COUNT, "unknown tile id");
+  XDNA_REQUIRE(!(kind == XDNA_KIND_CONV && is_small(tile)), "the small-M kernel does not run convs");
+  std::lock_guard<std::mutex> lock(g_tile_mu);
+  const TileKey key{kind, m, n, k};
+  if (tile == T_AUTO) g_tiles.erase(key);
+  else g_tiles[key] = tile;
+  g_tile_count.store((int)g_tiles.size(), std::memory_order_release);
+  return XDNA_OK;
+}
+
+int xdna_tile_get(int kind, int64_t m, int64_t n, int64_t k) {
+  XDNA_REQUIRE(kind == XDNA_KIND_I8 || kind == XDNA_KIND_BF16 || kind == XDNA_KIND_CONV, "unknown kind");
+  XDNA_REQUIRE(m >= 1 && n >= 1 && k >= 1, "bad sizes");
+  return choose_tile(kind, m, n, k, kind == XDNA_KIND_BF16 ? 2 * k : k);
+}
+
+int xdna_tile_clear(void) {
+  std::lock_guard<std::mutex> lock(g_tile_mu);
+  g_tiles.clear();
+  g_tile_count.store(0, std::memory_order_release);
+  return XDNA_OK;
 }
 
 }  // extern "C"

@@ -8,7 +8,8 @@ alias of "gpu".
 Fields whose meaning was specific to the NPU are accepted and keep their validation:
   row_buckets    the GPU kernels take any row count without padding; buckets only name the row
                  group in autotune keys (as in the reference's `_choose`).
-  tuned_tilings  the GPU picks its tile per shape itself; accepted, no effect.
+  tuned_tilings  per-shape tile choices from the shipped MI355X sweep table (torch_xdna/tuned/), or
+                 TORCH_XDNA_TUNED; off: the library's built-in tile rule.
   stacks         the fused Qwen3 stack op is not part of this build; accepted, no effect.
 """
 

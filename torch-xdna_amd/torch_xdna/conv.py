@@ -168,7 +168,10 @@ def _gpu_route(cfg, layer, on_gpu):
         return False
     if on_gpu:
         _require_lib()
-    return kernels.available()
+    if not kernels.available():
+        return False
+    kernels.use_tuned(cfg.tuned_tilings)
+    return True
 
 
 def _first_call(cfg, layer, run_gpu, run_cpu, on_gpu):

@@ -104,6 +104,9 @@ def _declare(L):
         "xdna_conv_requant_next": ([p, i, i, i, i64, i64, i64, i64, p, p, p, i, p, i64, p, p, p], i),
         "xdna_nchw_to_nhwc_i8": ([p, i64, i64, i64, i64, p, i64, p], i),
         "xdna_nhwc_to_nchw_i8": ([p, i64, i64, i64, i64, p, p], i),
+        "xdna_tile_set": ([i, i64, i64, i64, i], i),
+        "xdna_tile_get": ([i, i64, i64, i64], i),
+        "xdna_tile_clear": ([], i),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -112,7 +115,8 @@ def _declare(L):
 
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
            "xdna_gemm_i8_dequant", "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc", "xdna_conv_weight_pack",
-           "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8", "xdna_nhwc_to_nchw_i8")
+           "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8", "xdna_nhwc_to_nchw_i8",
+           "xdna_tile_set", "xdna_tile_get", "xdna_tile_clear")
 
 
 def _check(status, what):
@@ -167,21 +171,87 @@ def num_cus(dev) -> int:
     return _cus[idx]
 
 
-def gemm_variant(dev, M, N, K) -> str:
-    """Which GEMM kernel the library runs for M x N x K (mirrors the library's pick_tile): one
-    NPU-program key of the reference (runtime.py:207) corresponds to one (variant, N, K) here."""
-    if M <= 64:
-        return "small"
-    cus = num_cus(dev)
-    if N <= 64:
-        return "t64x64"
-    t256 = -(-M // 256) * -(-N // 256)
-    t128 = -(-M // 128) * -(-N // 128)
-    if 2 * t256 >= 3 * cus:
-        return "t256x256w8"
-    if 4 * t128 >= 3 * cus:
-        return "t128x256" if K >= 4096 and 2 * t256 >= cus else "t128x128"
-    return "t64x64"
+# ------------------------------------------------------------------------------ tiles
+KIND_I8, KIND_BF16, KIND_CONV = 0, 1, 2          # XDNA_KIND_*
+KINDS = {"i8": KIND_I8, "bf16": KIND_BF16, "conv": KIND_CONV}
+# XDNA_TILE_* by id: the tile engine's workgroup tiles, then the small-M kernel by waves
+TILES = ("auto", "t256x256w8", "t256x256w4", "t256x128", "t128x256", "t128x128", "t64x64",
+         "small_w1", "small_w2", "small_w4", "small_w8", "small_w16")
+TILE_ID = {name: i for i, name in enumerate(TILES)}
+
+
+def tile_set(kind, M, N, K, tile):
+    """Make every later launch of exactly (kind, M, N, K) use `tile` (a TILES name; "auto" removes the
+    entry). For convs M = n*h*w, N = Co, K = 9*Ci_pad. Results do not depend on the tile."""
+    _check(lib().xdna_tile_set(KINDS.get(kind, kind), M, N, K, TILE_ID[tile]), "tile_set")
+
+
+def tile_get(dev, kind, M, N, K) -> str:
+    """The tile the next launch of (kind, M, N, K) on dev uses: the table's entry, else the library's
+    built-in rule."""
+    with _on(dev):
+        t = lib().xdna_tile_get(KINDS.get(kind, kind), M, N, K)
+    if t < 0:
+        _check(t, "tile_get")
+    return TILES[t]
+
+
+def tile_clear():
+    _check(lib().xdna_tile_clear(), "tile_clear")
+
+
+def gemm_variant(dev, M, N, K, kind=KIND_I8) -> str:
+    """Which GEMM kernel runs for M x N x K (the library's choice): one NPU-program key of the
+    reference (runtime.py:207) corresponds to one (variant, N, K) here."""
+    return tile_get(dev, kind, M, N, K)
+
+
+TUNED_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tuned", "mi355x.json")
+_tuned = None
+_tuned_applied = None
+
+
+def tuned_table():
+    """{(kind, M, N, K): tile} from a sweep (python -m torch_xdna.sweep); TORCH_XDNA_TUNED overrides the
+    shipped table (the reference's kernels.tuned_table, torch_xdna/kernels.py:126-141)."""
+    global _tuned
+    with _lock:
+        if _tuned is None:
+            import json
+            import re
+
+            path = os.environ.get("TORCH_XDNA_TUNED") or TUNED_PATH
+            table = {}
+            if os.path.exists(path):
+                with open(path) as f:
+                    doc = json.load(f)
+                for kind in KINDS:
+                    for key, v in doc.get(kind, {}).items():
+                        m = re.fullmatch(r"(\d+)x(\d+)x(\d+)", key)
+                        if m and v.get("tiling") in TILE_ID and v["tiling"] != "auto":
+                            table[(kind,) + tuple(int(x) for x in m.groups())] = v["tiling"]
+            _tuned = table
+        return _tuned
+
+
+def tiling_for(kind, M, N, K):
+    """The swept best tile for this launch when the table has one, else None (the library's rule)."""
+    return tuned_table().get((kind, M, N, K))
+
+
+def use_tuned(on: bool):
+    """Register the tuned table in the library (Config.tuned_tilings) or take it out; a no-op when
+    already in that state."""
+    global _tuned_applied
+    on = bool(on)
+    if _tuned_applied is on:
+        return
+    with _lock:
+        if _tuned_applied is on:
+            return
+        for (kind, M, N, K), tile in tuned_table().items():
+            tile_set(kind, M, N, K, tile if on else "auto")
+        _tuned_applied = on
 
 
 # ------------------------------------------------------------------------------ launchers

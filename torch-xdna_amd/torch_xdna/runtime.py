@@ -256,7 +256,7 @@ def _gpu_bf16(x2d, qw, bias, dtype):
     b = None if bias is None else bias.to(dev, torch.float32).contiguous()
     y = kernels.mm_bf16(xb, wb, b, dtype)
     stats.launches += 1
-    key = ("bf16", kernels.gemm_variant(dev, x2d.shape[0], qw.N, 2 * qw.Kp), qw.N, qw.K, str(dtype))
+    key = ("bf16", kernels.gemm_variant(dev, x2d.shape[0], qw.N, qw.Kp, kernels.KIND_BF16), qw.N, qw.K, str(dtype))
 
     def want():     # the reference's check: the bf16 operands multiplied in float32 (runtime.py:233-234)
         yb = xb[:, :qw.K].cpu().float() @ wb[:, :qw.K].cpu().float().t()
@@ -325,6 +325,8 @@ def _choose(cfg, R, qw, on_gpu, gpu_fn, cpu_fn):
     """'gpu' or 'cpu' for a call of R rows; gpu_fn / cpu_fn run it on either (for autotune)."""
     if cfg.policy == "cpu":
         return "cpu"
+    if kernels.available():
+        kernels.use_tuned(cfg.tuned_tilings)
     if on_gpu:
         _require_lib()
         if not kernels.available() or _key(cfg, R, qw) in _failed:
