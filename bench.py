@@ -64,25 +64,6 @@ def gen(seed):
     return torch.Generator().manual_seed(seed)
 
 
-class Timer:
-    """Per-launch HIP-event timing of one kernel family on torch's current stream."""
-
-    def __init__(self):
-        self.pairs = []
-
-    def __call__(self, fn, *a, **kw):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        out = fn(*a, **kw)
-        e.record()
-        self.pairs.append((s, e))
-        return out
-
-    def ms(self):
-        torch.cuda.synchronize()
-        return [s.elapsed_time(e) for s, e in self.pairs]
-
-
 # ------------------------------------------------------------------------------ GEMM workloads
 def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed=0):
     """Per set: for each (M, N, K): x [M, K], quantized weight [N, K] + sw (+ bias) on the GPU."""
@@ -266,6 +247,22 @@ def gated_timed_steps(a, step, timer, host_ms_per_step):
     return e0.elapsed_time(e1) / 1e3 / a.steps
 
 
+def back_to_back_us(calls, launches):
+    """Microseconds per launch of `launches` calls (cycling through `calls`) queued behind a gate and
+    run back to back between two events (no events between the launches)."""
+    for fn in calls:
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gate(2.0 + 0.05 * launches)
+    e0.record()
+    for i in range(launches):
+        calls[i % len(calls)]()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / launches
+
+
 def per_shape_us(sets, launches=10):
     """Microseconds per launch of each shape's fused GEMM: `launches` back-to-back launches of that
     shape (cycling through the weight sets) behind a gate, between two events."""
@@ -310,6 +307,13 @@ def traffic(workload):
         return None
 
 
+def gemm_kernels(dev, shapes):
+    """The GEMM kernels the shapes launch (the library's tile choice per shape, tuned table applied)."""
+    tiles = sorted({kernels.gemm_variant(dev, M, N, kernels.round_up(K, 16)) for M, N, K in shapes})
+    names = sorted({"mm_small_kernel" if t.startswith("small") else "mm_tile_kernel" for t in tiles})
+    return f"{' + '.join(names)} (EPI_DQ): {', '.join(tiles)}"
+
+
 def roofline_us(ops, nbytes):
     """Lower bound on a launch's duration from the two MI355X ceilings, in microseconds."""
     return max(ops / (PEAK_INT8_TOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) * 1e6
@@ -346,9 +350,7 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
                       "bias": bias, "rotating_sets": len(sets)},
            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic(label.lower()),
-                        "kernel": "mm_tile_kernel (EPI_DQ_BF16/F32)" if min(s[0] for s in shapes) > 64
-                        else "mm_small_kernel (EPI_DQ_BF16)" if max(s[0] for s in shapes) <= 64
-                        else "mm_tile_kernel / mm_small_kernel (EPI_DQ)",
+                        "kernel": gemm_kernels(dev, shapes),
                         "launches": nshape * reps, "avg_launch_us": round(g_sec / (nshape * reps) * 1e6, 2),
                         "alg_bytes_per_launch": round(g_bytes / (nshape * reps)),
                         "hbm_GBs_equiv": round(g_bytes / g_sec / 1e9, 1),
@@ -363,7 +365,8 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
     for j, (M, N, K) in enumerate(shapes):
         t = per_shape[j] / 1e6
         b = gemm_bytes(M, N, K, xb, yb, bias)
-        out["per_shape"].append({"mnk": [M, N, K], "us": round(t * 1e6, 2), "TOPS": round(2 * M * N * K / t / 1e12, 1),
+        out["per_shape"].append({"mnk": [M, N, K], "tile": kernels.gemm_variant(dev, M, N, kernels.round_up(K, 16)),
+                                 "us": round(t * 1e6, 2), "TOPS": round(2 * M * N * K / t / 1e12, 1),
                                  "GBs": round(b / t / 1e9, 1),
                                  "roofline_us": round(roofline_us(2 * M * N * K, b), 2)})
     if not a.no_cpu_baseline:
@@ -460,17 +463,17 @@ def bench_quant(a, dev):
     g = gen(0)
     M, K = 8192, 14336
     xs = [torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev) for _ in range(2)]
-    t = Timer()
-    sec, host = timed_steps(a, lambda i, tm: tm(kernels.quant_rows, xs[i % 2]) if tm else kernels.quant_rows(xs[i % 2]), t)
-    ms = t.ms()
+    # one launch per step, back to back behind the gate: GPU seconds per step = the launch's duration
+    sec, host = timed_steps(a, lambda i, tm: kernels.quant_rows(xs[i % 2]), None)
     b = quant_bytes(M, K, 2)
-    gbs = b / (sum(ms) / len(ms) / 1e3) / 1e9
+    gbs = b / sec / 1e9
     return {"metric": "activation quantize GB/s on 1 MI355X", "unit": "GB/s", "value": round(b / sec / 1e9, 1),
             "ms_per_step": round(sec * 1e3, 4), "host_ms_per_step": round(host * 1e3, 4), "dtype": "bf16->int8",
             "config": {"workload": "quantize bf16 [8192, 14336] per row"},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic("quant"),
-                         "kernel": "quant_rows_vec_kernel", "alg_bytes_per_launch": b}}
+                         "kernel": "quant_rows_stream_kernel", "avg_launch_us": round(sec * 1e6, 2),
+                         "alg_bytes_per_launch": b}}
 
 
 def bench_copy(a, dev):
@@ -479,12 +482,9 @@ def bench_copy(a, dev):
     n = 1 << 28
     src = torch.randint(-2 ** 31, 2 ** 31 - 1, (n,), dtype=torch.int32, device=dev)
     dst = torch.empty_like(src)
-    t = Timer()
-    sec, host = timed_steps(a, lambda i, tm: tm(torch.bitwise_not, src, out=dst) if tm
-                      else torch.bitwise_not(src, out=dst), t)
-    ms = t.ms()
+    sec, host = timed_steps(a, lambda i, tm: torch.bitwise_not(src, out=dst), None)
     b = 2 * n * 4
-    gbs = b / (sum(ms) / len(ms) / 1e3) / 1e9
+    gbs = b / sec / 1e9
     return {"metric": "copy GB/s on 1 MI355X (counter calibration)", "unit": "GB/s",
             "value": round(b / sec / 1e9, 1), "ms_per_step": round(sec * 1e3, 4), "host_ms_per_step": round(host * 1e3, 4),
             "dtype": "int32",
@@ -511,17 +511,16 @@ def bench_c4(a, dev):
         shift = 10
         sets.append((xq, wq, shift))
     torch.cuda.synchronize()
-    t = Timer()
-    sec, host = timed_steps(a, lambda i, tm: (tm or (lambda f, *x: f(*x)))(kernels.conv3x3, *sets[i % 3], True), t)
-    ms = t.ms()
+    # one conv launch per step, back to back behind the gate: GPU seconds per step = its duration
+    sec, host = timed_steps(a, lambda i, tm: kernels.conv3x3(*sets[i % 3], True), None)
     ops = 2 * n * h * w * c * c * 9
-    ach = ops / (sum(ms) / len(ms) / 1e3) / 1e12
+    ach = ops / sec / 1e12
     out = {"value": round(ops / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
            "host_ms_per_step": round(host * 1e3, 4),
            "config": {"workload": "C4 int8 conv3x3 256->256 on 1x256x1536x64, ReLU, NHWC int8 in/out"},
            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic("c4"), "kernel": "mm_tile_kernel (conv)",
-                        "avg_launch_us": round(sum(ms) / len(ms) * 1e3, 2),
+                        "avg_launch_us": round(sec * 1e6, 2),
                         "alg_bytes_per_launch": n * c * h * w * 2 + 9 * c * c + 4 * c}}
     if not a.no_cpu_baseline:
         tops, nrep, best = cpu_baseline_conv(1, 256, 128, 64, 1)
@@ -577,18 +576,24 @@ def bench_c3(a, dev):
     if not torch.equal(step(0), step_parts(0)):
         raise SystemExit("chained and per-layer C3 outputs differ")
     sec_parts, _ = timed_steps(a, step_parts, None)
-    ct = Timer()
-    sec, host = timed_steps(a, step, ct)
-    ms = ct.ms()
+    sec, host = timed_steps(a, step, None)
+    # the dominant kernel alone: the step's four conv launches on their chained inputs, back to back
+    convs, xq, sx = [], *kernels.conv_quant(x, c_pad)
+    for j, ((wq, sw, _), s, sc) in enumerate(zip(layers, shifts, scales)):
+        convs.append(lambda xq=xq, wq=wq, s=s: kernels.conv3x3(xq, wq, s, True))
+        if j < L - 1:
+            xq, sx = kernels.conv_requant_next(kernels.conv3x3(xq, wq, s, True), True, False, sc, sx, None,
+                                               torch.float32, c_pad)
+    conv_us = back_to_back_us(convs, L * a.steps)
     ops = 2 * n * h * w * c * c * 9
-    ach = ops / (sum(ms) / len(ms) / 1e3) / 1e12
+    ach = ops / (conv_us / 1e6) / 1e12
     out = {"value": round(ops * L / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
            "host_ms_per_step": round(host * 1e3, 4), "unchained_ms_per_step": round(sec_parts * 1e3, 4),
            "config": {"workload": "C3 4x (conv3x3 256->256 + ReLU) on 1x256x64x64, chained: quantize once, "
                                   "int8 NHWC requantize between convs, dequantize once"},
            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic("c3"), "kernel": "mm_tile_kernel (conv)",
-                        "avg_launch_us": round(sum(ms) / len(ms) * 1e3, 2)}}
+                        "avg_launch_us": round(conv_us, 2)}}
     if not a.no_cpu_baseline:
         tops, nrep, best = cpu_baseline_conv(n, c, h, w, L)
         out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
