@@ -63,6 +63,8 @@ extern "C" {
 #define XDNA_TILE_SMALL_W4 9
 #define XDNA_TILE_SMALL_W8 10
 #define XDNA_TILE_SMALL_W16 11
+#define XDNA_TILE_192x256 12
+#define XDNA_TILE_256x192 13
 
 /* Library version (XDNA_ABI_VERSION). Replaces the import probe of kernels.available()
  * (torch_xdna/kernels.py:43-56): a loader checks it before trusting the other symbols. */

@@ -10,9 +10,11 @@
 // K is staged through S LDS stages of 64-byte slices by the LDS-DMA form of the raw buffer load:
 // each lane's 16 bytes land at M0 + 16 * lane, so no VGPRs carry the tile, and S - 1 slices are in
 // flight while one is consumed. LDS rows are 64 bytes; the 16-byte chunk c of row r sits at chunk
-// c ^ f(r) with f(r) = ((r >> 1) ^ (r >> 3)) & 3, which keeps the 8- and 16-lane phases of a
-// fragment read on distinct bank groups and depends only on r & 31, so fragment offsets are
-// immediates. Out-of-range rows, K chunks and conv halo pixels are out-of-range buffer loads, which
+// c ^ f(r) with f(r) = (r >> 2) & 3. gfx950's LDS has 64 banks (a 256-byte period) and serves a
+// 64-lane ds_read_b128 in 4 cycles when it is conflict-free; a fragment read (32 rows x 2 chunks)
+// under this f measured 4.0 cycles per instruction and no SQ_LDS_BANK_CONFLICT cycles, where
+// f(r) = ((r >> 1) ^ (r >> 3)) & 3 measured 8 (2-way) and no swizzle 16. f depends only on r & 15,
+// so fragment offsets are immediates. Out-of-range rows, K chunks and conv halo pixels are out-of-range buffer loads, which
 // read 0.
 //
 // Integer sums are exact, so the order in which K is split between lanes, MFMAs or waves does not
@@ -262,11 +264,13 @@ __device__ __forceinline__ void tile_coords(uint32_t pid, uint32_t tiles_m, uint
 }
 
 // LDS rows are 64 bytes (one 64-deep K slice of a tile row); the 16-byte chunk c (0..3) of row r sits
-// at chunk c ^ f(r) with f(r) = ((r >> 1) ^ (r >> 3)) & 3. A fragment read touches 32 consecutive rows
-// at one logical chunk: each 8 of them (LDS serving 8 lanes of 16 bytes per pass) land in 8 distinct
-// 16-byte bank groups of a 128-byte line, and each 16 in 16 distinct groups of a 256-byte line (16
-// lanes per pass). f depends only on r & 31, so fragments 32 rows apart differ by a constant offset.
-__device__ __forceinline__ int swz_f(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+// at chunk c ^ f(r) with f(r) = (r >> 2) & 3. A fragment read touches 32 consecutive rows at logical
+// chunks 2 ks and 2 ks + 1 (lanes 0-31 and 32-63). Under this f every 16 consecutive lanes cover the 16
+// bank groups of a 256-byte line and lanes l, l + 32 never share a 16-byte group within a 4-row block;
+// measured on gfx950 (rocprofv3 SQ_LDS_IDX_ACTIVE / SQ_INSTS_LDS) at 4.0 cycles per ds_read_b128,
+// the conflict-free minimum. f depends only on r & 15, so fragments 32 rows apart differ by a
+// constant offset.
+__device__ __forceinline__ int swz_f(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int swz(int row, int chunk) { return (row << 6) + ((chunk ^ swz_f(row)) << 4); }
 
 // Raw buffer loads: a 16-byte load at a byte offset >= the resource's size returns zeros, which is how
@@ -379,7 +383,7 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
     }
   }
   // Epilogue read-back width: CB 32-column blocks side by side, CW columns per lane (8 lanes per row)
-  constexpr int CB = FN >= 2 ? 2 : 1;
+  constexpr int CB = FN % 2 == 0 ? 2 : 1;
   constexpr int CW = 4 * CB;
   EpiCols<EPI, CW> cols_pre[FN / CB];
 #pragma unroll
@@ -691,7 +695,8 @@ struct TileCfg {
 
 // Tile ids (XDNA_TILE_* in the header): the tile engine's shapes, then the small-M kernel by waves.
 constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128x256 = 4, T_128x128 = 5,
-              T_64x64 = 6, T_SMALL1 = 7, T_SMALL2 = 8, T_SMALL4 = 9, T_SMALL8 = 10, T_SMALL16 = 11, T_COUNT = 12;
+              T_64x64 = 6, T_SMALL1 = 7, T_SMALL2 = 8, T_SMALL4 = 9, T_SMALL8 = 10, T_SMALL16 = 11,
+              T_192x256 = 12, T_256x192 = 13, T_COUNT = 14;
 
 inline bool is_small(int t) { return t >= T_SMALL1 && t <= T_SMALL16; }
 inline int small_waves(int t) { return 1 << (t - T_SMALL1); }
@@ -703,6 +708,8 @@ inline TileCfg tile_cfg(int t) {
     case T_256x128: return {256, 128, 4};
     case T_128x256: return {128, 256, 4};
     case T_128x128: return {128, 128, 4};
+    case T_192x256: return {192, 256, 4};
+    case T_256x192: return {256, 192, 4};
     default: return {64, 64, 4};
   }
 }
@@ -787,6 +794,10 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
     XDNA_TILE_W(256, 256, 2, 4, 3)
   } else if (t.bm == 256 && t.bn == 256) {
     XDNA_TILE(256, 256, 4)
+  } else if (t.bm == 192) {
+    XDNA_TILE(192, 256, 4)
+  } else if (t.bn == 192) {
+    XDNA_TILE(256, 192, 4)
   } else if (t.bm == 256) {
     XDNA_TILE(256, 128, 4)
   } else if (t.bn == 256) {
