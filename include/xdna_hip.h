@@ -65,6 +65,9 @@ extern "C" {
 #define XDNA_TILE_SMALL_W16 11
 #define XDNA_TILE_192x256 12
 #define XDNA_TILE_256x192 13
+#define XDNA_TILE_64x32 14
+#define XDNA_TILE_32x64 15
+#define XDNA_TILE_32x32 16
 
 /* Library version (XDNA_ABI_VERSION). Replaces the import probe of kernels.available()
  * (torch_xdna/kernels.py:43-56): a loader checks it before trusting the other symbols. */

@@ -317,7 +317,7 @@ def tile_table():
 
 
 @pytest.mark.parametrize("tile", ["t256x256w8", "t256x256w4", "t256x128", "t128x256", "t128x128", "t64x64",
-                                  "t192x256", "t256x192"])
+                                  "t192x256", "t256x192", "t64x32", "t32x64", "t32x32"])
 def test_tiles_forced(gpu, tile, tile_table):
     """Each tile configuration of the engine, forced through the library's tile table: int32 and
     fused bf16 GEMMs with partial tiles and K both a multiple of 64 and not, and the conv with both
@@ -400,7 +400,7 @@ def test_sweep_tool(gpu, tile_table, tmp_path):
     n_lines = sum(1 for _ in open(out))
     sweep.main(["--kind", "i8", "--rows", "16", "300", "--shapes", "520x256", "--out", out])   # resumed: no-op
     recs = [json.loads(line) for line in open(out)]
-    assert len(recs) == n_lines == 13 + 8 + 8 + 8
+    assert len(recs) == n_lines == 16 + 11 + 11 + 11
     assert all(r["status"] == "ok" and r["exact"] and r["gpu_us"] > 0 for r in recs), recs
     assert {r["checked_against"] for r in recs} == {"cpu"}
     table_path = str(tmp_path / "tuned.json")

@@ -110,17 +110,12 @@ struct EpiCols {
       if (e.bias) load(e.bias, n, N, b);
     }
   }
+  // One straight-line path: no per-lane branch merges the loaded values, so nothing waits for them
+  // before the epilogue (the tile kernel issues these before its first K slice). Columns past N read
+  // column N - 1; their outputs are never stored.
   __device__ __forceinline__ static void load(const float* p, int64_t n, int64_t N, float (&v)[CW]) {
-    if (n + CW - 1 < N && (reinterpret_cast<uintptr_t>(p + n) & 15) == 0) {
 #pragma unroll
-      for (int q = 0; q < CW / 4; ++q) {
-        const f32x4 t = *reinterpret_cast<const f32x4*>(p + n + 4 * q);
-        v[4 * q] = t[0], v[4 * q + 1] = t[1], v[4 * q + 2] = t[2], v[4 * q + 3] = t[3];
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < CW; ++r) v[r] = n + r < N ? p[n + r] : 0.0f;
-    }
+    for (int r = 0; r < CW; ++r) v[r] = p[min(n + r, N - 1)];
   }
 };
 
@@ -379,7 +374,7 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
 #pragma unroll
     for (int rr = 0; rr < TM / 8; ++rr) {
       const int64_t m = m0 + wm * TM + rr * 8 + (lane >> 3);
-      sx_pre[rr] = m < M ? e.sx[m] : 0.0f;
+      sx_pre[rr] = e.sx[min(m, M - 1)];   // rows past M are never stored
     }
   }
   // Epilogue read-back width: CB 32-column blocks side by side, CW columns per lane (8 lanes per row)
@@ -696,7 +691,7 @@ struct TileCfg {
 // Tile ids (XDNA_TILE_* in the header): the tile engine's shapes, then the small-M kernel by waves.
 constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128x256 = 4, T_128x128 = 5,
               T_64x64 = 6, T_SMALL1 = 7, T_SMALL2 = 8, T_SMALL4 = 9, T_SMALL8 = 10, T_SMALL16 = 11,
-              T_192x256 = 12, T_256x192 = 13, T_COUNT = 14;
+              T_192x256 = 12, T_256x192 = 13, T_64x32 = 14, T_32x64 = 15, T_32x32 = 16, T_COUNT = 17;
 
 inline bool is_small(int t) { return t >= T_SMALL1 && t <= T_SMALL16; }
 inline int small_waves(int t) { return 1 << (t - T_SMALL1); }
@@ -710,6 +705,9 @@ inline TileCfg tile_cfg(int t) {
     case T_128x128: return {128, 128, 4};
     case T_192x256: return {192, 256, 4};
     case T_256x192: return {256, 192, 4};
+    case T_64x32: return {64, 32, 2};
+    case T_32x64: return {32, 64, 2};
+    case T_32x32: return {32, 32, 1};
     default: return {64, 64, 4};
   }
 }
@@ -804,6 +802,12 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
     XDNA_TILE(128, 256, 4)
   } else if (t.bm == 128) {
     XDNA_TILE(128, 128, 3)
+  } else if (t.bn == 32 && t.bm == 64) {
+    XDNA_TILE_W(64, 32, 2, 1, 4)
+  } else if (t.bm == 32 && t.bn == 64) {
+    XDNA_TILE_W(32, 64, 1, 2, 4)
+  } else if (t.bm == 32) {
+    XDNA_TILE_W(32, 32, 1, 1, 4)
   } else {
     XDNA_TILE(64, 64, 4)
   }
