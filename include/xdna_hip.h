@@ -195,6 +195,40 @@ int xdna_nchw_to_nhwc_i8(const int8_t* src, int64_t nb, int64_t ch, int64_t h, i
 int xdna_nhwc_to_nchw_i8(const void* src, int64_t nb, int64_t ch, int64_t h, int64_t w, void* dst,
                          void* stream);
 
+/* ---- xdna::qwen3_stack (replaces Triton-XDNA's tl.extra.npu.qwen3_stack, called from
+ * torch_xdna/stack.py:360-390 `run`). The stack runs on a packed activation of T valid tokens
+ * (all sequences one after another); its GEMMs are xdna_gemm_bf16 calls. Transformers' Qwen3
+ * semantics (modeling_qwen3: Qwen3RMSNorm, Qwen3Attention with q_norm / k_norm and RoPE,
+ * Qwen3MLP). */
+
+/* y[r, :] = bf16(w * (x[r, :] * rsqrt(mean(x[r, :]^2) + eps))), x float32 [rows, d], w [d] of
+ * w_dtype; d a multiple of 256, at most 4096. */
+int xdna_rmsnorm_bf16(const float* x, int64_t rows, int64_t d, const void* w, int w_dtype, float eps, void* y,
+                      void* stream);
+
+/* qkv float32 [T, (nh + 2 nkv) * 128] (q heads, then k heads, then v heads; head_dim 128): q and k
+ * heads RMSNorm'd over the head with q_w / k_w [128], then RoPE at position pos[t]
+ * (theta_j = pos * inv_freq[j], j < 64, rotate_half pairing j with j + 64), written bf16 to
+ * q [T, nh, 128] and k [T, nkv, 128]; v heads written bf16 transposed to vt[kv head][dim][vt_col[t]]
+ * (row stride ld_vt). */
+int xdna_qk_norm_rope(const float* qkv, int64_t T, int nh, int nkv, const void* q_w, const void* k_w, int w_dtype,
+                      const float* inv_freq, const int32_t* pos, const int32_t* vt_col, float eps, void* q, void* k,
+                      void* vt, int64_t ld_vt, void* stream);
+
+/* Bidirectional attention per sequence s (tokens seq_start[s] .. + seq_len[s] of q / k, vt columns
+ * seq_vt[s] .. + round_up(seq_len[s], 32), zero past seq_len[s]) and q head h (kv head
+ * h / (nh / nkv)): out = softmax(q k^T * scale) v, bf16 [T, nh, 128]. max_len >= every seq_len;
+ * ld_vt and seq_vt multiples of 8. */
+int xdna_attention_bf16(const void* q, const void* k, const void* vt, int64_t ld_vt, const int32_t* seq_start,
+                        const int32_t* seq_len, const int32_t* seq_vt, int64_t nseq, int64_t max_len, int nh, int nkv,
+                        float scale, void* out, void* stream);
+
+/* y = bf16(silu(gu[:, :inter]) * gu[:, inter:]), gu float32 [T, 2 inter] (gate, then up). */
+int xdna_silu_mul_bf16(const float* gu, int64_t T, int64_t inter, void* y, void* stream);
+
+/* x += y over n float32 values (residual adds). */
+int xdna_add_f32(float* x, const float* y, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -94,6 +94,35 @@ class VGGStack(torch.nn.Module):
         return torch.relu(self.features(x))
 
 
+class Stack(torch.nn.Module):
+    """A transformers Qwen3Model of Qwen3-0.6B's widths (random init) into a linear head, fed
+    embeddings and a 4-D attention mask (the reference's stack test model, OmniVoice's backbone in
+    miniature)."""
+
+    def __init__(self, layers=2, out=1000, bias=False):
+        super().__init__()
+        from transformers import Qwen3Config, Qwen3Model
+
+        cfg = Qwen3Config(hidden_size=1024, intermediate_size=3072, num_hidden_layers=layers, num_attention_heads=16,
+                          num_key_value_heads=8, head_dim=128, vocab_size=16, rms_norm_eps=1e-6,
+                          rope_parameters={"rope_type": "default", "rope_theta": 1e6}, attn_implementation="sdpa")
+        self.llm = Qwen3Model(cfg)
+        self.head = torch.nn.Linear(1024, out, bias=bias)
+
+    def forward(self, x, mask):
+        return self.head(self.llm(inputs_embeds=x, attention_mask=mask)[0])
+
+
+def prefix_mask(lens, L, device="cpu"):
+    """Sequence b's first n positions see those n; each padding position after them sees itself."""
+    m = torch.zeros(len(lens), 1, L, L, dtype=torch.bool)
+    for b, n in enumerate(lens):
+        m[b, :, :n, :n] = True
+        i = torch.arange(n, L)
+        m[b, :, i, i] = True
+    return m.to(device)
+
+
 def run(net, x, **opts):
     """torch.compile with the xdna backend from a fresh Dynamo cache and fresh stats."""
     from torch_xdna import runtime

@@ -339,3 +339,36 @@ def test_max_pool2_matches_torch():
         y = rng.standard_normal(shape).astype(np.float32)
         want = torch.nn.functional.max_pool2d(torch.from_numpy(y), 2, 2).numpy()
         assert np.array_equal(O.max_pool2(y), want)
+
+
+def test_qwen3_stack_matches_transformers():
+    """oracle.qwen3_stack vs transformers' own Qwen3Model (float64, 2 layers of Qwen3-0.6B's widths,
+    random weights, with a head and bias) under a prefix-block mask: the valid rows agree to float64
+    rounding. Pins RMSNorm placement, q / k norms, RoPE (pairing, sign, angles), grouped-query heads
+    and the SiLU MLP."""
+    from models import Stack, prefix_mask
+    from oracle import qwen3_stack as Q
+
+    torch.manual_seed(5)
+    net = Stack(layers=2, out=96, bias=True).double().eval()
+    with torch.no_grad():                       # non-trivial norm weights
+        for name, p in net.named_parameters():
+            if "norm" in name:
+                p.copy_(1 + 0.1 * torch.randn_like(p))
+    lens, L = [19, 12], 19
+    x = torch.randn(2, L, 1024, dtype=torch.float64)
+    with torch.no_grad():
+        y = net(x, prefix_mask(lens, L))
+    layers, norm, inv_freq = Q.model_weights(net.llm)
+    for b, n in enumerate(lens):
+        want = Q.stack_forward(x[b, :n], layers, norm, net.head.weight, net.head.bias, inv_freq)
+        err = float((y[b, :n] - want).norm() / want.norm())
+        assert err < 1e-10, (b, err)
+    # a plausible mistake fails: RoPE with the rotation's sign flipped
+    bad = Q.rope
+    try:
+        Q.rope = lambda t, f: bad(t, -f)        # noqa: E731
+        wrong = Q.stack_forward(x[0, :lens[0]], layers, norm, net.head.weight, net.head.bias, inv_freq)
+    finally:
+        Q.rope = bad
+    assert float((y[0, :lens[0]] - wrong).norm() / wrong.norm()) > 1e-3

@@ -693,6 +693,9 @@ constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128
               T_64x64 = 6, T_SMALL1 = 7, T_SMALL2 = 8, T_SMALL4 = 9, T_SMALL8 = 10, T_SMALL16 = 11,
               T_192x256 = 12, T_256x192 = 13, T_64x32 = 14, T_32x64 = 15, T_32x32 = 16, T_COUNT = 17;
 
+static_assert(T_SMALL2 == T_SMALL1 + 1 && T_SMALL4 == T_SMALL1 + 2 && T_SMALL8 == T_SMALL1 + 3 &&
+                  T_SMALL16 == T_SMALL1 + 4,
+              "small-M ids count waves as powers of two");
 inline bool is_small(int t) { return t >= T_SMALL1 && t <= T_SMALL16; }
 inline int small_waves(int t) { return 1 << (t - T_SMALL1); }
 

@@ -344,4 +344,11 @@ def _compile(gm, example_inputs, cfg):
 def xdna_backend(gm: torch.fx.GraphModule, example_inputs, options=None, mode=None):
     """The torch.compile backend; `options` are torch_xdna.Config fields."""
     cfg = _config.config.merged(options)
+    if cfg.stacks and cfg.policy != "cpu" and kernels.available():
+        from . import stack
+
+        plan = stack.find(gm, example_inputs)
+        if plan is not None:
+            # the graph twice: the stack as one GPU op, and as usual; a dispatcher picks per call
+            return stack.compile_fused(gm, example_inputs, cfg, ops.config_id(cfg), plan, _compile)
     return _compile(gm, example_inputs, cfg)

@@ -10,7 +10,8 @@ Fields whose meaning was specific to the NPU are accepted and keep their validat
                  group in autotune keys (as in the reference's `_choose`).
   tuned_tilings  per-shape tile choices from the shipped MI355X sweep table (torch_xdna/tuned/), or
                  TORCH_XDNA_TUNED; off: the library's built-in tile rule.
-  stacks         the fused Qwen3 stack op is not part of this build; accepted, no effect.
+  stacks         a Qwen3-0.6B-width transformer stack + linear head on GPU tensors becomes the one op
+                 xdna::qwen3_stack (HIP kernels), dispatched per call by the attention mask.
 """
 
 from dataclasses import dataclass, fields, replace

@@ -107,6 +107,11 @@ def _declare(L):
         "xdna_tile_set": ([i, i64, i64, i64, i], i),
         "xdna_tile_get": ([i, i64, i64, i64], i),
         "xdna_tile_clear": ([], i),
+        "xdna_rmsnorm_bf16": ([p, i64, i64, p, i, ctypes.c_float, p, p], i),
+        "xdna_qk_norm_rope": ([p, i64, i, i, p, p, i, p, p, p, ctypes.c_float, p, p, p, i64, p], i),
+        "xdna_attention_bf16": ([p, p, p, i64, p, p, p, i64, i64, i, i, ctypes.c_float, p, p], i),
+        "xdna_silu_mul_bf16": ([p, i64, i64, p, p], i),
+        "xdna_add_f32": ([p, p, i64, p], i),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -116,7 +121,8 @@ def _declare(L):
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
            "xdna_gemm_i8_dequant", "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc", "xdna_conv_weight_pack",
            "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8", "xdna_nhwc_to_nchw_i8",
-           "xdna_tile_set", "xdna_tile_get", "xdna_tile_clear")
+           "xdna_tile_set", "xdna_tile_get", "xdna_tile_clear", "xdna_rmsnorm_bf16", "xdna_qk_norm_rope",
+           "xdna_attention_bf16", "xdna_silu_mul_bf16", "xdna_add_f32")
 
 
 def _check(status, what):
@@ -473,3 +479,70 @@ def nhwc_to_nchw(q):
         with _on(dev):
             _check(lib().xdna_nhwc_to_nchw_i8(_ptr(q), n, c, h, w, _ptr(out), _stream(dev)), "nhwc_to_nchw")
     return out
+
+
+# ------------------------------------------------------------------------------ qwen3 stack pieces
+def _wcode(t):
+    return _DTYPE_CODE[t.dtype]
+
+
+def rmsnorm_bf16(x, w, eps):
+    """bf16(w * (x * rsqrt(mean(x^2) + eps))) of float32 rows x [R, D] (D a multiple of 256)."""
+    dev = _need_gpu(x, w)
+    R, D = x.shape
+    y = torch.empty((R, D), dtype=torch.bfloat16, device=dev)
+    if R:
+        with _on(dev):
+            _check(lib().xdna_rmsnorm_bf16(_ptr(x), R, D, _ptr(w), _wcode(w), float(eps), _ptr(y), _stream(dev)),
+                   "rmsnorm_bf16")
+    return y
+
+
+def qk_norm_rope(qkv, nh, nkv, q_w, k_w, inv_freq, pos, vt_col, eps, vt):
+    """Per token of qkv float32 [T, (nh + 2 nkv) * 128]: q / k heads RMSNorm'd and rotated (RoPE at
+    pos), v heads written transposed into vt [nkv, 128, ld_vt] at columns vt_col. Returns bf16
+    (q [T, nh, 128], k [T, nkv, 128])."""
+    dev = _need_gpu(qkv, q_w, k_w, inv_freq, pos, vt_col, vt)
+    T = qkv.shape[0]
+    q = torch.empty((T, nh, 128), dtype=torch.bfloat16, device=dev)
+    k = torch.empty((T, nkv, 128), dtype=torch.bfloat16, device=dev)
+    if T:
+        with _on(dev):
+            _check(lib().xdna_qk_norm_rope(_ptr(qkv), T, nh, nkv, _ptr(q_w), _ptr(k_w), _wcode(q_w), _ptr(inv_freq),
+                                           _ptr(pos), _ptr(vt_col), float(eps), _ptr(q), _ptr(k), _ptr(vt),
+                                           vt.shape[-1], _stream(dev)), "qk_norm_rope")
+    return q, k
+
+
+def attention_bf16(q, k, vt, seq_start, seq_len, seq_vt, max_len, scale):
+    """Bidirectional grouped-query attention per sequence: bf16 [T, nh, 128]."""
+    dev = _need_gpu(q, k, vt, seq_start, seq_len, seq_vt)
+    T, nh = q.shape[:2]
+    nkv = k.shape[1]
+    out = torch.empty((T, nh, 128), dtype=torch.bfloat16, device=dev)
+    if T:
+        with _on(dev):
+            _check(lib().xdna_attention_bf16(_ptr(q), _ptr(k), _ptr(vt), vt.shape[-1], _ptr(seq_start), _ptr(seq_len),
+                                             _ptr(seq_vt), seq_len.shape[0], int(max_len), nh, nkv, float(scale),
+                                             _ptr(out), _stream(dev)), "attention_bf16")
+    return out
+
+
+def silu_mul_bf16(gu):
+    """bf16(silu(gate) * up) of gu float32 [T, 2 * inter] (gate columns first)."""
+    dev = _need_gpu(gu)
+    T, two = gu.shape
+    y = torch.empty((T, two // 2), dtype=torch.bfloat16, device=dev)
+    if T:
+        with _on(dev):
+            _check(lib().xdna_silu_mul_bf16(_ptr(gu), T, two // 2, _ptr(y), _stream(dev)), "silu_mul_bf16")
+    return y
+
+
+def add_(x, y):
+    """x += y (float32, same shape, contiguous)."""
+    dev = _need_gpu(x, y)
+    if x.numel():
+        with _on(dev):
+            _check(lib().xdna_add_f32(_ptr(x), _ptr(y), x.numel(), _stream(dev)), "add_f32")
+    return x

@@ -12,7 +12,7 @@ from typing import Optional
 
 import torch
 
-from . import conv, runtime
+from . import conv, runtime, stack
 
 _configs = []  # cfg_id -> Config; the op's arguments must be plain values
 
@@ -111,3 +111,16 @@ def _(x, weights, biases, relus, relu_after, pools, cfg_id):
         if p:
             h, w = h // 2, w // 2
     return x.new_empty((x.shape[0], weights[-1].shape[0], h, w))
+
+
+@torch.library.custom_op("xdna::qwen3_stack", mutates_args=())
+def qwen3_stack(x: torch.Tensor, mask: torch.Tensor, stack_id: int, cfg_id: int) -> torch.Tensor:
+    """A Qwen3 stack found by the backend, and its head, on hidden states x [B, L, 1024] under a
+    prefix-block mask: the head's output [B, L, N], zero on padding rows (ops.py:79-89 in the
+    reference)."""
+    return stack.run(_configs[cfg_id], stack_id, x, mask)
+
+
+@qwen3_stack.register_fake
+def _(x, mask, stack_id, cfg_id):
+    return x.new_empty((x.shape[0], x.shape[1], stack.out_features(stack_id)))
