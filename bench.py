@@ -55,7 +55,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "decode", "quant", "bf16", "vgg16",
-                                                          "copy"])
+                                                          "stack", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -199,7 +199,7 @@ def main():
            "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic (seed 0, randn)"}
     bench = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
              "decode": bench_decode, "quant": bench_quant, "bf16": bench_bf16, "vgg16": bench_vgg16,
-             "copy": bench_copy}[a.workload]
+             "stack": bench_stack, "copy": bench_copy}[a.workload]
     res.update(bench(a, dev))
     print(json.dumps(res), flush=True)
 
@@ -679,6 +679,112 @@ def bench_vgg16(a, dev):
                                "kind": "port", "sample": f"one VGG-16 conv3 layer 256->256 at 1x256x56x56, min of "
                                f"{nrep} reps ({best * 1e3:.1f} ms): torch CPU quantize + fp32 conv2d of the int8 "
                                "values + shift + dequantize"}
+    return out
+
+
+# OmniVoice's backbone step (the reference's results/omnivoice_npu.md:3-12): 28 Qwen3-0.6B layers,
+# the final norm and 8 x 1025 audio heads, cond + uncond sequences; the NPU step (the dispatch alone)
+STACK_SHAPES = {"short": ((58, 43), 12.5), "mid": ((113, 92), 21.7), "long": ((264, 222), 55.3)}
+
+
+def bench_stack(a, dev):
+    """xdna::qwen3_stack on OmniVoice's step shapes: the op alone (GPU time of K steps behind a gate),
+    each shape's output checked against the transformers model run eagerly in float32."""
+    from transformers import Qwen3Config, Qwen3Model
+
+    from torch_xdna import Config, stack
+
+    torch.manual_seed(0)
+    cfg = Qwen3Config(hidden_size=1024, intermediate_size=3072, num_hidden_layers=28, num_attention_heads=16,
+                      num_key_value_heads=8, head_dim=128, vocab_size=16, rms_norm_eps=1e-6,
+                      rope_parameters={"rope_type": "default", "rope_theta": 1e6}, attn_implementation="sdpa")
+    llm = Qwen3Model(cfg).eval().to(dev)
+    head = torch.nn.Linear(1024, 8 * 1025, bias=False).to(dev)
+    weights = {}
+    for i, Lr in enumerate(llm.layers):
+        at, mlp = Lr.self_attn, Lr.mlp
+        for key, t in dict(q=at.q_proj.weight, k=at.k_proj.weight, v=at.v_proj.weight, o=at.o_proj.weight,
+                           gate=mlp.gate_proj.weight, up=mlp.up_proj.weight, down=mlp.down_proj.weight,
+                           input_norm=Lr.input_layernorm.weight, post_norm=Lr.post_attention_layernorm.weight,
+                           q_norm=at.q_norm.weight, k_norm=at.k_norm.weight).items():
+            weights[(i, key)] = t
+    weights.update(norm=llm.norm.weight, head=head.weight, inv_freq=llm.rotary_emb.inv_freq)
+    plan = stack.Plan([], None, None, 1, None, weights, None, 28, 8 * 1025, stack.MAX_TOKENS)
+    sid = stack.register(plan)
+    conf = Config(policy="gpu")
+    per_shape, steps = {}, {}
+    for name, (lens, npu_ms) in STACK_SHAPES.items():
+        L = max(lens)
+        g = gen(1)
+        x = torch.randn(len(lens), L, 1024, generator=g).to(dev)
+        mask = torch.zeros(len(lens), 1, L, L, dtype=torch.bool)
+        for b, n in enumerate(lens):
+            mask[b, :, :n, :n] = True
+            i = torch.arange(n, L)
+            mask[b, :, i, i] = True
+        mask = mask.to(dev)
+        with torch.no_grad():
+            y = stack.run(conf, sid, x, mask)
+            ref = head(llm(inputs_embeds=x, attention_mask=mask)[0])
+        err = max(float((y[b, :n] - ref[b, :n]).float().norm() / ref[b, :n].float().norm()) for b, n in enumerate(lens))
+        if not err < 0.08:
+            raise SystemExit(f"stack {name}: rel err {err:.3g} vs the float32 model")
+        st = stack._stacks[sid]
+
+        def op(i, t, st=st, x=x, mask=mask, lens=lens):
+            st.lens_hint = (mask, list(lens))   # what the dispatcher hands over after parsing the mask
+            return stack.run(conf, sid, x, mask)
+
+        with torch.no_grad():
+            sec, host = timed_steps(a, op, None)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(a.steps):
+                st.lens_hint = None
+                stack.run(conf, sid, x, mask)
+            torch.cuda.synchronize()
+            call = (time.perf_counter() - t0) / a.steps
+        st.lens_hint = None
+        macs = st.macs(list(lens))
+        per_shape[name] = {"tokens": list(lens), "gpu_ms": round(sec * 1e3, 3), "host_ms": round(host * 1e3, 3),
+                           "call_ms_with_mask_parse": round(call * 1e3, 3), "TOPS": round(2 * macs / sec / 1e12, 1),
+                           "reference_npu_step_ms": npu_ms, "rel_err_vs_fp32": round(err, 4),
+                           "hip_graph": stack.USE_GRAPHS}
+        steps[name] = (sec, host, macs)
+    sec, host, macs = steps["long"]
+    ach = 2 * macs / sec / 1e12
+    out = {"metric": "Qwen3 stack step (OmniVoice backbone) TOPS on 1 MI355X", "unit": "TOPS", "value": round(ach, 2),
+           "ms_per_step": round(sec * 1e3, 4), "host_ms_per_step": round(host * 1e3, 4), "dtype": "bf16",
+           "vs_baseline": round(STACK_SHAPES["long"][1] / (sec * 1e3), 2),
+           "baseline": "the reference's NPU step for the long text, 55.3 ms (results/omnivoice_npu.md:12); "
+                       "vs_baseline = that / ms_per_step",
+           "config": {"workload": "xdna::qwen3_stack, 28 Qwen3-0.6B layers + norm + 8x1025 heads, 2 sequences of "
+                                  "264 / 222 tokens (OmniVoice long text)"},
+           "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                        "kernel": "whole op (bf16 GEMMs, attention, norms)"},
+           "per_shape": per_shape}
+    if not a.no_cpu_baseline:
+        llm_c, head_c = llm.to("cpu"), head.to("cpu")
+        lens = STACK_SHAPES["short"][0]
+        L = max(lens)
+        x = torch.randn(len(lens), L, 1024, generator=gen(2))
+        mask = torch.zeros(len(lens), 1, L, L, dtype=torch.bool)
+        for b, n in enumerate(lens):
+            mask[b, :, :n, :n] = True
+            i = torch.arange(n, L)
+            mask[b, :, i, i] = True
+        ts = []
+        with torch.no_grad():
+            for _ in range(3):
+                t = time.perf_counter()
+                head_c(llm_c(inputs_embeds=x, attention_mask=mask)[0])
+                ts.append(time.perf_counter() - t)
+        best = min(ts)
+        out["cpu_baseline"] = {"value": round(2 * stack._stacks[sid].macs(list(lens)) / best / 1e12, 3), "unit": "TOPS",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"the short-text step (58 / 43 tokens) of the same model eagerly in float32 "
+                               f"on the CPU (transformers), min of 3 ({best * 1e3:.0f} ms)"}
     return out
 
 

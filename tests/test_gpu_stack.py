@@ -173,3 +173,39 @@ def test_stack_silent_wrong(gpu, monkeypatch):
     assert len(s["fallbacks"]) == 1 and "disagrees with the model" in s["fallbacks"][0][1], s["fallbacks"]
     assert s["stacks"] == {f"{NAME} on cpu": 2}, s["stacks"]
     assert max(rel_err(y[0], ref[0]), rel_err(y[1, :50], ref[1, :50])) < 0.05
+
+
+def test_stack_graph_replays(gpu, monkeypatch):
+    """The HIP graph of a call shape (captured on its second call) replays with new inputs: every
+    replay equals the eager run of the same inputs bit for bit, with other GPU work and syncs between
+    the replays."""
+    from torch_xdna import Config, stack
+
+    torch.manual_seed(7)
+    net = Stack(layers=2, out=300).eval().to(gpu)
+    weights = {}
+    for i, Lr in enumerate(net.llm.layers):
+        at, mlp = Lr.self_attn, Lr.mlp
+        for key, t in dict(q=at.q_proj.weight, k=at.k_proj.weight, v=at.v_proj.weight, o=at.o_proj.weight,
+                           gate=mlp.gate_proj.weight, up=mlp.up_proj.weight, down=mlp.down_proj.weight,
+                           input_norm=Lr.input_layernorm.weight, post_norm=Lr.post_attention_layernorm.weight,
+                           q_norm=at.q_norm.weight, k_norm=at.k_norm.weight).items():
+            weights[(i, key)] = t
+    weights.update(norm=net.llm.norm.weight, head=net.head.weight, inv_freq=net.llm.rotary_emb.inv_freq)
+    sid = stack.register(stack.Plan([], None, None, 1, None, weights, None, 2, 300, stack.MAX_TOKENS))
+    cfg = Config(policy="gpu")
+    lens, L = [40, 23], 40
+    mask = prefix_mask(lens, L, gpu)
+    xs = [torch.randn(2, L, 1024, device=gpu) for _ in range(4)]
+    with torch.no_grad():
+        monkeypatch.setattr(stack, "USE_GRAPHS", False)
+        want = [stack.run(cfg, sid, x, mask) for x in xs]
+        stack._stacks[sid].shapes.clear()
+        monkeypatch.setattr(stack, "USE_GRAPHS", True)
+        for rep in range(3):
+            for x, w in zip(xs, want):
+                got = stack.run(cfg, sid, x, mask)
+                torch.cuda.synchronize()
+                assert torch.equal(got, w), f"replay {rep} differs from the eager run"
+                _ = (torch.randn(256, 256, device=gpu) @ torch.randn(256, 256, device=gpu)).sum().item()
+    assert stack._stacks[sid].shapes[(tuple(lens), L, torch.float32, xs[0].device)].graph is not None

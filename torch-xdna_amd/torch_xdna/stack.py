@@ -306,6 +306,8 @@ class _Stack:
         self.capture = False    # keep a copy of the next output (for the check)
         self.captured = None
         self._packed = None     # (weakrefs, versions, device, packed weights)
+        self.shapes = {}        # call shape -> _Shape (static buffers, HIP graph)
+        self.lens_hint = None   # (mask, lengths) the dispatcher parsed for the call in flight
 
     def packed(self, dev):
         """The GEMM weights as bf16 [N, K] on dev (q|k|v and gate|up concatenated), the norms and
@@ -399,32 +401,71 @@ def _round_up(n, m):
     return -(-n // m) * m
 
 
-def _forward(pk, layers, x2d, lens):
-    """The stack + head on the packed valid tokens x2d float32 [T, 1024] of sequences of lengths
-    `lens` (one after another): float32 [T, N]."""
-    dev = x2d.device
+class _Shape:
+    """One call shape of a stack (sequence lengths, padded length, dtype, device): static input and
+    output buffers, the attention metadata, and the call captured as a HIP graph. The first run is
+    eager (it also warms the kernels up); the second captures; later calls copy the input in and
+    replay the graph, so a call costs one launch of host work instead of ~11 per layer."""
+
+    def __init__(self, st, pk, lens, L, dtype, dev):
+        self.pk, self.lens, self.dev = pk, list(lens), dev
+        B = len(lens)
+        i32 = dict(dtype=torch.int32)
+        cols = [_round_up(n, QBLOCK) for n in lens]
+        starts = [sum(lens[:b]) for b in range(B)]
+        vts = [sum(cols[:b]) for b in range(B)]
+        self.rows = torch.cat([torch.arange(n) + b * L for b, n in enumerate(lens)]).to(dev)
+        self.pos = torch.cat([torch.arange(n, **i32) for n in lens]).to(dev)
+        self.vt_col = torch.cat([torch.arange(n, **i32) + c for n, c in zip(lens, vts)]).to(dev)
+        meta = torch.tensor([starts, lens, vts], **i32).to(dev)
+        self.seq_start, self.seq_len, self.seq_vt = (meta[r].contiguous() for r in range(3))
+        # columns past a sequence's length stay zero: the attention reads them with zero weight
+        self.vt = torch.zeros((NKV, DH, _round_up(sum(cols), 8)), dtype=torch.bfloat16, device=dev)
+        self.x = torch.zeros((B, L, D), dtype=dtype, device=dev)
+        self.out = torch.zeros((B * L, st.N), dtype=dtype, device=dev)   # padding rows stay zero
+        self.runs, self.graph = 0, None
+
+    def compute(self):
+        """The whole op on self.x into the valid rows of self.out."""
+        B, L = self.x.shape[:2]
+        x2d = self.x.reshape(B * L, D).index_select(0, self.rows).float()
+        y = _forward(self.pk, self, x2d)
+        self.out.index_copy_(0, self.rows, y.to(self.out.dtype))
+
+    def __call__(self, x):
+        self.x.copy_(x)
+        if not USE_GRAPHS or self.runs == 0:
+            self.compute()
+        elif self.graph is None:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.compute()
+            self.graph = g
+            g.replay()
+        else:
+            self.graph.replay()
+        self.runs += 1
+        return self.out.view(*self.x.shape[:2], -1).clone()
+
+
+# Capture each call shape as a HIP graph (TORCH_XDNA_STACK_GRAPHS=0: every call eager).
+USE_GRAPHS = __import__("os").environ.get("TORCH_XDNA_STACK_GRAPHS", "1") != "0"
+MAX_SHAPES = 8                 # call shapes kept per stack (least recently used dropped)
+
+
+def _forward(pk, shape, x2d):
+    """The stack + head on the packed valid tokens x2d float32 [T, 1024] of the shape's sequences
+    (one after another): float32 [T, N]."""
     T = x2d.shape[0]
-    cols = [_round_up(n, QBLOCK) for n in lens]
-    starts, vts, s, v = [], [], 0, 0
-    for n, c in zip(lens, cols):
-        starts.append(s)
-        vts.append(v)
-        s, v = s + n, v + c
-    i32 = dict(dtype=torch.int32)
-    pos = torch.cat([torch.arange(n, **i32) for n in lens])
-    vt_col = torch.cat([torch.arange(n, **i32) + c0 for n, c0 in zip(lens, vts)])
-    meta = torch.tensor([starts, lens, vts], **i32)
-    pos, vt_col, meta = pos.to(dev, non_blocking=False), vt_col.to(dev), meta.to(dev)
-    seq_start, seq_len, seq_vt = meta[0].contiguous(), meta[1].contiguous(), meta[2].contiguous()
-    ld_vt = _round_up(v, 8)
-    vt = torch.zeros((NKV, DH, ld_vt), dtype=torch.bfloat16, device=dev)   # columns past a length stay 0
-    X = x2d
-    max_len = max(lens)
-    for L in layers:
+    X = x2d.contiguous()
+    max_len = max(shape.lens)
+    for L in pk["layers"]:
         h = kernels.rmsnorm_bf16(X, L["input_norm"], EPS)
         qkv = kernels.mm_bf16(h, L["qkv"], None, torch.float32)
-        q, k = kernels.qk_norm_rope(qkv, NH, NKV, L["q_norm"], L["k_norm"], pk["inv_freq"], pos, vt_col, EPS, vt)
-        att = kernels.attention_bf16(q, k, vt, seq_start, seq_len, seq_vt, max_len, DH ** -0.5)
+        q, k = kernels.qk_norm_rope(qkv, NH, NKV, L["q_norm"], L["k_norm"], pk["inv_freq"], shape.pos, shape.vt_col,
+                                    EPS, shape.vt)
+        att = kernels.attention_bf16(q, k, shape.vt, shape.seq_start, shape.seq_len, shape.seq_vt, max_len,
+                                     DH ** -0.5)
         kernels.add_(X, kernels.mm_bf16(att.view(T, NH * DH), L["o"], None, torch.float32))
         h = kernels.rmsnorm_bf16(X, L["post_norm"], EPS)
         act = kernels.silu_mul_bf16(kernels.mm_bf16(h, L["gu"], None, torch.float32))
@@ -437,7 +478,8 @@ def run(cfg, stack_id, x, mask):
     """xdna::qwen3_stack: hidden states x [B, L, 1024] -> the head's output [B, L, N], on the GPU."""
     st = _stacks[stack_id]
     B, L = x.shape[:2]
-    lens = lengths(mask)
+    hint = st.lens_hint
+    lens = hint[1] if hint is not None and hint[0] is mask else lengths(mask)
     if lens is not None and len(lens) == 1 and B > 1:
         lens = lens * B
     if lens is None or len(lens) != B or mask.shape[-1] != L or not all(1 <= n <= st.max_tokens for n in lens):
@@ -448,12 +490,14 @@ def run(cfg, stack_id, x, mask):
     dev = x.device
     with _lock:
         pk = st.packed(dev)
-        rows = torch.cat([torch.arange(n) + b * L for b, n in enumerate(lens)]).to(dev)
-        x2d = x.detach().reshape(B * L, D).index_select(0, rows).float().contiguous()
-        y = _forward(pk, pk["layers"], x2d, lens)
-        out = torch.zeros((B * L, st.N), dtype=x.dtype, device=dev)
-        out.index_copy_(0, rows, y.to(x.dtype))
-        out = out.view(B, L, st.N)
+        key = (tuple(lens), L, x.dtype, dev)
+        shape = st.shapes.pop(key, None)
+        if shape is None or shape.pk is not pk:           # new shape, or weights repacked
+            shape = _Shape(st, pk, lens, L, x.dtype, dev)
+        st.shapes[key] = shape                            # most recently used last
+        while len(st.shapes) > MAX_SHAPES:
+            st.shapes.pop(next(iter(st.shapes)))
+        out = shape(x.detach())
         stats.launches += 1
         if st.capture:
             st.captured = out.float().clone()
@@ -518,6 +562,7 @@ class Dispatch:
             shapes = _groups(lens)
             verify = self.cfg.verify == "always" or (self.cfg.verify == "first" and not shapes <= st.verified)
             st.capture = verify
+            st.lens_hint = (args[self.plan.mask_index], lens)
             try:
                 out = self.fused(*args)
                 if verify:
@@ -527,7 +572,7 @@ class Dispatch:
             except Exception as e:      # launch failure, or a mismatch
                 st.fail(e)
             finally:
-                st.capture, st.captured = False, None
+                st.capture, st.captured, st.lens_hint = False, None, None
         stats.stacks[(st.name, "cpu")] += 1
         return self.plain(*args)
 
