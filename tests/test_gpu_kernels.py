@@ -381,9 +381,44 @@ def test_tiles_forced_decode(gpu, tile, tile_table):
         want, bound = O.gemm_bf16(x.numpy(), wf.numpy())
         _bf16_bracket(_f32(yb), want, bound, "f32")
     assert kernels.tile_get(gpu, "i8", 1, 520, 4160) == tile
-    assert kernels.tile_get(gpu, "i8", 1, 520, 4176).startswith("small_w")     # not in the table: the rule
+    assert kernels.tile_get(gpu, "i8", 1, 520, 4176) == "gemv_w4"      # not in the table: the rule
+    assert kernels.tile_get(gpu, "i8", 16, 520, 4176).startswith("small_w")
     kernels.tile_set("i8", 1, 520, 4160, "auto")
-    assert kernels.tile_get(gpu, "i8", 1, 520, 4160) == "small_w2"
+    assert kernels.tile_get(gpu, "i8", 1, 520, 4160) == "gemv_w4"
+
+
+@pytest.mark.parametrize("tile", ["gemv_w4", "gemv_w2", "gemv_w8"])
+def test_gemv_one_row(gpu, tile, tile_table):
+    """The one-row kernel (M = 1: 16 K segments on the MFMA's 16 columns, the trace summed): int32 sums,
+    the fused dequant to every output dtype with and without bias, and the bf16 GEMM, against the
+    oracle, for K from one 16-byte chunk to more than one 16 KB round and N not a multiple of the
+    waves per workgroup. Forced on more rows, the tile falls back to the rule with the same results."""
+    from torch_xdna import kernels
+
+    for n, k in [(520, 16), (1001, 1040), (264, 4160), (300, 4096), (97, 4112), (130, 16400), (3, 14336)]:
+        for m in (1, 3):
+            kernels.tile_set("i8", m, n, k, tile)
+            kernels.tile_set("bf16", m, n, k // 2 if k >= 32 else 8, tile)
+            a, w = _i8((m, k), seed=m + k + n), _i8((n, k), seed=n + k)
+            acc = c_oracle.gemm_i32(a.numpy(), w.numpy())
+            assert np.array_equal(_np(kernels.mm_i8(a.to(gpu), w.to(gpu))), acc), (tile, m, n, k)
+            sx, sw = torch.rand(m) + 0.01, torch.rand(n) + 0.01
+            b = torch.randn(n)
+            for out in ("f32", "bf16", "f16"):
+                for bias in (b, None):
+                    y = kernels.mm_i8_dequant(a.to(gpu), sx.to(gpu), w.to(gpu), sw.to(gpu),
+                                              None if bias is None else bias.to(gpu), DT[out])
+                    want = O.dequant(acc, sx.numpy(), sw.numpy(), None if bias is None else bias.numpy())
+                    assert np.array_equal(_f32(y), O.to_dtype(want, out)), (tile, m, n, k, out, bias is None)
+            kb = k // 2 if k >= 32 else 8
+            x = _rand((m, kb), torch.float32, seed=m + k)
+            wf = _rand((n, kb), torch.float32, seed=n + k, scale=0.05)
+            bb = _rand((n,), torch.float32, seed=n, scale=0.1)
+            yb = kernels.mm_bf16(kernels.bf16_rows(x.to(gpu), kb), kernels.bf16_rows(wf.to(gpu), kb), bb.to(gpu),
+                                 torch.float32)
+            want, bound = O.gemm_bf16(x.numpy(), wf.numpy(), bb.numpy())
+            _bf16_bracket(_f32(yb), want, bound, "f32")
+    assert kernels.tile_get(gpu, "i8", 1, 264, 4160) == tile
 
 
 def test_sweep_tool(gpu, tile_table, tmp_path):

@@ -30,7 +30,7 @@ def test_shipped_table_is_valid(fresh_table, monkeypatch):
         for key, v in doc.get(kind, {}).items():
             assert v["tiling"] in kernels.TILES and v["tiling"] != v["rule"] and v["gpu_us"] < v["rule_us"], (key, v)
             if kind == "conv":
-                assert not v["tiling"].startswith("small"), key
+                assert not v["tiling"].startswith(("small", "gemv")), key
             n += 1
     table = kernels.tuned_table()
     assert len(table) == n and n > 0
@@ -88,6 +88,8 @@ def test_summary_keeps_clear_wins(tmp_path):
 
 def test_sweep_candidates():
     assert sweep.candidates("i8", 16) == sweep.ENGINE_TILES + sweep.SMALL_TILES
+    assert sweep.candidates("i8", 1) == sweep.ENGINE_TILES + sweep.SMALL_TILES + sweep.GEMV_TILES
+    assert sweep.candidates("bf16", 1) == sweep.candidates("i8", 1)
     assert sweep.candidates("i8", 3000) == sweep.ENGINE_TILES
-    assert sweep.candidates("conv", 16) == sweep.ENGINE_TILES
-    assert set(sweep.ENGINE_TILES + sweep.SMALL_TILES) == set(kernels.TILES) - {"auto"}
+    assert sweep.candidates("conv", 1) == sweep.ENGINE_TILES
+    assert set(sweep.ENGINE_TILES + sweep.SMALL_TILES + sweep.GEMV_TILES) == set(kernels.TILES) - {"auto"}

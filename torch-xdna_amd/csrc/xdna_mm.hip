@@ -31,7 +31,8 @@
 //
 // Small M (decode, M <= 64) uses a separate weight-streaming kernel: each workgroup owns 16 output
 // columns, its waves (2, or 4 for K above 8 KB) split K, each wave keeps a batch of 16-byte weight loads in flight
-// while it runs the MFMAs of the previous batch, and the partial sums meet in LDS.
+// while it runs the MFMAs of the previous batch, and the partial sums meet in LDS. A single row (M = 1)
+// has its own kernel that puts 16 K segments where the 16 rows would go (mm_gemv_kernel).
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -683,6 +684,85 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
   calib_flush<EPI>(e, calib);
 }
 
+// ------------------------------------------------------------------------------ one row (M = 1)
+// GEMV for a single activation row. The 16 columns of the 16x16x64 MFMA carry 16 K segments of the
+// one row instead of 16 rows: in a 1 KB step at byte kb, lane l (A row and B column i = l % 16, k chunk
+// c = l / 16) holds bytes kb + 16 l .. +15 of both the weight row and the activation, so D[i][i] sums
+// exactly the bytes kb + 16 (i + 16 c) + q over c and q, and the trace of D over the steps is the dot
+// product (the off-diagonal sums are discarded; integer sums are exact in any order). Every weight
+// load is one contiguous KB of one row and every activation byte is loaded once per wave, where the
+// 16-row layout of mm_small_kernel spends a mostly-empty activation load per weight load. A wave owns
+// one output column; KS steps (KS KB of K) are loaded before their MFMAs, longer K in rounds.
+template <int EPI, typename T>
+__device__ __forceinline__ void epilogue1(const EpiArgs& e, int64_t n, T v) {
+  static_assert(EPI != EPI_REQUANT && EPI != EPI_CALIB, "GEMM epilogues only");
+  if constexpr (EPI == EPI_I32) {
+    reinterpret_cast<int32_t*>(e.out)[n] = v;
+  } else {
+    // the arithmetic of epilogue_w: ((float)acc * sx) * sw (+ bias), or the float sum (+ bias)
+    float t;
+    if constexpr (epi_bf(EPI)) {
+      t = v;
+    } else {
+      t = (float)v;
+      t = t * e.sx[0];
+      t = t * e.sw[n];
+    }
+    if (e.bias) t = t + e.bias[n];
+    if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_BF_F32) reinterpret_cast<float*>(e.out)[n] = t;
+    else if constexpr (EPI == EPI_DQ_BF16 || EPI == EPI_BF_BF16) reinterpret_cast<uint16_t*>(e.out)[n] = f32_to_bf16_bits(t);
+    else reinterpret_cast<uint16_t*>(e.out)[n] = f32_to_f16_bits(t);
+  }
+}
+
+template <int W, int KS, int EPI>
+__global__ __launch_bounds__(W * 64) void mm_gemv_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ w,
+                                                         int64_t ldw, int64_t N, int64_t K, EpiArgs e) {
+  constexpr bool BFE = epi_bf(EPI);       // bf16 operands, float accumulators
+  using Acc4 = std::conditional_t<BFE, f32x4, i32x4>;
+  using T = std::conditional_t<BFE, float, int32_t>;
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * W + (threadIdx.x >> 6);
+  if (n >= N) return;                     // wave-uniform, and the kernel has no barrier
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(N * ldw));
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a, (uint32_t)K);
+  const uint32_t wrow = (uint32_t)(n * ldw);
+  auto mfma = [&](const i32x4& w_, const i32x4& a_, Acc4& c) {
+    if constexpr (BFE) c = mfma16x16x32bf(w_, a_, c);
+    else c = mfma16x16x64(w_, a_, c);
+  };
+  Acc4 acc0 = {}, acc1 = {};
+  for (int64_t kc = 0; kc < K; kc += KS * 1024) {
+    i32x4 wv[KS], xv[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int64_t k = kc + s * 1024 + 16 * lane;
+      if (kc + s * 1024 < K) {            // uniform: steps wholly past K issue no loads
+        wv[s] = buf_load16(rw, k < K ? wrow + (uint32_t)k : OOB);
+        xv[s] = buf_load16(ra, k < K ? (uint32_t)k : OOB);
+      } else {
+        wv[s] = i32x4{0, 0, 0, 0};
+        xv[s] = i32x4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < KS; s += 2) {     // two accumulators: consecutive MFMAs do not wait on each other
+      mfma(wv[s], xv[s], acc0);
+      if (s + 1 < KS) mfma(wv[s + 1], xv[s + 1], acc1);
+    }
+  }
+  const Acc4 acc = acc0 + acc1;
+  // lane l holds D[4 (l / 16) + j][l % 16] in element j: the diagonal is in lanes with
+  // (l % 16) / 4 == l / 16, element l % 4
+  const int i = lane & 15;
+  const int j = lane & 3;
+  const T d = j == 0 ? acc[0] : j == 1 ? acc[1] : j == 2 ? acc[2] : acc[3];
+  T v = (i >> 2) == (lane >> 4) ? d : T(0);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  if (lane == 0) epilogue1<EPI>(e, n, v);
+}
+
 // ------------------------------------------------------------------------------ dispatch
 struct TileCfg {
   int bm, bn, waves;
@@ -691,13 +771,16 @@ struct TileCfg {
 // Tile ids (XDNA_TILE_* in the header): the tile engine's shapes, then the small-M kernel by waves.
 constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128x256 = 4, T_128x128 = 5,
               T_64x64 = 6, T_SMALL1 = 7, T_SMALL2 = 8, T_SMALL4 = 9, T_SMALL8 = 10, T_SMALL16 = 11,
-              T_192x256 = 12, T_256x192 = 13, T_64x32 = 14, T_32x64 = 15, T_32x32 = 16, T_COUNT = 17;
+              T_192x256 = 12, T_256x192 = 13, T_64x32 = 14, T_32x64 = 15, T_32x32 = 16, T_GEMV4 = 17,
+              T_GEMV2 = 18, T_GEMV8 = 19, T_COUNT = 20;
 
 static_assert(T_SMALL2 == T_SMALL1 + 1 && T_SMALL4 == T_SMALL1 + 2 && T_SMALL8 == T_SMALL1 + 3 &&
                   T_SMALL16 == T_SMALL1 + 4,
               "small-M ids count waves as powers of two");
 inline bool is_small(int t) { return t >= T_SMALL1 && t <= T_SMALL16; }
 inline int small_waves(int t) { return 1 << (t - T_SMALL1); }
+inline bool is_gemv(int t) { return t >= T_GEMV4 && t <= T_GEMV8; }
+inline int gemv_waves(int t) { return t == T_GEMV2 ? 2 : t == T_GEMV8 ? 8 : 4; }
 
 inline TileCfg tile_cfg(int t) {
   switch (t) {
@@ -744,6 +827,7 @@ int tile_lookup(int kind, int64_t m, int64_t n, int64_t k) {
 
 // The built-in rule, from back-to-back timed sweeps of every tile shape over the BASELINE GEMM and
 // conv shapes on MI355X (t128 / t256: tiles of that size the problem needs; kbytes: K in bytes):
+//   * M == 1: the one-row kernel, 4 waves (one output column each) per workgroup;
 //   * M <= 64 (decode): the small-M kernel, 2 waves per workgroup, 4 once K exceeds 8 KB;
 //   * 64 x 64 for N <= 64; for N <= 128 no 256-wide tile (half of it would be idle);
 //   * 256 x 256 with 8 waves (one workgroup per CU) from 1.5 rounds of such tiles, or from three
@@ -754,6 +838,7 @@ int tile_lookup(int kind, int64_t m, int64_t n, int64_t k) {
 //   * 64 x 64 for smaller problems.
 // A shape the tuned table lists uses the table's tile instead.
 int rule_tile(int64_t M, int64_t N, int64_t kbytes, bool small_ok) {
+  if (small_ok && M == 1) return T_GEMV4;
   if (small_ok && M <= 64) return (kbytes + 63) / 64 > 128 ? T_SMALL4 : T_SMALL2;
   const int64_t cus = device_cus();
   if (M <= 64 || N <= 64) return T_64x64;
@@ -837,8 +922,36 @@ constexpr int out_bytes() {
 template <int EPI>
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                 const EpiArgs& e, int tile, hipStream_t st) {
-  // the small-M kernel addresses the whole activation with one buffer resource, 16 rows per grid row
+  // the one-row kernel takes one row; the small-M kernel addresses the whole activation with one buffer
+  // resource, 16 rows per grid row
+  if (is_gemv(tile) && M != 1) tile = rule_tile(M, N, K, M > 1);
   if (is_small(tile) && (M * lda > MAX_BUF || (M + 15) / 16 >= 65536)) tile = rule_tile(M, N, K, false);
+  if (is_gemv(tile)) {
+    // one wave per output column, the weight in row chunks one buffer resource can address; K in
+    // rounds of 4 KB (K <= 4 KB) or 16 KB
+    const int64_t nrows = std::max<int64_t>(1, MAX_BUF / ldw);
+    const int waves = gemv_waves(tile);
+    for (int64_t n0 = 0; n0 < N; n0 += nrows) {
+      const int64_t nc = std::min(nrows, N - n0);
+      dim3 grid((unsigned)((nc + waves - 1) / waves), 1, 1);
+      const EpiArgs en = shift_epi(e, out_bytes<EPI>(), 0, n0);
+      const int8_t* wn = w + n0 * ldw;
+#define XDNA_GEMV(W_)                                                                                      \
+  if (K <= 4096) mm_gemv_kernel<W_, 4, EPI><<<grid, W_ * 64, 0, st>>>(a, wn, ldw, nc, K, en);              \
+  else mm_gemv_kernel<W_, 16, EPI><<<grid, W_ * 64, 0, st>>>(a, wn, ldw, nc, K, en);
+      if (waves == 2) {
+        XDNA_GEMV(2)
+      } else if (waves == 8) {
+        XDNA_GEMV(8)
+      } else {
+        XDNA_GEMV(4)
+      }
+#undef XDNA_GEMV
+      const int rc = launch_status("mm_gemv");
+      if (rc) return rc;
+    }
+    return XDNA_OK;
+  }
   if (is_small(tile)) {
     // weight streaming: the waves of a workgroup split K into multiples of 64 bytes; the weight is
     // processed in row chunks that one buffer resource can address. Waves per workgroup, from a
@@ -995,7 +1108,8 @@ int xdna_tile_set(int kind, int64_t m, int64_t n, int64_t k, int tile) {
   XDNA_REQUIRE(kind == XDNA_KIND_I8 || kind == XDNA_KIND_BF16 || kind == XDNA_KIND_CONV, "unknown kind");
   XDNA_REQUIRE(m >= 1 && n >= 1 && k >= 1, "bad sizes");
   XDNA_REQUIRE(tile >= T_AUTO && tile < T_COUNT, "unknown tile id");
-  XDNA_REQUIRE(!(kind == XDNA_KIND_CONV && is_small(tile)), "the small-M kernel does not run convs");
+  XDNA_REQUIRE(!(kind == XDNA_KIND_CONV && (is_small(tile) || is_gemv(tile))),
+               "the small-M and one-row kernels do not run convs");
   std::lock_guard<std::mutex> lock(g_tile_mu);
   const TileKey key{kind, m, n, k};
   if (tile == T_AUTO) g_tiles.erase(key);

@@ -38,13 +38,15 @@ CONV_SHAPES = [(1, 256, 256, 64, 64), (1, 256, 256, 1536, 64), (8, 3, 64, 224, 2
 CPU_CHECK_MACS = 1 << 31          # exactness against the CPU up to this many MACs, else against the rule
 ENGINE_TILES = [t for t in kernels.TILES if t.startswith("t")]
 SMALL_TILES = [t for t in kernels.TILES if t.startswith("small")]
+GEMV_TILES = [t for t in kernels.TILES if t.startswith("gemv")]
 
 
 def candidates(kind, M):
-    """Tiles to try: every tile-engine shape; the small-M kernel's widths for up to 256 rows."""
+    """Tiles to try: every tile-engine shape; the small-M kernel's widths for up to 256 rows; the one-row
+    kernel's widths for one row."""
     if kind == "conv" or M > 256:
         return list(ENGINE_TILES)
-    return ENGINE_TILES + SMALL_TILES
+    return ENGINE_TILES + SMALL_TILES + (GEMV_TILES if M == 1 else [])
 
 
 _cycles_per_ms = None
