@@ -76,6 +76,31 @@ def test_quant_rows_ties_zero_rows_strided(gpu):
     assert _np(xq)[1, :8].tolist() == [127, 2, -2, 4, -4, 0, 2, 0]
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("k", [1024, 200, 16384, 40000])
+def test_quant_rows_near_half(gpu, dtype, k):
+    """Quotients x / s placed within 6e-5 of half-integers, on both sides and exactly on them, under
+    irregular scales: the kernels round fl(x / s) like torch (the fast product with 1 / s is trusted only
+    farther than 2^-15 from a half-integer). Covers the 16-element-group, per-vector and long-row paths."""
+    from torch_xdna import kernels
+
+    rng = np.random.default_rng(k + len(dtype))
+    rows = 64
+    amax = rng.uniform(0.5, 300.0, rows).astype(np.float32)
+    s = (amax / np.float32(127)).astype(np.float32)
+    half = rng.integers(-127, 127, (rows, k)).astype(np.float64) + 0.5
+    d = rng.choice([0.0, 1e-7, -1e-7, 3e-6, -3e-6, 1.5e-5, -1.5e-5, 2.9e-5, -2.9e-5, 3.1e-5, -3.1e-5, 6e-5, -6e-5],
+                   (rows, k))
+    x = ((half + d) * s[:, None].astype(np.float64)).astype(np.float32)
+    x[:, 0] = amax                                   # fixes the row's amax, hence s
+    xt = torch.from_numpy(x).to(DT[dtype])
+    xq, sx = kernels.quant_rows(xt.to(gpu))
+    q_ref, s_ref = O.quant_rows(_f32(xt))
+    assert np.array_equal(_np(sx).view(np.uint32), s_ref.view(np.uint32))
+    bad = _np(xq)[:, :k] != q_ref
+    assert not bad.any(), f"{bad.sum()} of {bad.size} differ"
+
+
 # ------------------------------------------------------------------------------ int32 GEMM
 GEMM_SHAPES = [(1, 16, 64), (3, 50, 208), (16, 4096, 1024), (64, 1000, 512), (65, 300, 208), (200, 300, 208),
                (256, 512, 1024), (1000, 777, 96), (2048, 2048, 256), (4096, 4096, 128), (333, 4112, 48)]

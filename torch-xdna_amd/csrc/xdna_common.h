@@ -119,31 +119,40 @@ __device__ __forceinline__ float quantf(float x, float s, float r) {
 __device__ __forceinline__ int quant1(float x, float s, float r) { return (int)quantf(x, s, r); }
 
 // N values quantized and packed as N int8 bytes (value e in byte e % 4 of word e / 4), the vector form
-// of quant1. The products with the reciprocal are rounded first; only when some lane of the wave
-// holds a product within 2^-14 of a half-integer (rare) does the wave take the IEEE-division branch,
-// which is wave-uniform so the divisions are not computed speculatively for every element. q + 128
-// is an exact integer in [1, 255], which v_cvt_pk_u8_f32 writes into its byte lane; flipping bit 7
-// of every byte then gives the two's-complement int8.
+// of quant1; the integer is round_half_even(fl(x / s)), the correctly rounded quotient rounded again, as
+// torch.round(x / s) computes it. With r = fl(1 / s), t = fl(x * r) is within 127 * 2^-23 * (1 + 2^-24)
+// < 1.52e-5 of the exact quotient (two roundings of relative size 2^-24, |x / s| <= 127), and fl(x / s)
+// within a further 2^-18, so when t is at least 2^-15 (3.05e-5) from a half-integer, fl(x / s) lies on
+// the same side of it and both round alike. v_cvt_pk_u8_f32 rounds to nearest even and saturates to
+// [0, 255] (checked on gfx950 over every float in [-2, 258] at 2^-12 spacing and the neighbours of every
+// half-integer), so the byte q + 128 is that conversion of t + 128: the sum's rounding (at most 2^-17)
+// cannot carry it across the boundary either. Within 2^-15 of a half-integer (rare) the IEEE division
+// computes fl(x / s) itself; that branch is taken when some lane of the wave holds such a value, so it
+// is wave-uniform and the divisions are not computed speculatively for every element. |x / s| <= 127,
+// so the only clamp needed is the lower bound for -inf, which also maps NaN to -127 (max returns the
+// non-NaN operand); +inf saturates to 127. Flipping bit 7 of every byte then gives the two's-complement
+// int8.
 template <int N>
 __device__ __forceinline__ void quant_pack(const float (&x)[N], float s, float r, uint32_t (&w)[N / 4]) {
-  float t[N];
+  constexpr float NEAR = 3.0517578125e-05f;   // 2^-15
+  float t[N], b[N];
   bool near = false;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     t[i] = x[i] * r;
-    near |= fabsf(__builtin_amdgcn_fractf(t[i]) - 0.5f) < 6.103515625e-05f;
+    near |= fabsf(__builtin_amdgcn_fractf(t[i]) - 0.5f) < NEAR;
+    b[i] = t[i] + 128.0f;
   }
   if (__builtin_amdgcn_ballot_w64(near)) {
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      if (fabsf(__builtin_amdgcn_fractf(t[i]) - 0.5f) < 6.103515625e-05f) t[i] = x[i] / s;
+      if (fabsf(__builtin_amdgcn_fractf(t[i]) - 0.5f) < NEAR) b[i] = rintf(x[i] / s) + 128.0f;
   }
 #pragma unroll
   for (int g = 0; g < N / 4; ++g) {
     uint32_t v = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      v = __builtin_amdgcn_cvt_pk_u8_f32(fminf(fmaxf(rintf(t[4 * g + e]), -127.0f), 127.0f) + 128.0f, e, v);
+    for (int e = 0; e < 4; ++e) v = __builtin_amdgcn_cvt_pk_u8_f32(fmaxf(b[4 * g + e], 1.0f), e, v);
     w[g] = v ^ 0x80808080u;
   }
 }
@@ -153,6 +162,22 @@ __device__ __forceinline__ float scale_from_amax(float amax) {
   float a = amax > 1e-8f ? amax : 1e-8f;
   if (amax != amax) a = amax;   // NaN propagates as torch.clamp does
   return a / 127.0f;
+}
+
+// Raw buffer loads: a 16-byte load at a byte offset >= the resource's size returns zeros, which is how
+// rows past M / N, chunks past K and conv taps outside the image read as zero without a branch.
+constexpr uint32_t OOB = 0x7ffffff0u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes at byte offset off of a buffer resource (zeros past its end). NT: the non-temporal (slc)
+// form, for data read once that should not displace cached data.
+template <bool NT = false>
+__device__ __forceinline__ uint4 buf_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, NT ? 2 : 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
 // Wavefront (64 lanes) max reduction.

@@ -269,13 +269,6 @@ __device__ __forceinline__ void tile_coords(uint32_t pid, uint32_t tiles_m, uint
 __device__ __forceinline__ int swz_f(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int swz(int row, int chunk) { return (row << 6) + ((chunk ^ swz_f(row)) << 4); }
 
-// Raw buffer loads: a 16-byte load at a byte offset >= the resource's size returns zeros, which is how
-// rows past M / N, chunks past K and conv taps outside the image read as zero without a branch.
-constexpr uint32_t OOB = 0x7ffffff0u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
