@@ -50,8 +50,9 @@ extern "C" {
 #define XDNA_KIND_CONV 2 /* xdna_conv3x3_i8: m = nb * h * w, n = co, k = 9 * c_pad */
 
 /* Tile ids: the tile engine's workgroup tiles (rows x columns of the output, waves), the small-M
- * (weight-streaming) kernel by waves per workgroup, and the one-row (M = 1) kernel by waves per
- * workgroup (one output column per wave; any other M falls back to the built-in rule). */
+ * (weight-streaming) kernel by waves per workgroup, the one-row (M = 1) kernel by waves per workgroup
+ * (one output column per wave), and the few-row (M <= 16) kernel by output columns per workgroup
+ * (8 or 16); a tile forced on a shape its kernel does not take falls back to the built-in rule. */
 #define XDNA_TILE_AUTO 0
 #define XDNA_TILE_256x256W8 1
 #define XDNA_TILE_256x256W4 2
@@ -72,6 +73,8 @@ extern "C" {
 #define XDNA_TILE_GEMV_W4 17
 #define XDNA_TILE_GEMV_W2 18
 #define XDNA_TILE_GEMV_W8 19
+#define XDNA_TILE_SEG4_R2 20
+#define XDNA_TILE_SEG4_R4 21
 
 /* Library version (XDNA_ABI_VERSION). Replaces the import probe of kernels.available()
  * (torch_xdna/kernels.py:43-56): a loader checks it before trusting the other symbols. */

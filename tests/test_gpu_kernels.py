@@ -446,6 +446,41 @@ def test_gemv_one_row(gpu, tile, tile_table):
     assert kernels.tile_get(gpu, "i8", 1, 264, 4160) == tile
 
 
+@pytest.mark.parametrize("tile", ["seg4_r2", "seg4_r4"])
+def test_seg4_few_rows(gpu, tile, tile_table):
+    """The few-row kernel (M <= 16: 4 weight rows x 4 K segments on the MFMA's rows, 4 activation rows x 4
+    segments on its columns, quad sums): int32 sums, the fused dequant with and without bias and the bf16
+    GEMM against the oracle, for every activation group count, K from one 16-byte chunk to 14336 bytes
+    (partial steps and rounds), N not a multiple of the columns per workgroup; 17 rows fall back to the
+    rule."""
+    from torch_xdna import kernels
+
+    for m, n, k in [(2, 520, 16), (3, 1001, 272), (4, 64, 1040), (5, 300, 4112), (8, 97, 2064), (11, 130, 14336),
+                    (16, 1001, 4096), (16, 8, 256), (17, 200, 1040)]:
+        kernels.tile_set("i8", m, n, k, tile)
+        kb = max(8, k // 2)
+        kernels.tile_set("bf16", m, n, kb, tile)
+        a, w = _i8((m, k), seed=3 * m + k + n), _i8((n, k), seed=n + 2 * k)
+        acc = c_oracle.gemm_i32(a.numpy(), w.numpy())
+        assert np.array_equal(_np(kernels.mm_i8(a.to(gpu), w.to(gpu))), acc), (tile, m, n, k)
+        sx, sw = torch.rand(m) + 0.01, torch.rand(n) + 0.01
+        b = torch.randn(n)
+        for out in ("f32", "bf16", "f16"):
+            for bias in (b, None):
+                y = kernels.mm_i8_dequant(a.to(gpu), sx.to(gpu), w.to(gpu), sw.to(gpu),
+                                          None if bias is None else bias.to(gpu), DT[out])
+                want = O.dequant(acc, sx.numpy(), sw.numpy(), None if bias is None else bias.numpy())
+                assert np.array_equal(_f32(y), O.to_dtype(want, out)), (tile, m, n, k, out, bias is None)
+        x = _rand((m, kb), torch.float32, seed=m + k)
+        wf = _rand((n, kb), torch.float32, seed=n + k, scale=0.05)
+        bb = _rand((n,), torch.float32, seed=n, scale=0.1)
+        yb = kernels.mm_bf16(kernels.bf16_rows(x.to(gpu), kb), kernels.bf16_rows(wf.to(gpu), kb), bb.to(gpu),
+                             torch.float32)
+        want, bound = O.gemm_bf16(x.numpy(), wf.numpy(), bb.numpy())
+        _bf16_bracket(_f32(yb), want, bound, "f32")
+    assert kernels.tile_get(gpu, "i8", 16, 1001, 4096) == tile
+
+
 def test_sweep_tool(gpu, tile_table, tmp_path):
     """python -m torch_xdna.sweep on small shapes of each kind: one exact, timed JSONL line per
     candidate tile; resuming skips finished lines; --summary writes a table the runtime can load."""
@@ -460,7 +495,9 @@ def test_sweep_tool(gpu, tile_table, tmp_path):
     n_lines = sum(1 for _ in open(out))
     sweep.main(["--kind", "i8", "--rows", "16", "300", "--shapes", "520x256", "--out", out])   # resumed: no-op
     recs = [json.loads(line) for line in open(out)]
-    assert len(recs) == n_lines == 16 + 11 + 11 + 11
+    want = len(sweep.candidates("i8", 16)) + len(sweep.candidates("i8", 300)) + \
+        len(sweep.candidates("bf16", 300)) + len(sweep.candidates("conv", 2 * 13 * 37))
+    assert len(recs) == n_lines == want
     assert all(r["status"] == "ok" and r["exact"] and r["gpu_us"] > 0 for r in recs), recs
     assert {r["checked_against"] for r in recs} == {"cpu"}
     table_path = str(tmp_path / "tuned.json")

@@ -87,9 +87,11 @@ def test_summary_keeps_clear_wins(tmp_path):
 
 
 def test_sweep_candidates():
-    assert sweep.candidates("i8", 16) == sweep.ENGINE_TILES + sweep.SMALL_TILES
-    assert sweep.candidates("i8", 1) == sweep.ENGINE_TILES + sweep.SMALL_TILES + sweep.GEMV_TILES
+    assert sweep.candidates("i8", 16) == sweep.ENGINE_TILES + sweep.SMALL_TILES + sweep.SEG4_TILES
+    assert sweep.candidates("i8", 17) == sweep.ENGINE_TILES + sweep.SMALL_TILES
+    assert sweep.candidates("i8", 1) == sweep.ENGINE_TILES + sweep.SMALL_TILES + sweep.GEMV_TILES + sweep.SEG4_TILES
     assert sweep.candidates("bf16", 1) == sweep.candidates("i8", 1)
     assert sweep.candidates("i8", 3000) == sweep.ENGINE_TILES
     assert sweep.candidates("conv", 1) == sweep.ENGINE_TILES
-    assert set(sweep.ENGINE_TILES + sweep.SMALL_TILES + sweep.GEMV_TILES) == set(kernels.TILES) - {"auto"}
+    assert set(sweep.ENGINE_TILES + sweep.SMALL_TILES + sweep.GEMV_TILES + sweep.SEG4_TILES) == \
+        set(kernels.TILES) - {"auto"}

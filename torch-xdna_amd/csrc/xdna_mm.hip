@@ -686,25 +686,27 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
 // load is one contiguous KB of one row and every activation byte is loaded once per wave, where the
 // 16-row layout of mm_small_kernel spends a mostly-empty activation load per weight load. A wave owns
 // one output column; KS steps (KS KB of K) are loaded before their MFMAs, longer K in rounds.
+// One output element (row m, column n) of a GEMM epilogue, with the arithmetic of epilogue_w.
 template <int EPI, typename T>
-__device__ __forceinline__ void epilogue1(const EpiArgs& e, int64_t n, T v) {
+__device__ __forceinline__ void epilogue1(const EpiArgs& e, int64_t m, int64_t n, T v) {
   static_assert(EPI != EPI_REQUANT && EPI != EPI_CALIB, "GEMM epilogues only");
+  const int64_t off = m * e.ldo + n;
   if constexpr (EPI == EPI_I32) {
-    reinterpret_cast<int32_t*>(e.out)[n] = v;
+    reinterpret_cast<int32_t*>(e.out)[off] = v;
   } else {
-    // the arithmetic of epilogue_w: ((float)acc * sx) * sw (+ bias), or the float sum (+ bias)
+    // ((float)acc * sx) * sw (+ bias), or the float sum (+ bias)
     float t;
     if constexpr (epi_bf(EPI)) {
       t = v;
     } else {
       t = (float)v;
-      t = t * e.sx[0];
+      t = t * e.sx[m];
       t = t * e.sw[n];
     }
     if (e.bias) t = t + e.bias[n];
-    if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_BF_F32) reinterpret_cast<float*>(e.out)[n] = t;
-    else if constexpr (EPI == EPI_DQ_BF16 || EPI == EPI_BF_BF16) reinterpret_cast<uint16_t*>(e.out)[n] = f32_to_bf16_bits(t);
-    else reinterpret_cast<uint16_t*>(e.out)[n] = f32_to_f16_bits(t);
+    if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_BF_F32) reinterpret_cast<float*>(e.out)[off] = t;
+    else if constexpr (EPI == EPI_DQ_BF16 || EPI == EPI_BF_BF16) reinterpret_cast<uint16_t*>(e.out)[off] = f32_to_bf16_bits(t);
+    else reinterpret_cast<uint16_t*>(e.out)[off] = f32_to_f16_bits(t);
   }
 }
 
@@ -753,7 +755,107 @@ __global__ __launch_bounds__(W * 64) void mm_gemv_kernel(const int8_t* __restric
   T v = (i >> 2) == (lane >> 4) ? d : T(0);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  if (lane == 0) epilogue1<EPI>(e, n, v);
+  if (lane == 0) epilogue1<EPI>(e, 0, n, v);
+}
+
+// ------------------------------------------------------------------------------ a few rows (M <= 16)
+// The segment trick with 4 segments of 4 rows: the 16 rows of the MFMA's A operand are 4 weight rows x 4
+// segments and its 16 columns 4 activation rows x 4 segments. In a 256-byte step at byte kb, lane l
+// (row / column i = l % 16, k chunk c = l / 16) holds bytes kb + 16 (i % 4 + 4 c) .. +15 of weight row
+// i / 4 (A) and of activation row i / 4 (B), so D[i][m] with i % 4 == m % 4 sums segment i % 4 of the
+// step for weight row i / 4 and activation row m / 4, and the four segments together cover the step.
+// In the accumulator, lane l's element l % 4 is that segment's sum for weight row l / 16 and activation
+// row (l % 16) / 4; the sum over the lane's quad is the dot product over the step. Every load is 4 rows x
+// 256 contiguous bytes. The activation comes in XG groups of 4 rows, each loaded once per step and used
+// for the R weight-row groups of the workgroup; the W waves split K into multiples of 256 bytes and
+// their sums meet in LDS.
+template <int W, int R, int XG, int EPI>
+__global__ __launch_bounds__(W * 64) void mm_seg4_kernel(const int8_t* __restrict__ a, int64_t lda,
+                                                         const int8_t* __restrict__ w, int64_t ldw, int64_t M,
+                                                         int64_t N, int64_t K, int64_t kper, EpiArgs e) {
+  constexpr bool BFE = epi_bf(EPI);       // bf16 operands, float accumulators
+  using Acc4 = std::conditional_t<BFE, f32x4, i32x4>;
+  using T = std::conditional_t<BFE, float, int32_t>;
+  constexpr int KS = 4;                   // 256-byte steps loaded before their MFMAs
+  __shared__ T red[W][R][XG][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t n0 = (int64_t)blockIdx.x * (4 * R);
+  const int rsub = (lane & 15) >> 2;      // this lane's row within a group of 4 (A and B alike)
+  const uint32_t koff = 16 * ((lane & 3) + 4 * (lane >> 4));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(N * ldw));
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a, (uint32_t)(M * lda));
+  uint32_t wrow[R], arow[XG];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t n = n0 + 4 * r + rsub;
+    wrow[r] = n < N ? (uint32_t)(n * ldw) : OOB;
+  }
+#pragma unroll
+  for (int q = 0; q < XG; ++q) {
+    const int64_t m = 4 * q + rsub;
+    arow[q] = m < M ? (uint32_t)(m * lda) : OOB;
+  }
+  const int64_t kbeg = (int64_t)wave * kper;
+  const int64_t kend = min(K, kbeg + kper);
+  auto mfma = [&](const i32x4& w_, const i32x4& a_, Acc4& c) {
+    if constexpr (BFE) c = mfma16x16x32bf(w_, a_, c);
+    else c = mfma16x16x64(w_, a_, c);
+  };
+  Acc4 acc[R][XG];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int q = 0; q < XG; ++q) acc[r][q] = Acc4{};
+  for (int64_t kc = kbeg; kc < kend; kc += KS * 256) {
+    i32x4 wv[R][KS], xv[XG][KS];
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      const int64_t k = kc + st * 256 + koff;
+      const bool in = k < kend;
+      if (kc + st * 256 < kend) {         // uniform: steps wholly past the range issue no loads
+#pragma unroll
+        for (int q = 0; q < XG; ++q) xv[q][st] = buf_load16(ra, in && arow[q] != OOB ? arow[q] + (uint32_t)k : OOB);
+#pragma unroll
+        for (int r = 0; r < R; ++r) wv[r][st] = buf_load16(rw, in && wrow[r] != OOB ? wrow[r] + (uint32_t)k : OOB);
+      } else {
+#pragma unroll
+        for (int q = 0; q < XG; ++q) xv[q][st] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < R; ++r) wv[r][st] = i32x4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int st = 0; st < KS; ++st)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < XG; ++q) mfma(wv[r][st], xv[q][st], acc[r][q]);
+  }
+  const int j = lane & 3;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int q = 0; q < XG; ++q) {
+      const Acc4& c = acc[r][q];
+      T v = j == 0 ? c[0] : j == 1 ? c[1] : j == 2 ? c[2] : c[3];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      red[wave][r][q][lane] = v;
+    }
+  __syncthreads();
+  if (wave != 0 || j != 0) return;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int q = 0; q < XG; ++q) {
+      T v = red[0][r][q][lane];
+#pragma unroll
+      for (int u = 1; u < W; ++u) v += red[u][r][q][lane];
+      const int64_t m = 4 * q + rsub;
+      const int64_t n = n0 + 4 * r + (lane >> 4);
+      if (m < M && n < N) epilogue1<EPI>(e, m, n, v);
+    }
 }
 
 // ------------------------------------------------------------------------------ dispatch
@@ -765,7 +867,7 @@ struct TileCfg {
 constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128x256 = 4, T_128x128 = 5,
               T_64x64 = 6, T_SMALL1 = 7, T_SMALL2 = 8, T_SMALL4 = 9, T_SMALL8 = 10, T_SMALL16 = 11,
               T_192x256 = 12, T_256x192 = 13, T_64x32 = 14, T_32x64 = 15, T_32x32 = 16, T_GEMV4 = 17,
-              T_GEMV2 = 18, T_GEMV8 = 19, T_COUNT = 20;
+              T_GEMV2 = 18, T_GEMV8 = 19, T_SEG4R2 = 20, T_SEG4R4 = 21, T_COUNT = 22;
 
 static_assert(T_SMALL2 == T_SMALL1 + 1 && T_SMALL4 == T_SMALL1 + 2 && T_SMALL8 == T_SMALL1 + 3 &&
                   T_SMALL16 == T_SMALL1 + 4,
@@ -774,6 +876,7 @@ inline bool is_small(int t) { return t >= T_SMALL1 && t <= T_SMALL16; }
 inline int small_waves(int t) { return 1 << (t - T_SMALL1); }
 inline bool is_gemv(int t) { return t >= T_GEMV4 && t <= T_GEMV8; }
 inline int gemv_waves(int t) { return t == T_GEMV2 ? 2 : t == T_GEMV8 ? 8 : 4; }
+inline bool is_seg4(int t) { return t == T_SEG4R2 || t == T_SEG4R4; }
 
 inline TileCfg tile_cfg(int t) {
   switch (t) {
@@ -821,6 +924,7 @@ int tile_lookup(int kind, int64_t m, int64_t n, int64_t k) {
 // The built-in rule, from back-to-back timed sweeps of every tile shape over the BASELINE GEMM and
 // conv shapes on MI355X (t128 / t256: tiles of that size the problem needs; kbytes: K in bytes):
 //   * M == 1: the one-row kernel, 4 waves (one output column each) per workgroup;
+//   * 2 <= M <= 8 with K of at least 2 KB: the few-row kernel, 8 output columns per workgroup;
 //   * M <= 64 (decode): the small-M kernel, 2 waves per workgroup, 4 once K exceeds 8 KB;
 //   * 64 x 64 for N <= 64; for N <= 128 no 256-wide tile (half of it would be idle);
 //   * 256 x 256 with 8 waves (one workgroup per CU) from 1.5 rounds of such tiles, or from three
@@ -832,6 +936,7 @@ int tile_lookup(int kind, int64_t m, int64_t n, int64_t k) {
 // A shape the tuned table lists uses the table's tile instead.
 int rule_tile(int64_t M, int64_t N, int64_t kbytes, bool small_ok) {
   if (small_ok && M == 1) return T_GEMV4;
+  if (small_ok && M <= 8 && kbytes >= 2048) return T_SEG4R2;
   if (small_ok && M <= 64) return (kbytes + 63) / 64 > 128 ? T_SMALL4 : T_SMALL2;
   const int64_t cus = device_cus();
   if (M <= 64 || N <= 64) return T_64x64;
@@ -918,6 +1023,35 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
   // the one-row kernel takes one row; the small-M kernel addresses the whole activation with one buffer
   // resource, 16 rows per grid row
   if (is_gemv(tile) && M != 1) tile = rule_tile(M, N, K, M > 1);
+  if (is_seg4(tile) && M > 16) tile = rule_tile(M, N, K, true);
+  if (is_seg4(tile)) {
+    // four rows per segment group; the workgroup's 4 waves split K into multiples of 256 bytes
+    constexpr int W = 4;
+    const int64_t steps = (K + 255) / 256;
+    const int64_t kper = ((steps + W - 1) / W) * 256;
+    const int R = tile == T_SEG4R2 ? 2 : 4;
+    const int64_t nrows = std::max<int64_t>(4 * R, (MAX_BUF / ldw) / (4 * R) * (4 * R));
+    for (int64_t n0 = 0; n0 < N; n0 += nrows) {
+      const int64_t nc = std::min(nrows, N - n0);
+      dim3 grid((unsigned)((nc + 4 * R - 1) / (4 * R)), 1, 1);
+      const EpiArgs en = shift_epi(e, out_bytes<EPI>(), 0, n0);
+      const int8_t* wn = w + n0 * ldw;
+#define XDNA_SEG4(R_, XG_) mm_seg4_kernel<W, R_, XG_, EPI><<<grid, W * 64, 0, st>>>(a, lda, wn, ldw, M, nc, K, kper, en)
+      if (R == 2) {
+        if (M <= 4) XDNA_SEG4(2, 1);
+        else if (M <= 8) XDNA_SEG4(2, 2);
+        else XDNA_SEG4(2, 4);
+      } else {
+        if (M <= 4) XDNA_SEG4(4, 1);
+        else if (M <= 8) XDNA_SEG4(4, 2);
+        else XDNA_SEG4(4, 4);
+      }
+#undef XDNA_SEG4
+      const int rc = launch_status("mm_seg4");
+      if (rc) return rc;
+    }
+    return XDNA_OK;
+  }
   if (is_small(tile) && (M * lda > MAX_BUF || (M + 15) / 16 >= 65536)) tile = rule_tile(M, N, K, false);
   if (is_gemv(tile)) {
     // one wave per output column, the weight in row chunks one buffer resource can address; K in
@@ -1101,8 +1235,8 @@ int xdna_tile_set(int kind, int64_t m, int64_t n, int64_t k, int tile) {
   XDNA_REQUIRE(kind == XDNA_KIND_I8 || kind == XDNA_KIND_BF16 || kind == XDNA_KIND_CONV, "unknown kind");
   XDNA_REQUIRE(m >= 1 && n >= 1 && k >= 1, "bad sizes");
   XDNA_REQUIRE(tile >= T_AUTO && tile < T_COUNT, "unknown tile id");
-  XDNA_REQUIRE(!(kind == XDNA_KIND_CONV && (is_small(tile) || is_gemv(tile))),
-               "the small-M and one-row kernels do not run convs");
+  XDNA_REQUIRE(!(kind == XDNA_KIND_CONV && (is_small(tile) || is_gemv(tile) || is_seg4(tile))),
+               "the small-M, one-row and few-row kernels do not run convs");
   std::lock_guard<std::mutex> lock(g_tile_mu);
   const TileKey key{kind, m, n, k};
   if (tile == T_AUTO) g_tiles.erase(key);

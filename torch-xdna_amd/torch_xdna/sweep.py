@@ -7,7 +7,9 @@ the library's tile table, checked for exact results (int8: int32 sums equal to t
 torch._int_mm, or for shapes too large for the CPU in seconds, to the rule's tile on the GPU; conv:
 requantized integers equal to the CPU's exact float conv of the integers, or the rule's tile; bf16:
 the reference's 5e-2 relative-norm check against a float32 matmul of the bf16 operands) and timed
-as back-to-back launches between two events behind a GPU spin gate (GPU time only).
+as back-to-back launches between two events behind a GPU spin gate (GPU time only); launches of
+weight-streaming shapes (up to 256 rows) cycle through copies of the weight that span more than the
+256 MB Infinity Cache, so every launch reads its weight from HBM.
 
 usage: python -m torch_xdna.sweep [--kind i8|bf16|conv] [--rows 128 512 1024 3000]
                                   [--shapes 4096x1024 ...] [--convs 1x256x256x64x64 ...]
@@ -19,6 +21,7 @@ exact tile when it beats the library's rule by more than 2%.
 """
 
 import argparse
+import itertools
 import json
 import os
 import sys
@@ -39,14 +42,15 @@ CPU_CHECK_MACS = 1 << 31          # exactness against the CPU up to this many MA
 ENGINE_TILES = [t for t in kernels.TILES if t.startswith("t")]
 SMALL_TILES = [t for t in kernels.TILES if t.startswith("small")]
 GEMV_TILES = [t for t in kernels.TILES if t.startswith("gemv")]
+SEG4_TILES = [t for t in kernels.TILES if t.startswith("seg4")]
 
 
 def candidates(kind, M):
     """Tiles to try: every tile-engine shape; the small-M kernel's widths for up to 256 rows; the one-row
-    kernel's widths for one row."""
+    kernel's widths for one row; the few-row kernel's widths for up to 16 rows."""
     if kind == "conv" or M > 256:
         return list(ENGINE_TILES)
-    return ENGINE_TILES + SMALL_TILES + (GEMV_TILES if M == 1 else [])
+    return ENGINE_TILES + SMALL_TILES + (GEMV_TILES if M == 1 else []) + (SEG4_TILES if M <= 16 else [])
 
 
 _cycles_per_ms = None
@@ -66,7 +70,7 @@ def _gate(ms):
     torch.cuda._sleep(int(ms * _cycles_per_ms))
 
 
-def gpu_us(fn, reps=20):
+def gpu_us(fn, reps=48):
     """Microseconds per launch of fn: reps launches behind a gate, between two events."""
     fn()
     torch.cuda.synchronize()
@@ -88,6 +92,24 @@ def _gen(seed):
     return torch.Generator().manual_seed(seed)
 
 
+MALL_BYTES = 256 << 20             # MI355X Infinity Cache
+
+
+def _weight_copies(w, M):
+    """Copies of the device weight w that the timed launches cycle through: for weight-streaming shapes
+    (up to 256 rows) enough copies to span more than the Infinity Cache, so each launch reads its weight
+    from HBM as a model's layers do, not from the cache the previous launch filled."""
+    if M > 256:
+        return [w]
+    n = min(96, -(-(MALL_BYTES + (64 << 20)) // (w.numel() * w.element_size())))
+    return [w] + [w.clone() for _ in range(n - 1)]
+
+
+def _cycling(fn, items):
+    it = itertools.cycle(items)
+    return lambda: fn(next(it))
+
+
 def _gemm_case(kind, M, N, K, dev):
     """(timed launch, launch whose result is checked, the CPU's result or None, how to compare, ops)
     for one GEMM shape."""
@@ -97,7 +119,9 @@ def _gemm_case(kind, M, N, K, dev):
         w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
         sx, sw = torch.rand(M, generator=g) + 0.01, torch.rand(N, generator=g) + 0.01
         ag, wg, sxg, swg = a.to(dev), w.to(dev), sx.to(dev), sw.to(dev)
-        bench = lambda: kernels.mm_i8_dequant(ag, sxg, wg, swg, None, torch.bfloat16)   # what the product runs
+        # what the product runs
+        bench = _cycling(lambda wc: kernels.mm_i8_dequant(ag, sxg, wc, swg, None, torch.bfloat16),
+                         _weight_copies(wg, M))
         exact = lambda: kernels.mm_i8(ag, wg)
         want = torch._int_mm(a, w.t().contiguous()) if M * N * K <= CPU_CHECK_MACS else None
         return bench, exact, want, "equal", 2 * M * N * K
@@ -105,8 +129,9 @@ def _gemm_case(kind, M, N, K, dev):
     w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
     xg, wg = x.to(dev), w.to(dev)
     run = lambda: kernels.mm_bf16(xg, wg, None, torch.float32)
+    bench = _cycling(lambda wc: kernels.mm_bf16(xg, wc, None, torch.float32), _weight_copies(wg, M))
     want = x.float() @ w.float().t() if M * N * K <= CPU_CHECK_MACS else None
-    return run, run, want, "norm", 2 * M * N * K
+    return bench, run, want, "norm", 2 * M * N * K
 
 
 def _conv_case(n, ci, co, h, w, dev):
