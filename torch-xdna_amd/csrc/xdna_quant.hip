@@ -368,9 +368,13 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
     return launch_status("quant_rows_scalar");
   }
   const int64_t nvec = k / VEC;
-  // one wavefront per row with 16-element groups: 16-bit inputs up to 16384 per row, float32 up to 8192
+  // One wavefront per row with 16-element groups (16-bit inputs up to 16384 per row, float32 up to 8192),
+  // except for fewer than 512 rows longer than 2048 elements: a row's latency then dominates, and the
+  // 256-thread blocks below give each row four times the lanes (measured on the decode rows, 1 and 16
+  // rows of 4096 and 14336 bf16: 4.0 us per launch instead of 4.3 and 11.2 us).
   const int64_t gpl = cdiv(k / 16, 64);  // groups per lane
-  if (k % 16 == 0 && k < (int64_t(1) << 31) && gpl <= (DT == XDNA_F32 ? 8 : 16)) {
+  const bool few = rows < 512;
+  if (k % 16 == 0 && k < (int64_t(1) << 31) && gpl <= (DT == XDNA_F32 ? 8 : 16) && !(few && gpl > 2)) {
     const bool nt = rows * k * (DT == XDNA_F32 ? 4 : 2) >= (int64_t(128) << 20);   // half the Infinity Cache
     const dim3 grid((unsigned)cdiv(rows, 4));
 #define XDNA_QW(G_)                                                                                     \
@@ -390,7 +394,7 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
 #undef XDNA_QW
     return launch_status("quant_rows");
   }
-  if (nvec <= 64 * 8) {  // one wavefront per row, four rows per block
+  if (nvec <= 64 * 8 && !few) {  // one wavefront per row, four rows per block
     quant_rows_vec_kernel<DT, 64, 8><<<dim3((unsigned)cdiv(rows, 4)), 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
   } else if (nvec <= 256 * 8) {
     quant_rows_stream_kernel<DT, 8><<<dim3(stream_blocks(quant_rows_stream_kernel<DT, 8>, rows)), 256, 0, st>>>(
