@@ -51,8 +51,9 @@ extern "C" {
 
 /* Tile ids: the tile engine's workgroup tiles (rows x columns of the output, waves), the small-M
  * (weight-streaming) kernel by waves per workgroup, the one-row (M = 1) kernel by waves per workgroup
- * (one output column per wave), and the few-row (M <= 16) kernel by output columns per workgroup
- * (8 or 16); a tile forced on a shape its kernel does not take falls back to the built-in rule. */
+ * (one output column per wave), the few-row (M <= 16) kernel by output columns per workgroup
+ * (8 or 16), and tile-engine tiles whose workgroup splits K between 2 or 4 groups of waves (K2 / K4);
+ * a tile forced on a shape its kernel does not take falls back to the built-in rule. */
 #define XDNA_TILE_AUTO 0
 #define XDNA_TILE_256x256W8 1
 #define XDNA_TILE_256x256W4 2
@@ -75,6 +76,11 @@ extern "C" {
 #define XDNA_TILE_GEMV_W8 19
 #define XDNA_TILE_SEG4_R2 20
 #define XDNA_TILE_SEG4_R4 21
+#define XDNA_TILE_64x64K2 22
+#define XDNA_TILE_64x64K4 23
+#define XDNA_TILE_32x64K4 24
+#define XDNA_TILE_32x32K4 25
+#define XDNA_TILE_128x128K2 26
 
 /* Library version (XDNA_ABI_VERSION). Replaces the import probe of kernels.available()
  * (torch_xdna/kernels.py:43-56): a loader checks it before trusting the other symbols. */

@@ -342,18 +342,22 @@ def tile_table():
 
 
 @pytest.mark.parametrize("tile", ["t256x256w8", "t256x256w4", "t256x128", "t128x256", "t128x128", "t64x64",
-                                  "t192x256", "t256x192", "t64x32", "t32x64", "t32x32"])
+                                  "t192x256", "t256x192", "t64x32", "t32x64", "t32x32",
+                                  "t64x64k2", "t64x64k4", "t32x64k4", "t32x32k4", "t128x128k2"])
 def test_tiles_forced(gpu, tile, tile_table):
     """Each tile configuration of the engine, forced through the library's tile table: int32 and
-    fused bf16 GEMMs with partial tiles and K both a multiple of 64 and not, and the conv with both
-    A loaders (C_pad % 64 == 0 and not), against the oracle."""
+    fused bf16 GEMMs with partial tiles and K both a multiple of 64 and not (for the K-group tiles:
+    slice counts not a multiple of the groups, and a single slice per group), and the conv with both A
+    loaders (C_pad % 64 == 0 and not; for K groups C_pad % (64 * groups) == 0 and not) and its
+    calibration maximum, against the oracle."""
     from torch_xdna import kernels
 
     for m, n, k in [(700, 1000, 4160), (333, 520, 208), (700, 1000, 2080), (333, 520, 104)]:
         kernels.tile_set("i8", m, n, k, tile)
         kernels.tile_set("bf16", m, n, k, tile)
         assert kernels.tile_get(gpu, "i8", m, n, k) == tile
-    for n, ci, co, h, w_ in [(2, 64, 96, 16, 20), (1, 48, 40, 13, 37)]:
+    convs = [(2, 64, 96, 16, 20), (1, 48, 40, 13, 37), (1, 256, 64, 8, 12), (1, 128, 48, 9, 10)]
+    for n, ci, co, h, w_ in convs:
         kernels.tile_set("conv", n * h * w_, co, 9 * -(-ci // 16) * 16, tile)
         assert kernels.tile_get(gpu, "conv", n * h * w_, co, 9 * -(-ci // 16) * 16) == tile
     for m, n, k in [(700, 1000, 4160), (333, 520, 208)]:
@@ -370,7 +374,7 @@ def test_tiles_forced(gpu, tile, tile_table):
         y = kernels.mm_bf16(kernels.bf16_rows(x.to(gpu), k), kernels.bf16_rows(w.to(gpu), k), None, torch.float32)
         want, bound = O.gemm_bf16(x.numpy(), w.numpy())
         _bf16_bracket(_f32(y), want, bound, "f32")
-    for n, ci, co, h, w_ in [(2, 64, 96, 16, 20), (1, 48, 40, 13, 37)]:
+    for n, ci, co, h, w_ in convs:
         xq = _i8((n, ci, h, w_), seed=ci + h)
         wq = _i8((co, ci, 3, 3), seed=co + w_)
         c_pad = -(-ci // 16) * 16
@@ -380,6 +384,8 @@ def test_tiles_forced(gpu, tile, tile_table):
         acc = c_oracle.conv3x3_acc(xq.numpy(), wq.numpy())
         q = kernels.conv3x3(x_nhwc, packed.to(gpu), 9, False)
         assert np.array_equal(_np(q).transpose(0, 3, 1, 2), O.requant(acc, 9, False)), (n, ci, co, h, w_)
+        if n == 1:
+            assert kernels.conv3x3_calibrate(x_nhwc, packed.to(gpu), False) == int(np.abs(acc).max())
 
 
 @pytest.mark.parametrize("tile", ["small_w1", "small_w2", "small_w4", "small_w8", "small_w16", "t64x64", "t128x128"])

@@ -330,8 +330,13 @@ struct PinTwo {
 //   reads of slice kt+1's step-0 fragments in between.
 // Slices past the end of K are loaded as out-of-range (zero) reads, which keeps the wait counts and
 // the loop uniform.
-template <int BM, int BN, int WM, int WN, int S, int CONVM, int EPI, bool KFULL>
-__global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __restrict__ a, int64_t lda,
+// KG > 1 splits K inside the workgroup: KG groups of WM x WN waves each run this pipeline in their own
+// LDS stages over every KG-th slice (group g: slices g, g + KG, ...), all groups meeting at the same
+// barriers; at the end groups 1 .. KG-1 leave their accumulators in LDS and group 0 adds them before
+// the epilogue. It multiplies the loads in flight and the MFMA streams of a tile for shapes with few
+// tiles and deep K (integer sums are exact in any order).
+template <int BM, int BN, int WM, int WN, int S, int CONVM, int EPI, bool KFULL, int KG = 1>
+__global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t* __restrict__ a, int64_t lda,
                                                                const int8_t* __restrict__ w, int64_t ldw, int64_t M,
                                                                int64_t N, int64_t K, ConvGeom cg, EpiArgs e) {
   constexpr bool CONV = CONVM != 0;      // CONVM: 0 GEMM, 1 conv with C_pad % 64 == 0, 2 any C_pad
@@ -344,16 +349,19 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
   static_assert(FM >= 1 && FN >= 1, "wave tile below 32 x 32");
   static_assert(IA >= 1 && IW >= 1 && BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "tile / wave mismatch");
   constexpr int STAGE = (BM + BN) * BK;
-  static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS stages");
+  static_assert(S >= 2 && KG >= 1 && KG * S * STAGE <= 160 * 1024, "LDS stages");
   constexpr int NDMA = IA + IW;
   static_assert((S - 1) * NDMA <= 63, "vmcnt range");
 
-  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+  __shared__ __attribute__((aligned(1024))) int8_t lds_all[KG * S * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: keeps LDS bases scalar
+  const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: keeps LDS bases scalar
+  const int kg = wave_all / NW;          // K group
+  const int wave = wave_all - kg * NW;   // wave within the group
   const int wm = wave / WN, wn = wave % WN;
+  int8_t* const lds = lds_all + kg * (S * STAGE);
 
   const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int64_t tm, tn;
@@ -418,9 +426,14 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
   }
 
   const int64_t nk = (K + BK - 1) / BK;
-  // CONVM 1: the slices are issued in order, so the tap and channel offset of the next slice to load
-  // are kept as running counters instead of being divided out of k.
+  // CONVM 1: a group's slices are issued in order, KG slices apart, so the tap and channel offset of
+  // its next slice are kept as running counters instead of being divided out of k (the launcher takes
+  // CONVM 1 with KG > 1 only when c_pad is a multiple of KG * 64, so each step wraps at most once).
   int dtap = 0, dc0 = 0;
+  if constexpr (CONVM == 1) {
+    dtap = (kg * BK) / (int)cg.c_pad;
+    dc0 = (kg * BK) - dtap * (int)cg.c_pad;
+  }
   (void)dtap;
   (void)dc0;
   auto dma_slice = [&](int64_t kt, int8_t* stage) {
@@ -439,9 +452,9 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
         const bool ok = live && sy >= 0 && sy < cg.h && sx >= 0 && sx < cg.w;
         dma16(ra_rsrc, ok ? (uint32_t)(oa[j] + delta + ca[j] * 16) : OOB, sa + ((wave * IA + j) << 10));
       }
-      dc0 += BK;
-      if (dc0 == cg.c_pad) {
-        dc0 = 0;
+      dc0 += BK * KG;
+      if (dc0 >= cg.c_pad) {
+        dc0 -= (int)cg.c_pad;
         ++dtap;
       }
     } else if constexpr (CONVM == 2) {
@@ -514,9 +527,9 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
       }
   };
 
-  // prologue: slices 0 .. S-1 into stages 0 .. S-1, then wait for slice 0
+  // prologue: the group's slices 0 .. S-1 into stages 0 .. S-1, then wait for slice 0
 #pragma unroll
-  for (int s = 0; s < S; ++s) dma_slice(s, lds + s * STAGE);
+  for (int s = 0; s < S; ++s) dma_slice(kg + (int64_t)KG * s, lds + s * STAGE);
   // bare barrier: __syncthreads() would also fence, i.e. wait for every load of the prologue
   wait_vmcnt<(S - 1) * NDMA>();
   __builtin_amdgcn_s_barrier();
@@ -525,7 +538,9 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
 
   constexpr int NMF = FM * FN, NRD = FM + FN;
   int cur_s = 0;
-  for (int64_t kt = 0; kt < nk; ++kt) {
+  const int64_t nkg = (nk + KG - 1) / KG;   // slices per group (past nk: zero slices)
+  for (int64_t it = 0; it < nkg; ++it) {
+    const int64_t kt = kg + KG * it;
     int8_t* cur = lds + cur_s * STAGE;
     const int nxt_s = cur_s + 1 == S ? 0 : cur_s + 1;
     const int8_t* nxt = lds + nxt_s * STAGE;
@@ -539,7 +554,7 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     // step 1
-    dma_slice(kt + S, cur);
+    dma_slice(kt + (int64_t)KG * S, cur);
     read_frags(nxt, 0, 0);
     mfmas(1);
     PinTwo<SG_VMEM_READ, NDMA, SG_DS_READ, NRD, NMF>::emit();
@@ -558,7 +573,45 @@ __global__ __launch_bounds__(WM * WN * 64) void mm_tile_kernel(const int8_t* __r
   static_assert(NW * 32 * PITCH <= S * STAGE, "staging does not fit in LDS");
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();                       // every wave is done with the K-loop's LDS stages
-  int8_t* stg = lds + wave * 32 * PITCH;
+  if constexpr (KG > 1) {
+    // groups 1 .. KG-1 hand their accumulators to group 0 through LDS, past group 0's staging area
+    constexpr int ACCB = FN * FM * 64 * 64;            // bytes of one wave's accumulators
+    constexpr int RED0 = ((NW * 32 * PITCH + 1023) / 1024) * 1024;
+    static_assert(RED0 + (KG - 1) * NW * ACCB <= KG * S * STAGE, "reduction does not fit in LDS");
+    if (kg > 0) {
+      int8_t* r = lds_all + RED0 + ((kg - 1) * NW + wave) * ACCB;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const i32x16 c = __builtin_bit_cast(i32x16, acc[j][i]);
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<i32x4*>(r + ((j * FM + i) * 4 + g) * 1024 + lane * 16) =
+                i32x4{c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
+        }
+    }
+    __syncthreads();
+    if (kg > 0) return;                  // no barrier follows
+#pragma unroll
+    for (int u = 1; u < KG; ++u) {
+      const int8_t* r = lds_all + RED0 + ((u - 1) * NW + wave) * ACCB;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            // the partner's values in their own type (float sums for bf16 operands): no bit casts of
+            // vector elements
+            using V4 = std::conditional_t<BFE, f32x4, i32x4>;
+            const V4 t = *reinterpret_cast<const V4*>(r + ((j * FM + i) * 4 + g) * 1024 + lane * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[j][i][4 * g + q] += t[q];
+          }
+    }
+  }
+  int8_t* stg = lds + wave * 32 * PITCH;     // group 0: lds == lds_all
   int calib = 0;
   // uniform: the whole tile is inside M x N and the output rows take CW-wide vector stores
   const bool full = m0 + BM <= M && n0 + BN <= N && (EPI == EPI_CALIB || e.vec_ok);
@@ -860,14 +913,15 @@ __global__ __launch_bounds__(W * 64) void mm_seg4_kernel(const int8_t* __restric
 
 // ------------------------------------------------------------------------------ dispatch
 struct TileCfg {
-  int bm, bn, waves;
+  int bm, bn, waves, kg;   // kg: K groups of `waves` waves each
 };
 
 // Tile ids (XDNA_TILE_* in the header): the tile engine's shapes, then the small-M kernel by waves.
 constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128x256 = 4, T_128x128 = 5,
               T_64x64 = 6, T_SMALL1 = 7, T_SMALL2 = 8, T_SMALL4 = 9, T_SMALL8 = 10, T_SMALL16 = 11,
               T_192x256 = 12, T_256x192 = 13, T_64x32 = 14, T_32x64 = 15, T_32x32 = 16, T_GEMV4 = 17,
-              T_GEMV2 = 18, T_GEMV8 = 19, T_SEG4R2 = 20, T_SEG4R4 = 21, T_COUNT = 22;
+              T_GEMV2 = 18, T_GEMV8 = 19, T_SEG4R2 = 20, T_SEG4R4 = 21, T_64x64K2 = 22, T_64x64K4 = 23,
+              T_32x64K4 = 24, T_32x32K4 = 25, T_128x128K2 = 26, T_COUNT = 27;
 
 static_assert(T_SMALL2 == T_SMALL1 + 1 && T_SMALL4 == T_SMALL1 + 2 && T_SMALL8 == T_SMALL1 + 3 &&
                   T_SMALL16 == T_SMALL1 + 4,
@@ -880,17 +934,22 @@ inline bool is_seg4(int t) { return t == T_SEG4R2 || t == T_SEG4R4; }
 
 inline TileCfg tile_cfg(int t) {
   switch (t) {
-    case T_256x256W8: return {256, 256, 8};
-    case T_256x256W4: return {256, 256, 4};
-    case T_256x128: return {256, 128, 4};
-    case T_128x256: return {128, 256, 4};
-    case T_128x128: return {128, 128, 4};
-    case T_192x256: return {192, 256, 4};
-    case T_256x192: return {256, 192, 4};
-    case T_64x32: return {64, 32, 2};
-    case T_32x64: return {32, 64, 2};
-    case T_32x32: return {32, 32, 1};
-    default: return {64, 64, 4};
+    case T_256x256W8: return {256, 256, 8, 1};
+    case T_256x256W4: return {256, 256, 4, 1};
+    case T_256x128: return {256, 128, 4, 1};
+    case T_128x256: return {128, 256, 4, 1};
+    case T_128x128: return {128, 128, 4, 1};
+    case T_192x256: return {192, 256, 4, 1};
+    case T_256x192: return {256, 192, 4, 1};
+    case T_64x32: return {64, 32, 2, 1};
+    case T_32x64: return {32, 64, 2, 1};
+    case T_32x32: return {32, 32, 1, 1};
+    case T_64x64K2: return {64, 64, 4, 2};
+    case T_64x64K4: return {64, 64, 4, 4};
+    case T_32x64K4: return {32, 64, 2, 4};
+    case T_32x32K4: return {32, 32, 1, 4};
+    case T_128x128K2: return {128, 128, 4, 2};
+    default: return {64, 64, 4, 1};
   }
 }
 
@@ -932,7 +991,10 @@ int tile_lookup(int kind, int64_t m, int64_t n, int64_t k) {
 //     the idle CUs;
 //   * otherwise, once 128 x 128 tiles fill three quarters of the CUs: 128 x 256 (four waves) for deep K
 //     when there are at least half a round of 256-wide tiles, else 128 x 128 (three workgroups per CU);
-//   * 64 x 64 for smaller problems.
+//   * smaller problems with deep K (at least 2 KB): tiles whose workgroups split K between wave groups,
+//     32 x 32 x 4 groups below an eighth of a round of 64 x 64 tiles, 32 x 64 x 4 groups up to half a
+//     round, 64 x 64 x 2 groups up to a round;
+//   * 64 x 64 otherwise.
 // A shape the tuned table lists uses the table's tile instead.
 int rule_tile(int64_t M, int64_t N, int64_t kbytes, bool small_ok) {
   if (small_ok && M == 1) return T_GEMV4;
@@ -945,6 +1007,12 @@ int rule_tile(int64_t M, int64_t N, int64_t kbytes, bool small_ok) {
   const bool deep = kbytes >= 4096;
   if (N > 128 && (2 * t256 >= 3 * cus || (deep && 4 * t256 >= 3 * cus))) return T_256x256W8;
   if (4 * t128 >= 3 * cus) return (N > 128 && deep && 2 * t256 >= cus) ? T_128x256 : T_128x128;
+  if (kbytes >= 2048) {
+    const int64_t t64 = ((M + 63) / 64) * ((N + 63) / 64);
+    if (8 * t64 < cus) return T_32x32K4;
+    if (2 * t64 <= cus) return T_32x64K4;
+    if (t64 <= cus) return T_64x64K2;
+  }
   return T_64x64;
 }
 
@@ -970,11 +1038,25 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
   const bool kfull = K % 64 == 0;
   // LDS stages per tile shape, from a measured sweep of 3 / 4 / 5 (and 4 / 8 / 12 for 64 x 64): 3 for
   // the large tiles (96 KB at 256 x 256; 48 KB at 128 x 128, three workgroups per CU), 4 for 64 x 64
-#define XDNA_TILE_W(BM_, BN_, WM_, WN_, S_)                                                                   \
-  if (kfull) mm_tile_kernel<BM_, BN_, WM_, WN_, S_, CONVM, EPI, true><<<grid, WM_ * WN_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e); \
-  else mm_tile_kernel<BM_, BN_, WM_, WN_, S_, CONVM, EPI, false><<<grid, WM_ * WN_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
+#define XDNA_TILE_WK(BM_, BN_, WM_, WN_, S_, KG_)                                                             \
+  if (kfull) mm_tile_kernel<BM_, BN_, WM_, WN_, S_, CONVM, EPI, true, KG_><<<grid, WM_ * WN_ * KG_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e); \
+  else mm_tile_kernel<BM_, BN_, WM_, WN_, S_, CONVM, EPI, false, KG_><<<grid, WM_ * WN_ * KG_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
+#define XDNA_TILE_W(BM_, BN_, WM_, WN_, S_) XDNA_TILE_WK(BM_, BN_, WM_, WN_, S_, 1)
 #define XDNA_TILE(BM_, BN_, S_) XDNA_TILE_W(BM_, BN_, 2, 2, S_)
-  if (t.bm == 256 && t.bn == 256 && t.waves == 8) {
+  if (t.kg > 1) {
+    // K groups (in-workgroup split-K) for tiles with few tiles and deep K
+    if (t.bm == 128) {
+      XDNA_TILE_WK(128, 128, 2, 2, 4, 2)
+    } else if (t.bm == 64 && t.kg == 2) {
+      XDNA_TILE_WK(64, 64, 2, 2, 4, 2)
+    } else if (t.bm == 64) {
+      XDNA_TILE_WK(64, 64, 2, 2, 4, 4)
+    } else if (t.bn == 64) {
+      XDNA_TILE_WK(32, 64, 1, 2, 4, 4)
+    } else {
+      XDNA_TILE_WK(32, 32, 1, 1, 4, 4)
+    }
+  } else if (t.bm == 256 && t.bn == 256 && t.waves == 8) {
     XDNA_TILE_W(256, 256, 2, 4, 3)
   } else if (t.bm == 256 && t.bn == 256) {
     XDNA_TILE(256, 256, 4)
@@ -999,6 +1081,7 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
   }
 #undef XDNA_TILE
 #undef XDNA_TILE_W
+#undef XDNA_TILE_WK
   return launch_status("mm_tile");
 }
 
@@ -1132,8 +1215,10 @@ int launch_conv(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad
     const int64_t bc = std::min(imgs, nb - b0);
     const EpiArgs eb = shift_epi(e, 1, b0 * h * w, 0);
     const int8_t* xb = x + b0 * per_img;
-    int rc = (c_pad % 64 == 0) ? launch_tiles<1, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st)
-                                : launch_tiles<2, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st);
+    // the running tap counters of CONVM 1 step by KG slices of 64 channels
+    int rc = (c_pad % (64 * tile_cfg(tile).kg) == 0)
+                 ? launch_tiles<1, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st)
+                 : launch_tiles<2, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st);
     if (rc) return rc;
   }
   return XDNA_OK;
