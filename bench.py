@@ -316,7 +316,8 @@ def traffic(workload):
 def gemm_kernels(dev, shapes):
     """The GEMM kernels the shapes launch (the library's tile choice per shape, tuned table applied)."""
     tiles = sorted({kernels.gemm_variant(dev, M, N, kernels.round_up(K, 16)) for M, N, K in shapes})
-    names = sorted({"mm_small_kernel" if t.startswith("small") else "mm_tile_kernel" for t in tiles})
+    kernel_of = {"small": "mm_small_kernel", "gemv": "mm_gemv_kernel", "seg4": "mm_seg4_kernel"}
+    names = sorted({kernel_of.get(t.split("_")[0], "mm_tile_kernel") for t in tiles})
     return f"{' + '.join(names)} (EPI_DQ): {', '.join(tiles)}"
 
 
