@@ -81,6 +81,8 @@ extern "C" {
 #define XDNA_TILE_32x64K4 24
 #define XDNA_TILE_32x32K4 25
 #define XDNA_TILE_128x128K2 26
+#define XDNA_TILE_128x256W8 27
+#define XDNA_TILE_256x128W8 28
 
 /* Library version (XDNA_ABI_VERSION). Replaces the import probe of kernels.available()
  * (torch_xdna/kernels.py:43-56): a loader checks it before trusting the other symbols. */

@@ -921,7 +921,7 @@ constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128
               T_64x64 = 6, T_SMALL1 = 7, T_SMALL2 = 8, T_SMALL4 = 9, T_SMALL8 = 10, T_SMALL16 = 11,
               T_192x256 = 12, T_256x192 = 13, T_64x32 = 14, T_32x64 = 15, T_32x32 = 16, T_GEMV4 = 17,
               T_GEMV2 = 18, T_GEMV8 = 19, T_SEG4R2 = 20, T_SEG4R4 = 21, T_64x64K2 = 22, T_64x64K4 = 23,
-              T_32x64K4 = 24, T_32x32K4 = 25, T_128x128K2 = 26, T_COUNT = 27;
+              T_32x64K4 = 24, T_32x32K4 = 25, T_128x128K2 = 26, T_128x256W8 = 27, T_256x128W8 = 28, T_COUNT = 29;
 
 static_assert(T_SMALL2 == T_SMALL1 + 1 && T_SMALL4 == T_SMALL1 + 2 && T_SMALL8 == T_SMALL1 + 3 &&
                   T_SMALL16 == T_SMALL1 + 4,
@@ -949,6 +949,8 @@ inline TileCfg tile_cfg(int t) {
     case T_32x64K4: return {32, 64, 2, 4};
     case T_32x32K4: return {32, 32, 1, 4};
     case T_128x128K2: return {128, 128, 4, 2};
+    case T_128x256W8: return {128, 256, 8, 1};
+    case T_256x128W8: return {256, 128, 8, 1};
     default: return {64, 64, 4, 1};
   }
 }
@@ -1056,6 +1058,10 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
     } else {
       XDNA_TILE_WK(32, 32, 1, 1, 4, 4)
     }
+  } else if (t.waves == 8 && t.bm == 128) {
+    XDNA_TILE_W(128, 256, 2, 4, 4)
+  } else if (t.waves == 8 && t.bn == 128) {
+    XDNA_TILE_W(256, 128, 4, 2, 4)
   } else if (t.bm == 256 && t.bn == 256 && t.waves == 8) {
     XDNA_TILE_W(256, 256, 2, 4, 3)
   } else if (t.bm == 256 && t.bn == 256) {
