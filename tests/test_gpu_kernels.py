@@ -389,6 +389,45 @@ def test_tiles_forced(gpu, tile, tile_table):
             assert kernels.conv3x3_calibrate(x_nhwc, packed.to(gpu), False) == int(np.abs(acc).max())
 
 
+@pytest.mark.parametrize("tile", ["t256x256w8", "t256x128w8", "t128x256"])
+def test_tiles_tail_split(gpu, tile, tile_table):
+    """A one-workgroup-per-CU tile whose last round of tiles would fill at most half of the CUs runs the
+    whole rounds with that tile and the leftover rows as a second launch (for the conv, from a pixel
+    offset into the same images): GEMM int32 sums and fused dequant, and the conv's requantized output,
+    with full and partial last tiles, against the oracle; the tail's tile as the library picks it and as
+    the tile table lists it for the tail's own shape."""
+    from torch_xdna import kernels
+
+    cus = kernels.num_cus(gpu)
+    bm, bn = (int(v) for v in tile[1:].split("w")[0].split("x"))
+    n, k = bn, 64
+    for m, tail in [(bm * (cus + cus // 4), None), (bm * (cus + cus // 4) - 100, None),
+                    (bm * (cus + cus // 4) - 100, "t64x64k2")]:
+        kernels.tile_set("i8", m, n, k, tile)
+        if tail:
+            kernels.tile_set("i8", m - bm * cus, n, k, tail)
+        a, w = _i8((m, k), seed=m), _i8((n, k), seed=n + 1)
+        acc = c_oracle.gemm_i32(a.numpy(), w.numpy())
+        assert np.array_equal(_np(kernels.mm_i8(a.to(gpu), w.to(gpu))), acc), (tile, m)
+        sx, sw = torch.rand(m) + 0.01, torch.rand(n) + 0.01
+        y = kernels.mm_i8_dequant(a.to(gpu), sx.to(gpu), w.to(gpu), sw.to(gpu), None, torch.float32)
+        assert np.array_equal(_f32(y), O.dequant(acc, sx.numpy(), sw.numpy())), (tile, m)
+    # conv: h * w pixels make 1.25 rounds of row tiles, less a partial last tile
+    ci, co = 64, bn
+    h, w_ = bm * (cus + cus // 4) // 320, 319
+    kernels.tile_set("conv", h * w_, co, 9 * ci, tile)
+    xq, wq = _i8((1, ci, h, w_), seed=h), _i8((co, ci, 3, 3), seed=co)
+    packed = wq.permute(0, 2, 3, 1).reshape(co, 9, ci).contiguous()
+    x_nhwc = kernels.nchw_to_nhwc(xq.to(gpu), ci)
+    acc = c_oracle.conv3x3_acc(xq.numpy(), wq.numpy())
+    want = O.requant(acc, 9, True)
+    for tail in (None, "t128x128k2"):       # a K-group tail takes the general A loader (64 % (2 * 64) != 0)
+        if tail:
+            kernels.tile_set("conv", h * w_ - bm * cus, co, 9 * ci, tail)
+        q = kernels.conv3x3(x_nhwc, packed.to(gpu), 9, True)
+        assert np.array_equal(_np(q).transpose(0, 3, 1, 2), want), (tile, tail, h, w_)
+
+
 @pytest.mark.parametrize("tile", ["small_w1", "small_w2", "small_w4", "small_w8", "small_w16", "t64x64", "t128x128"])
 def test_tiles_forced_decode(gpu, tile, tile_table):
     """Decode-sized and mid-sized GEMMs with a forced tile: the small-M kernel at every width (also

@@ -70,6 +70,7 @@ struct EpiArgs {
 
 struct ConvGeom {
   int64_t h, w, c_pad;  // NHWC input geometry
+  int64_t m0;           // pixel (within the launch's images) of the launch's row 0
 };
 
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
@@ -387,7 +388,10 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
   for (int jp = 0; jp < FN / CB; ++jp)
     cols_pre[jp] = EpiCols<EPI, CW>(e, n0 + wn * TN + jp * 32 * CB + (lane & 7) * CW, N);
 
-  const __amdgpu_buffer_rsrc_t ra_rsrc = make_rsrc(a, (uint32_t)(CONV ? (M * cg.c_pad) : (M * lda)));
+  // conv: the launch's rows lie in whole images that start at a; a 3 x 3 window reads past the launch's
+  // first and last rows within those images
+  const int64_t conv_px = CONV ? (cg.m0 + M + cg.h * cg.w - 1) / (cg.h * cg.w) * (cg.h * cg.w) : 0;
+  const __amdgpu_buffer_rsrc_t ra_rsrc = make_rsrc(a, (uint32_t)(CONV ? (conv_px * cg.c_pad) : (M * lda)));
   const __amdgpu_buffer_rsrc_t rw_rsrc = make_rsrc(w, (uint32_t)(N * ldw));
 
   // This lane's rows: DMA instruction j of this wave covers tile rows r0 = (wave * I + j) * 16 .. +16,
@@ -407,7 +411,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
     if constexpr (CONV) {
       // 32-bit: M * c_pad stays below 2^30 (the launcher splits larger batches)
       const uint32_t hw = (uint32_t)(cg.h * cg.w);
-      const uint32_t mm = m < M ? (uint32_t)m : 0u;
+      const uint32_t mm = m < M ? (uint32_t)(cg.m0 + m) : 0u;
       const uint32_t p = mm % hw;
       const uint32_t yy = p / (uint32_t)cg.w;
       py[j] = m < M ? (int)yy : -1000000;  // an invalid row fails every bounds test
@@ -1027,9 +1031,24 @@ int choose_tile(int kind, int64_t m, int64_t n, int64_t k, int64_t kbytes) {
 // Buffer resources address at most 2 GB; larger operands are processed in row chunks.
 constexpr int64_t MAX_BUF = 0x40000000;   // 1 GB per resource
 
+// Output pointer of row block m0 / column block n0 of an epilogue.
+inline EpiArgs shift_epi(const EpiArgs& e, int out_bytes, int64_t m0, int64_t n0) {
+  EpiArgs r = e;
+  if (r.out) r.out = reinterpret_cast<char*>(r.out) + (m0 * e.ldo + n0) * out_bytes;
+  if (r.sx) r.sx += m0;
+  if (r.sw) r.sw += n0;
+  if (r.bias) r.bias += n0;
+  return r;
+}
+
+template <int EPI>
+constexpr int out_bytes() {
+  return EPI == EPI_I32 ? 4 : EPI == EPI_DQ_F32 ? 4 : (EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16) ? 2 : 1;
+}
+
 template <int CONVM, int EPI>
-int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
-                 ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
+int launch_tiles_once(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                      ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
   const TileCfg t = tile_cfg(tile);
   const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   if (tiles >= (1ll << 31)) {
@@ -1091,19 +1110,48 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
   return launch_status("mm_tile");
 }
 
-// Output pointer of row block m0 / column block n0 of an epilogue.
-inline EpiArgs shift_epi(const EpiArgs& e, int out_bytes, int64_t m0, int64_t n0) {
-  EpiArgs r = e;
-  if (r.out) r.out = reinterpret_cast<char*>(r.out) + (m0 * e.ldo + n0) * out_bytes;
-  if (r.sx) r.sx += m0;
-  if (r.sw) r.sw += n0;
-  if (r.bias) r.bias += n0;
-  return r;
-}
-
-template <int EPI>
-constexpr int out_bytes() {
-  return EPI == EPI_I32 ? 4 : EPI == EPI_DQ_F32 ? 4 : (EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16) ? 2 : 1;
+// Tiles whose LDS (or registers) allow one workgroup per CU run in rounds of one tile per CU. When the
+// last round would leave more than half of the CUs idle, the whole rounds run with the chosen tile and
+// the rows left over as a second launch with a smaller tile: e.g. C4's conv (384 tiles of 256 x 256 on
+// 256 CUs) as 256 of them plus 256 tiles of 128 x 256 over the last third of the rows. Row r of the tail
+// launch is row m1 + r of the problem; for the conv that is a pixel offset (ConvGeom::m0) into the same
+// images.
+template <int CONVM, int EPI>
+int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                 ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
+  const TileCfg t = tile_cfg(tile);
+  const bool one_per_cu = t.kg == 1 && t.bm >= 128 && t.bn >= 128 && !(t.bm == 128 && t.bn == 128);
+  if (one_per_cu) {
+    const int64_t cus = device_cus();
+    const int64_t tm = (M + t.bm - 1) / t.bm, tn = (N + t.bn - 1) / t.bn;
+    const int64_t rounds = (tm * tn) / cus, rem = (tm * tn) % cus;
+    const int64_t tm_head = rounds * cus / tn;
+    if (rounds >= 1 && rem > 0 && 2 * rem <= cus && tm_head >= 1 && tm_head < tm) {
+      const int64_t m1 = tm_head * t.bm;
+      int rc = launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, m1, N, K, cg, e, tile, st);
+      if (rc) return rc;
+      ConvGeom ct = cg;
+      const int8_t* at = a;
+      if constexpr (CONVM != 0) ct.m0 += m1;
+      else at += m1 * lda;
+      // the tail's tile: the table's entry for the tail's own shape if it lists an engine tile; else after
+      // 256 x 256 tiles the 8-wave 128 x 256 tile (two of them per leftover tile: at most one round), else
+      // the rule. C4 (1 x 256 x 1536 x 64) measured 79.8 us unsplit, 72.7 us with a 128 x 128 tail (the
+      // rule's) and 69.4 us with the 128 x 256 one.
+      const int kind = CONVM != 0 ? XDNA_KIND_CONV : epi_bf(EPI) ? XDNA_KIND_BF16 : XDNA_KIND_I8;
+      int tail = tile_lookup(kind, M - m1, N, epi_bf(EPI) ? K / 2 : K);
+      if (is_small(tail) || is_gemv(tail) || is_seg4(tail)) tail = T_AUTO;
+      if (tail == T_AUTO) tail = tile == T_256x256W8 ? T_128x256W8 : rule_tile(M - m1, N, K, false);
+      const EpiArgs et = shift_epi(e, out_bytes<EPI>(), m1, 0);
+      // the tail's tile may split K over groups: CONVM 1 needs c_pad to be a multiple of its groups' slices
+      if constexpr (CONVM != 0) {
+        if (cg.c_pad % (64 * tile_cfg(tail).kg) != 0)
+          return launch_tiles_once<2, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, tail, st);
+      }
+      return launch_tiles_once<CONVM, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, tail, st);
+    }
+  }
+  return launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, M, N, K, cg, e, tile, st);
 }
 
 template <int EPI>
