@@ -17,6 +17,8 @@ configs; seed 0), with inputs and device-resident int8 weights already in HBM:
   quant         the activation quantize kernel alone, bf16 [8192, 14336].
   bf16          precision "bf16" on the C2 shapes: the bf16 MFMA GEMM (bf16 in / out, float32 sums).
   copy          calibration of the HBM byte counters (a 1 GiB read + 1 GiB write elementwise kernel).
+  mfma          the int8 MFMA issue ceiling: register-only 32x32x32 int8 MFMAs on every SIMD with
+                constant and with random operands (libxdna_probe.so), and the shader clock held.
 
 Weight / activation sets are rotated so a step's working set exceeds the 256 MB MALL. Timing:
 W untimed steps, then K steps bracketed by torch.cuda.synchronize(); the dominant kernel is also
@@ -55,7 +57,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "decode", "quant", "bf16", "vgg16",
-                                                          "stack", "copy"])
+                                                          "stack", "copy", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -199,7 +201,7 @@ def main():
            "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic (seed 0, randn)"}
     bench = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
              "decode": bench_decode, "quant": bench_quant, "bf16": bench_bf16, "vgg16": bench_vgg16,
-             "stack": bench_stack, "copy": bench_copy}[a.workload]
+             "stack": bench_stack, "copy": bench_copy, "mfma": bench_mfma}[a.workload]
     res.update(bench(a, dev))
     print(json.dumps(res), flush=True)
 
@@ -498,6 +500,44 @@ def bench_copy(a, dev):
             "config": {"workload": "bitwise_not int32 [2^28]: reads 1 GiB, writes 1 GiB"},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": b, "kernel": "torch elementwise"}}
+
+
+def bench_mfma(a, dev):
+    """The int8 MFMA issue ceiling of the device: every SIMD runs back-to-back 32x32x32 int8 MFMAs on
+    registers only (libxdna_probe.so), once with constant operands and once with random bytes, the
+    data a GEMM feeds them. value: the random-operand rate; the clock: s_memtime shader cycles of the
+    last launch over its duration. With random operands the power limit lowers the clock, which
+    bounds every int8 GEMM on the device below the nominal 5.0 POP/s."""
+    import ctypes
+    L = ctypes.CDLL(os.path.join(os.path.dirname(kernels.LIB_PATH), "libxdna_probe.so"))
+    L.xdna_probe_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint32, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p]
+    L.xdna_probe_mfma_i8.restype = ctypes.c_int
+    blocks, iters = kernels.num_cus(dev), 10000
+    out = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    cyc = torch.zeros(blocks, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def run(random_operands, seed):
+        rc = L.xdna_probe_mfma_i8(blocks, iters, random_operands, seed, out.data_ptr(), cyc.data_ptr(), stream)
+        if rc:
+            raise RuntimeError(f"xdna_probe_mfma_i8: HIP error {rc}")
+
+    macs = blocks * 4 * iters * 16 * 32 * 32 * 32
+    res = {}
+    for rnd in (0, 1):
+        sec, host = timed_steps(a, lambda i, tm: run(rnd, i), None)
+        ghz = float(cyc.double().mean()) / sec / 1e9
+        res[rnd] = (2 * macs / sec / 1e12, ghz, sec, host)
+    tops, ghz, sec, host = res[1]
+    return {"metric": "int8 MFMA issue ceiling TOPS on 1 MI355X (register-only, random operands)", "unit": "TOPS",
+            "dtype": "int8", "value": round(tops, 1), "ms_per_step": round(sec * 1e3, 4),
+            "host_ms_per_step": round(host * 1e3, 4), "clock_ghz": round(ghz, 3),
+            "constant_operands": {"value": round(res[0][0], 1), "clock_ghz": round(res[0][1], 3)},
+            "config": {"workload": f"{blocks} workgroups x 4 waves, {iters} x 16 v_mfma_i32_32x32x32_i8 per wave"},
+            "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                         "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": 0, "kernel": "mfma_ceiling_kernel<true>",
+                         "avg_launch_us": round(sec * 1e6, 2)}}
 
 
 def conv_layer_data(dev, n, c, h, w, seed=0):

@@ -43,6 +43,21 @@ def test_library_exports_every_declared_symbol(lib):
     assert sorted(kernels.EXPORTS) == declared()
 
 
+def test_probe_library():
+    """The measurement probe behind bench.py's `mfma` workload is its own library, exporting only the
+    probe entry point (it adds nothing to the hot path's ABI); bad arguments are rejected on the host."""
+    from torch_xdna import kernels
+
+    path = os.path.join(os.path.dirname(kernels.LIB_PATH), "libxdna_probe.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    assert set(re.findall(r"\bT (xdna_\w+)$", out, re.M)) == {"xdna_probe_mfma_i8"}
+    L = ctypes.CDLL(path)
+    L.xdna_probe_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint32, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p]
+    assert L.xdna_probe_mfma_i8(0, 1, 1, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), None) != 0
+    assert L.xdna_probe_mfma_i8(1, 1, 1, 0, None, ctypes.c_void_p(16), None) != 0
+
+
 def test_abi_version(lib):
     from torch_xdna import kernels
 
