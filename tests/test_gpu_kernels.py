@@ -393,25 +393,33 @@ def test_tiles_forced(gpu, tile, tile_table):
 def test_tiles_tail_split(gpu, tile, tile_table):
     """A one-workgroup-per-CU tile whose last round of tiles would fill at most half of the CUs runs the
     whole rounds with that tile and the leftover rows as a second launch (for the conv, from a pixel
-    offset into the same images): GEMM int32 sums and fused dequant, and the conv's requantized output,
-    with full and partial last tiles, against the oracle; the tail's tile as the library picks it and as
-    the tile table lists it for the tail's own shape."""
+    offset into the same images), when the leftover rows fit one round of the tail's tile: the int8
+    GEMM's int32 sums and fused dequant, the bf16 GEMM and the conv's requantized output, with full and
+    partial last tiles, against the oracle; the tail's tile as the library picks it (a split after
+    256 x 256 tiles, none after the others at these shapes) and as the tile table lists it for the
+    tail's own shape (a K-group tile: its own loader for the conv)."""
     from torch_xdna import kernels
 
     cus = kernels.num_cus(gpu)
     bm, bn = (int(v) for v in tile[1:].split("w")[0].split("x"))
     n, k = bn, 64
     for m, tail in [(bm * (cus + cus // 4), None), (bm * (cus + cus // 4) - 100, None),
-                    (bm * (cus + cus // 4) - 100, "t64x64k2")]:
-        kernels.tile_set("i8", m, n, k, tile)
-        if tail:
-            kernels.tile_set("i8", m - bm * cus, n, k, tail)
+                    (bm * (cus + cus // 4) - 100, "t128x128k2")]:
+        m1 = bm * cus
+        for kind, kk in (("i8", k), ("bf16", k)):
+            kernels.tile_set(kind, m, n, kk, tile)
+            kernels.tile_set(kind, m - m1, n, kk, tail or "auto")
         a, w = _i8((m, k), seed=m), _i8((n, k), seed=n + 1)
         acc = c_oracle.gemm_i32(a.numpy(), w.numpy())
-        assert np.array_equal(_np(kernels.mm_i8(a.to(gpu), w.to(gpu))), acc), (tile, m)
+        assert np.array_equal(_np(kernels.mm_i8(a.to(gpu), w.to(gpu))), acc), (tile, m, tail)
         sx, sw = torch.rand(m) + 0.01, torch.rand(n) + 0.01
         y = kernels.mm_i8_dequant(a.to(gpu), sx.to(gpu), w.to(gpu), sw.to(gpu), None, torch.float32)
-        assert np.array_equal(_f32(y), O.dequant(acc, sx.numpy(), sw.numpy())), (tile, m)
+        assert np.array_equal(_f32(y), O.dequant(acc, sx.numpy(), sw.numpy())), (tile, m, tail)
+        x = _rand((m, k), torch.float32, seed=m)
+        wf = _rand((n, k), torch.float32, seed=n, scale=0.05)
+        yb = kernels.mm_bf16(kernels.bf16_rows(x.to(gpu), k), kernels.bf16_rows(wf.to(gpu), k), None, torch.float32)
+        want, bound = O.gemm_bf16(x.numpy(), wf.numpy())
+        _bf16_bracket(_f32(yb), want, bound, "f32")
     # conv: h * w pixels make 1.25 rounds of row tiles, less a partial last tile
     ci, co = 64, bn
     h, w_ = bm * (cus + cus // 4) // 320, 319
@@ -422,8 +430,7 @@ def test_tiles_tail_split(gpu, tile, tile_table):
     acc = c_oracle.conv3x3_acc(xq.numpy(), wq.numpy())
     want = O.requant(acc, 9, True)
     for tail in (None, "t128x128k2"):       # a K-group tail takes the general A loader (64 % (2 * 64) != 0)
-        if tail:
-            kernels.tile_set("conv", h * w_ - bm * cus, co, 9 * ci, tail)
+        kernels.tile_set("conv", h * w_ - bm * cus, co, 9 * ci, tail or "auto")
         q = kernels.conv3x3(x_nhwc, packed.to(gpu), 9, True)
         assert np.array_equal(_np(q).transpose(0, 3, 1, 2), want), (tile, tail, h, w_)
 
@@ -546,6 +553,9 @@ def test_sweep_tool(gpu, tile_table, tmp_path):
     assert len(recs) == n_lines == want
     assert all(r["status"] == "ok" and r["exact"] and r["gpu_us"] > 0 for r in recs), recs
     assert {r["checked_against"] for r in recs} == {"cpu"}
+    out2 = str(tmp_path / "sweep_tiles.jsonl")           # --tiles: only the named tiles
+    sweep.main(["--kind", "i8", "--rows", "300", "--shapes", "520x256", "--tiles", "t64x64", "t32x32k4", "--out", out2])
+    assert sorted(json.loads(line)["tiling"] for line in open(out2)) == ["t32x32k4", "t64x64"]
     table_path = str(tmp_path / "tuned.json")
     sweep.main(["--summary", out, "--table", table_path])
     doc = json.load(open(table_path))

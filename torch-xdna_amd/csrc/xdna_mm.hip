@@ -1041,9 +1041,12 @@ inline EpiArgs shift_epi(const EpiArgs& e, int out_bytes, int64_t m0, int64_t n0
   return r;
 }
 
+// Bytes of one output element: int32 sums and float32 results 4, bf16 / fp16 2, requantized int8 1.
 template <int EPI>
 constexpr int out_bytes() {
-  return EPI == EPI_I32 ? 4 : EPI == EPI_DQ_F32 ? 4 : (EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16) ? 2 : 1;
+  return (EPI == EPI_I32 || EPI == EPI_DQ_F32 || EPI == EPI_BF_F32) ? 4
+         : (EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16 || EPI == EPI_BF_BF16 || EPI == EPI_BF_F16) ? 2
+                                                                                               : 1;
 }
 
 template <int CONVM, int EPI>
@@ -1121,37 +1124,39 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
                  ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
   const TileCfg t = tile_cfg(tile);
   const bool one_per_cu = t.kg == 1 && t.bm >= 128 && t.bn >= 128 && !(t.bm == 128 && t.bn == 128);
-  if (one_per_cu) {
-    const int64_t cus = device_cus();
-    const int64_t tm = (M + t.bm - 1) / t.bm, tn = (N + t.bn - 1) / t.bn;
-    const int64_t rounds = (tm * tn) / cus, rem = (tm * tn) % cus;
-    const int64_t tm_head = rounds * cus / tn;
-    if (rounds >= 1 && rem > 0 && 2 * rem <= cus && tm_head >= 1 && tm_head < tm) {
-      const int64_t m1 = tm_head * t.bm;
-      int rc = launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, m1, N, K, cg, e, tile, st);
-      if (rc) return rc;
-      ConvGeom ct = cg;
-      const int8_t* at = a;
-      if constexpr (CONVM != 0) ct.m0 += m1;
-      else at += m1 * lda;
-      // the tail's tile: the table's entry for the tail's own shape if it lists an engine tile; else after
-      // 256 x 256 tiles the 8-wave 128 x 256 tile (two of them per leftover tile: at most one round), else
-      // the rule. C4 (1 x 256 x 1536 x 64) measured 79.8 us unsplit, 72.7 us with a 128 x 128 tail (the
-      // rule's) and 69.4 us with the 128 x 256 one.
-      const int kind = CONVM != 0 ? XDNA_KIND_CONV : epi_bf(EPI) ? XDNA_KIND_BF16 : XDNA_KIND_I8;
-      int tail = tile_lookup(kind, M - m1, N, epi_bf(EPI) ? K / 2 : K);
-      if (is_small(tail) || is_gemv(tail) || is_seg4(tail)) tail = T_AUTO;
-      if (tail == T_AUTO) tail = tile == T_256x256W8 ? T_128x256W8 : rule_tile(M - m1, N, K, false);
-      const EpiArgs et = shift_epi(e, out_bytes<EPI>(), m1, 0);
-      // the tail's tile may split K over groups: CONVM 1 needs c_pad to be a multiple of its groups' slices
-      if constexpr (CONVM != 0) {
-        if (cg.c_pad % (64 * tile_cfg(tail).kg) != 0)
-          return launch_tiles_once<2, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, tail, st);
-      }
-      return launch_tiles_once<CONVM, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, tail, st);
-    }
+  if (!one_per_cu) return launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, M, N, K, cg, e, tile, st);
+  const int64_t cus = device_cus();
+  const int64_t tm = (M + t.bm - 1) / t.bm, tn = (N + t.bn - 1) / t.bn;
+  const int64_t rounds = (tm * tn) / cus, rem = (tm * tn) % cus;
+  const int64_t tm_head = rounds * cus / tn;
+  if (!(rounds >= 1 && rem > 0 && 2 * rem <= cus && tm_head >= 1 && tm_head < tm))
+    return launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, M, N, K, cg, e, tile, st);
+  const int64_t m1 = tm_head * t.bm;
+  // the tail's tile: the table's entry for the tail's own shape if it lists an engine tile; else after
+  // 256 x 256 tiles the 8-wave 128 x 256 tile, else the rule. C4 (1 x 256 x 1536 x 64) measured 79.8 us
+  // unsplit, 72.7 us with a 128 x 128 tail (the rule's) and 69.4 us with the 128 x 256 one.
+  const int kind = CONVM != 0 ? XDNA_KIND_CONV : epi_bf(EPI) ? XDNA_KIND_BF16 : XDNA_KIND_I8;
+  int tail = tile_lookup(kind, M - m1, N, epi_bf(EPI) ? K / 2 : K);
+  if (is_small(tail) || is_gemv(tail) || is_seg4(tail)) tail = T_AUTO;
+  if (tail == T_AUTO) tail = tile == T_256x256W8 ? T_128x256W8 : rule_tile(M - m1, N, K, false);
+  // only when the leftover rows fit one round of the tail's tiles (8192 x 3072 in 256 x 256 tiles leaves
+  // 2816 rows, 264 tiles of 128 x 256: measured slower split than not)
+  const TileCfg tt = tile_cfg(tail);
+  if (((M - m1 + tt.bm - 1) / tt.bm) * ((N + tt.bn - 1) / tt.bn) > cus)
+    return launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, M, N, K, cg, e, tile, st);
+
+  int rc = launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, m1, N, K, cg, e, tile, st);
+  if (rc) return rc;
+  ConvGeom ct = cg;
+  const int8_t* at = a;
+  if constexpr (CONVM != 0) ct.m0 += m1;
+  else at += m1 * lda;
+  const EpiArgs et = shift_epi(e, out_bytes<EPI>(), m1, 0);
+  // the tail's tile may split K over groups: CONVM 1 needs c_pad to be a multiple of its groups' slices
+  if constexpr (CONVM != 0) {
+    if (cg.c_pad % (64 * tt.kg) != 0) return launch_tiles_once<2, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, tail, st);
   }
-  return launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, M, N, K, cg, e, tile, st);
+  return launch_tiles_once<CONVM, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, tail, st);
 }
 
 template <int EPI>

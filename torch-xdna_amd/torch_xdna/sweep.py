@@ -13,7 +13,7 @@ weight-streaming shapes (up to 256 rows) cycle through copies of the weight that
 
 usage: python -m torch_xdna.sweep [--kind i8|bf16|conv] [--rows 128 512 1024 3000]
                                   [--shapes 4096x1024 ...] [--convs 1x256x256x64x64 ...]
-                                  [--out sweep.jsonl]
+                                  [--tiles t256x256w8 ...] [--out sweep.jsonl]
        python -m torch_xdna.sweep --summary sweep.jsonl [--table torch_xdna/tuned/mi355x.json]
 
 Shapes: GEMMs as NxK (with --rows M), convs as NxCixCoxHxW. The table keeps, per shape, the fastest
@@ -157,8 +157,9 @@ def _agrees(got, want, how):
     return bool(torch.isfinite(got).all()) and float((got - want).norm() / want.norm().clamp(min=1e-30)) < 5e-2
 
 
-def sweep_shape(kind, M, N, K, dev, case, done, out):
-    """Every candidate tile of one shape: JSONL lines appended to `out` (skipping those in `done`)."""
+def sweep_shape(kind, M, N, K, dev, case, done, out, tiles=None):
+    """Every candidate tile of one shape (those in `tiles` if given): JSONL lines appended to `out`
+    (skipping those in `done`)."""
     bench, exact, want, how, ops = case
     kernels.tile_set(kind, M, N, K, "auto")
     rule = kernels.tile_get(dev, kind, M, N, K)
@@ -166,7 +167,7 @@ def sweep_shape(kind, M, N, K, dev, case, done, out):
     if want is None:               # too large for the CPU: the rule's tile is the reference
         want, ref_kind = exact(), "rule"
     for tile in candidates(kind, M):
-        if (kind, M, N, K, tile) in done:
+        if (kind, M, N, K, tile) in done or (tiles is not None and tile not in tiles):
             continue
         rec = {"kind": kind, "M": M, "N": N, "K": K, "tiling": tile, "rule": rule, "checked_against": ref_kind}
         try:
@@ -184,7 +185,7 @@ def sweep_shape(kind, M, N, K, dev, case, done, out):
         print(json.dumps(rec), flush=True)
 
 
-def sweep(kind, rows, shapes, convs, out_path):
+def sweep(kind, rows, shapes, convs, out_path, tiles=None):
     assert kernels.available(), kernels.unavailable_reason()
     dev = torch.device("cuda", torch.cuda.current_device())
     done = set()
@@ -198,12 +199,12 @@ def sweep(kind, rows, shapes, convs, out_path):
         if kind == "conv":
             for n, ci, co, h, w in convs:
                 case = _conv_case(n, ci, co, h, w, dev)
-                sweep_shape("conv", n * h * w, co, 9 * kernels.round_up(ci, 16), dev, case, done, out)
+                sweep_shape("conv", n * h * w, co, 9 * kernels.round_up(ci, 16), dev, case, done, out, tiles)
         else:
             for N, K in shapes:
                 for M in rows:
                     Kp = kernels.round_up(K, 16)
-                    sweep_shape(kind, M, N, Kp, dev, _gemm_case(kind, M, N, Kp, dev), done, out)
+                    sweep_shape(kind, M, N, Kp, dev, _gemm_case(kind, M, N, Kp, dev), done, out, tiles)
 
 
 def summarize(path):
@@ -238,6 +239,8 @@ def main(argv=None):
     ap.add_argument("--rows", type=int, nargs="*", default=GEMM_ROWS)
     ap.add_argument("--shapes", nargs="*", default=[f"{n}x{k}" for n, k in GEMM_SHAPES])
     ap.add_argument("--convs", nargs="*", default=["x".join(map(str, c)) for c in CONV_SHAPES])
+    ap.add_argument("--tiles", nargs="*", choices=[t for t in kernels.TILES if t != "auto"],
+                    help="sweep only these tiles (default: every candidate)")
     ap.add_argument("--out", default="sweep.jsonl")
     ap.add_argument("--summary", metavar="JSONL")
     ap.add_argument("--table", metavar="JSON", help="with --summary: merge the result into this tuned table")
@@ -264,7 +267,7 @@ def main(argv=None):
         return 0
     shapes = [tuple(int(v) for v in s.split("x")) for s in a.shapes]
     convs = [tuple(int(v) for v in s.split("x")) for s in a.convs]
-    sweep(a.kind, a.rows, shapes, convs, a.out)
+    sweep(a.kind, a.rows, shapes, convs, a.out, set(a.tiles) if a.tiles else None)
     return 0
 
 
