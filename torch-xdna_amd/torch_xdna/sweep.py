@@ -31,8 +31,9 @@ import torch
 
 from . import kernels
 
-# BASELINE shapes: C1, C2 (Qwen3-0.6B linear_cat qkv / gate-up / down), C5 (K=4096 / 14336)
-GEMM_SHAPES = [(3072, 1024), (4096, 1024), (6144, 1024), (1024, 3072), (14336, 4096), (4096, 14336)]
+# BASELINE shapes: C1, C2 (Qwen3-0.6B linear_cat qkv / gate-up / down), C5 (K=4096 with N 4096 / 14336,
+# K=14336 with N 4096)
+GEMM_SHAPES = [(3072, 1024), (4096, 1024), (6144, 1024), (1024, 3072), (4096, 4096), (14336, 4096), (4096, 14336)]
 GEMM_ROWS = [1, 16, 128, 256, 512, 1024, 2048, 3000, 8192]
 # C3, C4 and the VGG-16 layers at batch 8
 CONV_SHAPES = [(1, 256, 256, 64, 64), (1, 256, 256, 1536, 64), (8, 3, 64, 224, 224), (8, 64, 64, 224, 224),
