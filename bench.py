@@ -1,33 +1,42 @@
 """Benchmark of the int8 hot path on one MI355X: W8A8 GEMM and int8 conv3x3 TOPS vs the rooflines.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c1|c3|c4|c5|quant]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|c1|c2|c3|c4|c5|...]
 
 One step is one pass of the hot path over one batch of synthetic, seeded input (BASELINE.json
 configs; seed 0), with inputs and device-resident int8 weights already in HBM:
 
-  c2 (default)  Qwen3-0.6B projections as xdna::linear_cat runs them on the GPU: for M in
-                {128, 512, 1024, 3000}, bf16 x -> quantize -> int8 MFMA GEMM with the fused
-                dequantize epilogue -> bf16, for qkv (N 4096, K 1024), gate/up (N 6144, K 1024) and
-                down (N 1024, K 3072): 12 GEMMs + 12 quantizes per step.
+  headline (default)  the largest single-GPU config, C5's M=8192 W8A8 linear: bf16 x [8192, 4096]
+                with 0.1% outliers x20 -> per-row quantize -> int8 MFMA GEMM against the int8
+                weight [14336, 4096] with the dequantize + bias fused into its epilogue -> bf16 y.
+                The same JSON line carries sub-records, each with its own roofline and CPU
+                baseline: C4's 256-channel conv at 1x256x1536x64 and 8x256x256x256 run as the op
+                (xdna::conv3x3_fused: per-image quantize -> conv with the calibrated shift ->
+                dequantize, ReLU fused), with the conv kernel's back-to-back time beside it, and C2.
+  c2            Qwen3-0.6B projections as xdna::linear_cat runs them on the GPU: for M in
+                {128, 512, 1024, 3000}, bf16 x -> quantize -> fused GEMM -> bf16, for qkv
+                (N 4096, K 1024), gate/up (N 6144, K 1024) and down (N 1024, K 3072).
   c1            one W8A8 linear, fp32 x [128, 1024], W [3072, 1024], bias.
-  c3            4 x (conv3x3 + ReLU), 256 ch, 1x256x64x64, quantize -> conv -> dequantize per layer.
-  c4            conv3x3 256->256 on 1x256x1536x64 (int8 conv kernel, the shift already fixed).
-  c5            W8A8 GEMM, bf16 in/out with bias, K 4096 N 14336 M 8192 (the largest config).
+  c3            4 x (conv3x3 + ReLU), 256 ch, 1x256x64x64, chained on the GPU.
+  c4            C4's two 256-channel convs as the op (the headline's sub-records alone).
+  c5            the headline's main record alone.
   decode        the C5 decode GEMMs (M 1 and 16), HBM-bound: roofline in GB/s of algorithmic bytes.
   quant         the activation quantize kernel alone, bf16 [8192, 14336].
   bf16          precision "bf16" on the C2 shapes: the bf16 MFMA GEMM (bf16 in / out, float32 sums).
+  vgg16         VGG-16 features at batch 8 through torch.compile(backend="xdna"), convs chained.
+  stack         xdna::qwen3_stack on OmniVoice's step shapes.
   copy          calibration of the HBM byte counters (a 1 GiB read + 1 GiB write elementwise kernel).
-  mfma          the int8 MFMA issue ceiling: register-only 32x32x32 int8 MFMAs on every SIMD with
-                constant and with random operands (libxdna_probe.so), and the shader clock held.
 
 Weight / activation sets are rotated so a step's working set exceeds the 256 MB MALL. Timing:
 W untimed steps, then K steps bracketed by torch.cuda.synchronize(); the dominant kernel is also
 timed per launch with HIP events on the stream it runs on (torch's current stream). The timed
 steps are enqueued behind a GPU spin kernel that outlasts the host's enqueue time, so they run back
 to back and the events measure GPU time only; the ungated wall-clock time per step (host launch
-cost included) is reported beside it. Rank 0 prints one JSON line. The CPU baseline is the reference's CPU route (oracle/cpu_route.py: torch CPU
-quantize, torch._int_mm or an exact float conv, dequantize) timed on the host cores on a bounded
-sample of the same workload.
+cost included) is reported beside it. Rank 0 prints one JSON line.
+
+CPU baseline: the reference's CPU route (oracle/cpu_route.py: torch CPU quantize, torch._int_mm or
+an exact float conv of the integers, dequantize) on the GPU box's host cores, timed by the
+reference's protocol (tools/cpu_baseline.py:14-26: 5 warm-up runs, then 60 timed runs, min / p25 /
+median), with the thread count and the CPU model; each record says what its sample is.
 """
 
 import argparse
@@ -49,6 +58,8 @@ PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, TOP/s (5.0 POP/s)
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, TFLOP/s
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
 MALL_BYTES = 256 << 20
+METRIC = "W8A8 GEMM & int8 conv3x3 TOPS on 1 MI355X; % of int8 MFMA peak / HBM BW"
+WORKLOADS = ["headline", "c1", "c2", "c3", "c4", "c5", "decode", "quant", "bf16", "vgg16", "stack", "copy"]
 
 
 def parse():
@@ -56,8 +67,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "decode", "quant", "bf16", "vgg16",
-                                                          "stack", "copy", "mfma"])
+    ap.add_argument("--workload", default="headline", choices=WORKLOADS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -68,7 +78,8 @@ def gen(seed):
 
 # ------------------------------------------------------------------------------ GEMM workloads
 def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed=0):
-    """Per set: for each (M, N, K): x [M, K], quantized weight [N, K] + sw (+ bias) on the GPU."""
+    """Per set: for each (M, N, K): x [M, K] (0.1% outliers x20), quantized weight [N, K] + sw
+    (+ bias) on the GPU."""
     g = gen(seed)
     per_set = sum(M * K * x_dtype.itemsize + N * K + M * N * 2 + M * K for M, N, K in shapes)
     nsets = max(nsets_min, -(-(MALL_BYTES + (64 << 20)) // per_set))
@@ -89,8 +100,8 @@ def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed
 
 def run_gemm_step_split(items, ev=None):
     """One step ordered as all activation quantizes, then all fused GEMMs (the same work as
-    run_gemm_step); ev = three events recorded at the start, between the two groups and at the end,
-    so ev[1] -> ev[2] brackets exactly the step's GEMM launches, back to back."""
+    quantize -> GEMM per shape); ev = three events recorded at the start, between the two groups and
+    at the end, so ev[1] -> ev[2] brackets exactly the step's GEMM launches, back to back."""
     if ev:
         ev[0].record()
     qs = [kernels.quant_rows(x) for x, *_ in items]
@@ -100,15 +111,6 @@ def run_gemm_step_split(items, ev=None):
         kernels.mm_i8_dequant(xq, sx, wq, sw, b, x.dtype)
     if ev:
         ev[2].record()
-
-
-def run_gemm_step(items, timer=None, qtimer=None):
-    for x, wq, sw, b, M, N, K in items:
-        xq, sx = qtimer(kernels.quant_rows, x) if qtimer else kernels.quant_rows(x)
-        if timer:
-            timer(kernels.mm_i8_dequant, xq, sx, wq, sw, b, x.dtype)
-        else:
-            kernels.mm_i8_dequant(xq, sx, wq, sw, b, x.dtype)
 
 
 def gemm_bytes(M, N, K, xbytes, ybytes, bias):
@@ -121,15 +123,50 @@ def quant_bytes(M, K, xbytes):
 
 
 # ------------------------------------------------------------------------------ CPU baseline
-def cpu_baseline_gemm(shapes, x_dtype, bias, budget_s=15.0):
-    """The reference CPU route (oracle/cpu_route.py) on the same shapes: 5 warm-up, then reps until
-    about budget_s, min of the per-step times (tools/cpu_baseline.py:14-26 protocol)."""
+def cpu_model():
+    """The host CPU's model string (BASELINE.md asks for it beside every CPU number)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def cpu_protocol(step, ops, sample, budget_s=20.0, warmup=5, reps=60):
+    """Times `step` by the reference's protocol (tools/cpu_baseline.py:14-26): `warmup` untimed runs,
+    then `reps` timed runs (fewer when they would exceed budget_s, at least 10), min / p25 / median.
+    value = ops / min time, in TOPS (or TFLOP/s for a float route)."""
+    for _ in range(warmup):
+        step()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < reps and (time.perf_counter() < t_end or len(ts) < 10):
+        t = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t)
+    ts.sort()
+    rank = lambda p: ts[int(p * len(ts))]   # noqa: E731  (ts[15] / ts[30] of 60, as the reference)
+    return {"value": round(ops / ts[0] / 1e12, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": sample, "cpu_model": cpu_model(), "warmup": warmup, "reps": len(ts),
+            "min_ms": round(ts[0] * 1e3, 3), "p25_ms": round(rank(0.25) * 1e3, 3),
+            "median_ms": round(rank(0.5) * 1e3, 3)}
+
+
+def cpu_baseline_gemm(shapes, x_dtype, bias, label, budget_s=20.0):
+    """The reference's CPU route (oracle/cpu_route.py: quantize, torch._int_mm, dequantize + bias) on
+    the same shapes, one step per timed run."""
     from oracle import cpu_route
 
     g = gen(1)
     data = []
     for M, N, K in shapes:
-        x = torch.randn(M, K, generator=g).to(x_dtype)
+        x = torch.randn(M, K, generator=g)
+        x = torch.where(torch.rand(M, K, generator=g) < 1e-3, x * 20, x).to(x_dtype)
         w = torch.randn(N, K, generator=g) * 0.02
         b = torch.randn(N, generator=g) * 0.01 if bias else None
         w_kn, sw = cpu_route.weight_quant(w)
@@ -139,28 +176,21 @@ def cpu_baseline_gemm(shapes, x_dtype, bias, budget_s=15.0):
         for x, w_kn, sw, b in data:
             cpu_route.linear(x, w_kn, sw, b)
 
-    for _ in range(2):
-        step()
-    ts = []
-    t_end = time.perf_counter() + budget_s
-    while len(ts) < 60 and (time.perf_counter() < t_end or len(ts) < 3):
-        t = time.perf_counter()
-        step()
-        ts.append(time.perf_counter() - t)
-    ts.sort()
     ops = sum(2 * M * N * K for M, N, K in shapes)
-    return ops / ts[0] / 1e12, len(ts), ts[0]
+    return cpu_protocol(step, ops, f"{label}: the full step (torch CPU quantize + torch._int_mm + dequantize"
+                        + (" + bias" if bias else "") + ")", budget_s)
 
 
-def cpu_baseline_conv(n, c, h, w, layers, relu=True, budget_s=15.0):
+def cpu_baseline_conv(n, c, h, w, layers, sample, relu=True, budget_s=20.0):
+    """The reference's CPU conv route (quantize per image, exact float conv of the integers, shift /
+    round / saturate, dequantize) over `layers` layers of c -> c channels on [n, c, h, w]; the shift
+    of each layer is fixed on the first run (a warm-up run), as the reference fixes it on the first
+    call."""
     from oracle import cpu_route
 
     g = gen(1)
     x = torch.randn(n, c, h, w, generator=g)
-    convs = []
-    for _ in range(layers):
-        L = cpu_route.ConvLayerCPU(torch.randn(c, c, 3, 3, generator=g) * 0.02, relu)
-        convs.append(L)
+    convs = [cpu_route.ConvLayerCPU(torch.randn(c, c, 3, 3, generator=g) * 0.02, relu) for _ in range(layers)]
 
     def step():
         y = x
@@ -170,16 +200,8 @@ def cpu_baseline_conv(n, c, h, w, layers, relu=True, budget_s=15.0):
                 L.calibrate(xq[0])
             y = cpu_route.conv_dequant(L(xq), L.scale, sx, None, torch.float32)
 
-    step()
-    ts = []
-    t_end = time.perf_counter() + budget_s
-    while len(ts) < 60 and (time.perf_counter() < t_end or len(ts) < 2):
-        t = time.perf_counter()
-        step()
-        ts.append(time.perf_counter() - t)
-    ts.sort()
     ops = 2 * n * h * w * c * c * 9 * layers
-    return ops / ts[0] / 1e12, len(ts), ts[0]
+    return cpu_protocol(step, ops, sample, budget_s)
 
 
 # ------------------------------------------------------------------------------ main
@@ -196,12 +218,12 @@ def main():
     kernels.use_tuned(True)     # the shipped tile table, as Config.tuned_tilings (default) applies it
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    res = {"metric": "W8A8 GEMM & int8 conv3x3 TOPS on 1 MI355X; % of int8 MFMA peak / HBM BW",
-           "unit": "TOPS", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "higher_is_better": True,
-           "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic (seed 0, randn)"}
-    bench = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
-             "decode": bench_decode, "quant": bench_quant, "bf16": bench_bf16, "vgg16": bench_vgg16,
-             "stack": bench_stack, "copy": bench_copy, "mfma": bench_mfma}[a.workload]
+    res = {"metric": METRIC, "unit": "TOPS", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+           "data": "synthetic (seed 0, randn)"}
+    bench = {"headline": bench_headline, "c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4,
+             "c5": bench_c5, "decode": bench_decode, "quant": bench_quant, "bf16": bench_bf16, "vgg16": bench_vgg16,
+             "stack": bench_stack, "copy": bench_copy}[a.workload]
     res.update(bench(a, dev))
     print(json.dumps(res), flush=True)
 
@@ -379,10 +401,7 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
                                  "GBs": round(b / t / 1e9, 1),
                                  "roofline_us": round(roofline_us(2 * M * N * K, b), 2)})
     if not a.no_cpu_baseline:
-        tops, nrep, best = cpu_baseline_gemm(shapes, x_dtype, bias)
-        out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
-                               "kind": "port", "sample": f"{label}: full step, min of {nrep} reps "
-                               f"({best * 1e3:.1f} ms), torch CPU quantize + torch._int_mm + dequantize"}
+        out["cpu_baseline"] = cpu_baseline_gemm(shapes, x_dtype, bias, label)
     return out
 
 
@@ -400,8 +419,18 @@ def bench_c1(a, dev):
 
 
 def bench_c5(a, dev):
+    """The headline's main record: C5's M=8192 W8A8 linear (quantize + fused GEMM, bf16 + bias)."""
     return gemm_result(a, dev, [(8192, 14336, 4096)], torch.bfloat16, True,
-                       "C5 W8A8 GEMM M=8192 N=14336 K=4096 bf16 + bias", "C5")
+                       "C5 W8A8 linear M=8192 N=14336 K=4096: bf16 x (0.1% outliers x20) -> per-row quantize -> "
+                       "int8 MFMA GEMM + fused dequantize + bias -> bf16", "C5")
+
+
+def bench_headline(a, dev):
+    """C5 M=8192 (the largest single-GPU config) as the line, C4's two 256-channel convs (as the op)
+    and C2 as sub-records, each with its own roofline and CPU baseline."""
+    out = bench_c5(a, dev)
+    out["sub"] = bench_c4(a, dev)["sub"] + [dict(bench_c2(a, dev), workload_key="C2")]
+    return out
 
 
 def bench_bf16(a, dev):
@@ -444,18 +473,12 @@ def bench_bf16(a, dev):
                         "avg_launch_us": round(g_sec / (len(shapes) * a.steps) * 1e6, 2)}}
     if not a.no_cpu_baseline:
         xs = [(torch.randn(M, K, generator=g), torch.randn(N, K, generator=g) * 0.02) for M, N, K in shapes]
-        ts = []
-        t_end = time.perf_counter() + 15.0
-        while len(ts) < 30 and (time.perf_counter() < t_end or len(ts) < 2):
-            t = time.perf_counter()
+
+        def cpu_step():
             for x, w in xs:          # the reference's CPU route of precision bf16 (runtime.py:306-313)
                 (x.float() @ w.float().t()).to(torch.bfloat16)
-            ts.append(time.perf_counter() - t)
-        best = min(ts)
-        out["cpu_baseline"] = {"value": round(flops / best / 1e12, 3), "unit": "TFLOP/s",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": f"full step, min of {len(ts)} reps ({best * 1e3:.1f} ms): torch CPU "
-                                         "float32 matmul, the reference's CPU route of precision bf16"}
+        out["cpu_baseline"] = dict(cpu_protocol(cpu_step, flops, "the full step: torch CPU float32 matmul, the "
+                                                "reference's CPU route of precision bf16"), unit="TFLOP/s")
     return out
 
 
@@ -502,44 +525,6 @@ def bench_copy(a, dev):
                          "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": b, "kernel": "torch elementwise"}}
 
 
-def bench_mfma(a, dev):
-    """The int8 MFMA issue ceiling of the device: every SIMD runs back-to-back 32x32x32 int8 MFMAs on
-    registers only (libxdna_probe.so), once with constant operands and once with random bytes, the
-    data a GEMM feeds them. value: the random-operand rate; the clock: s_memtime shader cycles of the
-    last launch over its duration. With random operands the power limit lowers the clock, which
-    bounds every int8 GEMM on the device below the nominal 5.0 POP/s."""
-    import ctypes
-    L = ctypes.CDLL(os.path.join(os.path.dirname(kernels.LIB_PATH), "libxdna_probe.so"))
-    L.xdna_probe_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint32, ctypes.c_void_p,
-                                     ctypes.c_void_p, ctypes.c_void_p]
-    L.xdna_probe_mfma_i8.restype = ctypes.c_int
-    blocks, iters = kernels.num_cus(dev), 10000
-    out = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
-    cyc = torch.zeros(blocks, dtype=torch.int64, device=dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
-
-    def run(random_operands, seed):
-        rc = L.xdna_probe_mfma_i8(blocks, iters, random_operands, seed, out.data_ptr(), cyc.data_ptr(), stream)
-        if rc:
-            raise RuntimeError(f"xdna_probe_mfma_i8: HIP error {rc}")
-
-    macs = blocks * 4 * iters * 16 * 32 * 32 * 32
-    res = {}
-    for rnd in (0, 1):
-        sec, host = timed_steps(a, lambda i, tm: run(rnd, i), None)
-        ghz = float(cyc.double().mean()) / sec / 1e9
-        res[rnd] = (2 * macs / sec / 1e12, ghz, sec, host)
-    tops, ghz, sec, host = res[1]
-    return {"metric": "int8 MFMA issue ceiling TOPS on 1 MI355X (register-only, random operands)", "unit": "TOPS",
-            "dtype": "int8", "value": round(tops, 1), "ms_per_step": round(sec * 1e3, 4),
-            "host_ms_per_step": round(host * 1e3, 4), "clock_ghz": round(ghz, 3),
-            "constant_operands": {"value": round(res[0][0], 1), "clock_ghz": round(res[0][1], 3)},
-            "config": {"workload": f"{blocks} workgroups x 4 waves, {iters} x 16 v_mfma_i32_32x32x32_i8 per wave"},
-            "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                         "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": 0, "kernel": "mfma_ceiling_kernel<true>",
-                         "avg_launch_us": round(sec * 1e6, 2)}}
-
-
 def conv_layer_data(dev, n, c, h, w, seed=0):
     g = gen(seed)
     x = torch.randn(n, c, h, w, generator=g).to(dev)
@@ -549,32 +534,64 @@ def conv_layer_data(dev, n, c, h, w, seed=0):
     return x, wq, sw, c_pad
 
 
-def bench_c4(a, dev):
-    n, c, h, w = 1, 256, 1536, 64
-    sets = []
-    for s in range(3):
-        x, wq, sw, c_pad = conv_layer_data(dev, n, c, h, w, seed=s)
-        xq, sx = kernels.conv_quant(x, c_pad)
-        shift = 10
-        sets.append((xq, wq, shift))
-    torch.cuda.synchronize()
-    # one conv launch per step, back to back behind the gate: GPU seconds per step = its duration
-    sec, host = timed_steps(a, lambda i, tm: kernels.conv3x3(*sets[i % 3], True), None)
-    ops = 2 * n * h * w * c * c * 9
-    ach = ops / sec / 1e12
-    out = {"value": round(ops / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
-           "host_ms_per_step": round(host * 1e3, 4),
-           "config": {"workload": "C4 int8 conv3x3 256->256 on 1x256x1536x64, ReLU, NHWC int8 in/out"},
+def conv_op_record(a, dev, shape, sample_shape):
+    """One 256-channel conv as the op runs it on a GPU graph (xdna::conv3x3_fused with ReLU fused):
+    per-image quantize of the NCHW float32 input into NHWC int8, the implicit-GEMM conv with the
+    calibrated shift and the requantize fused, dequantize back to NCHW float32. The layer's first call
+    (weight quantize-once, shift calibration on image 0) runs in the warm-up. value: op-level TOPS
+    (GPU time of K op calls behind the gate); roofline: the conv kernel alone, its launches back to
+    back on the same inputs (the op's own conv call, measured with events on its stream)."""
+    from torch_xdna import Config, conv, ops
+
+    n, c, h, w = shape
+    cid = ops.config_id(Config(policy="gpu", verify="off"))
+    xs = []
+    nsets = max(2, -(-(MALL_BYTES + (64 << 20)) // (n * c * h * w * 9)))   # float in + int8 + float out
+    g = gen(0)
+    for _ in range(nsets):
+        xs.append(torch.randn(n, c, h, w, generator=g).to(dev))
+    wt = (torch.randn(c, c, 3, 3, generator=g) * 0.02).to(dev)
+    op = torch.ops.xdna.conv3x3_fused
+    sec, host = timed_steps(a, lambda i, tm: op(xs[i % nsets], wt, None, True, cid), None)
+    layer = conv._layer(wt, h, w, True)
+    if layer.device != "gpu" or layer.shift is None:
+        raise SystemExit(f"conv {shape} did not run on the GPU: {layer.device}")
+    # the conv kernel alone, back to back on the op's own quantized inputs
+    wq, _ = layer.gpu_weights(dev)
+    xq_list = [kernels.conv_quant(x, layer.ci_pad)[0] for x in xs[:3]]
+    conv_us = back_to_back_us([lambda xq=xq: kernels.conv3x3(xq, wq, layer.shift, True) for xq in xq_list],
+                              max(3, a.steps))
+    ops_ = 2 * n * h * w * c * c * 9
+    ach = ops_ / (conv_us / 1e6) / 1e12
+    conv_bytes = n * c * h * w * 2 + 9 * c * c + 4 * c
+    label = f"C4 conv3x3 {c}->{c} on {n}x{c}x{h}x{w}"
+    rec = {"workload_key": f"C4 {n}x{c}x{h}x{w}", "value": round(ops_ / sec / 1e12, 2), "unit": "TOPS",
+           "ms_per_step": round(sec * 1e3, 4), "host_ms_per_step": round(host * 1e3, 4),
+           "config": {"workload": f"{label} + ReLU as the op xdna::conv3x3_fused: float32 NCHW in -> per-image "
+                                  "quantize -> int8 implicit-GEMM conv (calibrated shift, round half up, uint8 "
+                                  "saturate) -> dequantize -> float32 NCHW out", "shift": layer.shift,
+                      "tile": kernels.tile_get(dev, "conv", n * h * w, c, 9 * layer.ci_pad), "rotating_inputs": nsets},
            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                        "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic("c4"), "kernel": "mm_tile_kernel (conv)",
-                        "avg_launch_us": round(sec * 1e6, 2),
-                        "alg_bytes_per_launch": n * c * h * w * 2 + 9 * c * c + 4 * c}}
+                        "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic(f"c4_{n}x{c}x{h}x{w}"),
+                        "kernel": "mm_tile_kernel (conv, EPI_REQUANT)", "avg_launch_us": round(conv_us, 2),
+                        "alg_bytes_per_launch": conv_bytes,
+                        "timing": "conv kernel launches back to back behind the gate, events around them"}}
     if not a.no_cpu_baseline:
-        tops, nrep, best = cpu_baseline_conv(1, 256, 128, 64, 1)
-        out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
-                               "kind": "port", "sample": f"one layer at 1x256x128x64 (1/12 of the image rows), "
-                               f"min of {nrep} reps ({best * 1e3:.1f} ms): torch CPU quantize + fp32 conv2d of the "
-                               "int8 values + shift + dequantize"}
+        sn, sc, sh, sw_ = sample_shape
+        rec["cpu_baseline"] = cpu_baseline_conv(
+            sn, sc, sh, sw_, 1, f"one layer at {sn}x{sc}x{sh}x{sw_}"
+            + (" (the full shape)" if sample_shape == shape else f" (a {sn * sh * sw_}/{n * h * w} pixel sample "
+               f"of {n}x{c}x{h}x{w})") + ": torch CPU per-image quantize + exact float conv2d of the integers + "
+            "shift + dequantize, shift fixed in the first warm-up run")
+    return rec
+
+
+def bench_c4(a, dev):
+    """C4's two 256-channel convs as the op (sub-records of the headline line); the first is the line."""
+    recs = [conv_op_record(a, dev, (1, 256, 1536, 64), (1, 256, 1536, 64)),
+            conv_op_record(a, dev, (8, 256, 256, 256), (1, 256, 256, 256))]
+    out = {k: v for k, v in recs[0].items() if k != "workload_key"}
+    out["sub"] = recs
     return out
 
 
@@ -642,9 +659,8 @@ def bench_c3(a, dev):
                         "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic("c3"), "kernel": "mm_tile_kernel (conv)",
                         "avg_launch_us": round(conv_us, 2)}}
     if not a.no_cpu_baseline:
-        tops, nrep, best = cpu_baseline_conv(n, c, h, w, L)
-        out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
-                               "kind": "port", "sample": f"full C3 step, min of {nrep} reps ({best * 1e3:.1f} ms)"}
+        out["cpu_baseline"] = cpu_baseline_conv(n, c, h, w, L, "the full C3 step (4 layers, each quantized from and "
+                                                "dequantized to float32 on the CPU)")
     return out
 
 
@@ -721,11 +737,9 @@ def bench_vgg16(a, dev):
                         "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None,
                         "kernel": "whole step (13 convs, their quantize / requantize passes, the final pool)"}}
     if not a.no_cpu_baseline:
-        tops, nrep, best = cpu_baseline_conv(1, 256, 56, 56, 1)
-        out["cpu_baseline"] = {"value": round(tops, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
-                               "kind": "port", "sample": f"one VGG-16 conv3 layer 256->256 at 1x256x56x56, min of "
-                               f"{nrep} reps ({best * 1e3:.1f} ms): torch CPU quantize + fp32 conv2d of the int8 "
-                               "values + shift + dequantize"}
+        out["cpu_baseline"] = cpu_baseline_conv(1, 256, 56, 56, 1, "one VGG-16 conv3 layer 256->256 at 1x256x56x56: "
+                                                "torch CPU quantize + exact float conv2d of the integers + shift + "
+                                                "dequantize")
     return out
 
 
@@ -821,17 +835,12 @@ def bench_stack(a, dev):
             mask[b, :, :n, :n] = True
             i = torch.arange(n, L)
             mask[b, :, i, i] = True
-        ts = []
-        with torch.no_grad():
-            for _ in range(3):
-                t = time.perf_counter()
+        def cpu_step():
+            with torch.no_grad():
                 head_c(llm_c(inputs_embeds=x, attention_mask=mask)[0])
-                ts.append(time.perf_counter() - t)
-        best = min(ts)
-        out["cpu_baseline"] = {"value": round(2 * stack._stacks[sid].macs(list(lens)) / best / 1e12, 3), "unit": "TOPS",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": f"the short-text step (58 / 43 tokens) of the same model eagerly in float32 "
-                               f"on the CPU (transformers), min of 3 ({best * 1e3:.0f} ms)"}
+        out["cpu_baseline"] = cpu_protocol(cpu_step, 2 * stack._stacks[sid].macs(list(lens)),
+                                           "the short-text step (58 / 43 tokens) of the same model eagerly in float32 "
+                                           "on the CPU (transformers)", budget_s=20.0, warmup=1)
     return out
 
 

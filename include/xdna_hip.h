@@ -98,13 +98,23 @@ int xdna_device_info(int* num_cus, int* gfx_major, int* gfx_minor);
 
 /* Per-shape tile table (replaces the reference's tuned NPU tilings: kernels.tuned_table /
  * tiling_for, torch_xdna/kernels.py:123-149, filled from tools/sweep.py). xdna_tile_set makes
- * every later launch of exactly (kind, m, n, k) use `tile` (XDNA_TILE_AUTO removes the entry);
- * any tile computes the same results, only the speed differs. The table is process-wide and
- * thread-safe. xdna_tile_get returns the tile the next such launch uses (the table's, else the
- * built-in rule's, which needs the current device) or a negative status; xdna_tile_clear empties
- * the table. */
+ * the first (head) launch of every later call of exactly (kind, m, n, k) use `tile`
+ * (XDNA_TILE_AUTO removes the entry); any tile computes the same results, only the speed differs.
+ * The table is process-wide and thread-safe. xdna_tile_get returns the head tile the next such call
+ * uses (the table's, else the built-in rule's, which needs the current device) or a negative
+ * status; xdna_tile_clear empties the table.
+ *
+ * A call whose head tile runs one workgroup per CU and whose last round of tiles would leave more
+ * than half of the CUs idle runs rows [0, m1) with the head tile and rows [m1, m) as a second launch
+ * with a smaller tail tile (the table's entry for (kind, m - m1, n, k) if it lists a tile-engine
+ * tile, else the built-in rule's). xdna_tile_plan reports that whole plan of a call: *head, *m1 (0:
+ * one launch, no tail) and *tail (XDNA_TILE_AUTO when there is none). GEMM operands above 1 GB run
+ * in row chunks; the plan is then that of the first chunk. The reference's verify key names the
+ * program of a launch (runtime.py:207: dtype, row bucket, Np, Kp, tiling); the plan is what
+ * identifies the kernels of a call here. */
 int xdna_tile_set(int kind, int64_t m, int64_t n, int64_t k, int tile);
 int xdna_tile_get(int kind, int64_t m, int64_t n, int64_t k);
+int xdna_tile_plan(int kind, int64_t m, int64_t n, int64_t k, int* head, int64_t* m1, int* tail);
 int xdna_tile_clear(void);
 
 /* Per-row symmetric int8 quantization of activations or weights:

@@ -43,21 +43,6 @@ def test_library_exports_every_declared_symbol(lib):
     assert sorted(kernels.EXPORTS) == declared()
 
 
-def test_probe_library():
-    """The measurement probe behind bench.py's `mfma` workload is its own library, exporting only the
-    probe entry point (it adds nothing to the hot path's ABI); bad arguments are rejected on the host."""
-    from torch_xdna import kernels
-
-    path = os.path.join(os.path.dirname(kernels.LIB_PATH), "libxdna_probe.so")
-    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
-    assert set(re.findall(r"\bT (xdna_\w+)$", out, re.M)) == {"xdna_probe_mfma_i8"}
-    L = ctypes.CDLL(path)
-    L.xdna_probe_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint32, ctypes.c_void_p,
-                                     ctypes.c_void_p, ctypes.c_void_p]
-    assert L.xdna_probe_mfma_i8(0, 1, 1, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), None) != 0
-    assert L.xdna_probe_mfma_i8(1, 1, 1, 0, None, ctypes.c_void_p(16), None) != 0
-
-
 def test_abi_version(lib):
     from torch_xdna import kernels
 
@@ -80,3 +65,7 @@ def test_argument_validation(lib):
     # empty work is a no-op success
     assert lib.xdna_gemm_i8_i32(None, 16, None, 16, None, 16, 0, 4, 16, None) == 0
     assert lib.xdna_quant_rows(None, 0, 0, 16, 16, None, 16, 16, None, None) == 0
+    # the launch-plan query validates its arguments before it needs a device
+    out_i, out_l = ctypes.c_int(), ctypes.c_int64()
+    assert lib.xdna_tile_plan(7, 4, 4, 16, ctypes.byref(out_i), ctypes.byref(out_l), ctypes.byref(out_i)) == -1
+    assert lib.xdna_tile_plan(0, 4, 4, 16, None, ctypes.byref(out_l), ctypes.byref(out_i)) == -1

@@ -69,6 +69,47 @@ def test_host_model_on_gpu(gpu):
     assert y.device.type == "cpu" and torch.equal(y, run(net, x, policy="cpu", fallback="eager"))
 
 
+def test_auto_host_model(gpu):
+    """policy "auto", the reference's default (config.py:17; its case_auto, tests/test_backend.py:82-94):
+    a host-resident model's GEMMs are timed on the GPU and on the CPU once per (precision, row bucket,
+    N, K), three decisions are recorded, the output equals the CPU route bit for bit, and a second
+    compile reuses the decisions."""
+    from torch_xdna import runtime
+
+    torch.manual_seed(12)
+    net = Net().eval()
+    x = torch.randn(512, 200)
+    y = run(net, x, policy="auto")
+    s = _stats()
+    d = s["decisions"]
+    assert len(d) == 3 and all(v[0] in ("gpu", "cpu") and v[1] > 0 and v[2] > 0 for v in d.values()), d
+    assert sum(s["calls"].values()) == 3 and not s["fallbacks"], s
+    y_cpu = run(net, x, policy="cpu")
+    assert y.device.type == "cpu" and torch.equal(y, y_cpu), "policy auto and the CPU route differ"
+    y2 = run(net, x, policy="auto")
+    assert torch.equal(y2, y_cpu) and len(runtime.decisions) == 3
+
+
+def test_auto_host_conv(gpu):
+    """policy "auto" on a host-resident conv net: each of the three rewritten convs is timed on the GPU
+    and the CPU on its first call (conv.py:122-138) and keeps the faster; the output equals the CPU
+    route's integers bit for bit."""
+    from torch_xdna import conv as xconv
+
+    torch.manual_seed(13)
+    net = CNN().eval()
+    x = torch.randn(2, 64, 32, 64)
+    y = run(net, x, policy="auto", fallback="eager")
+    s = _stats()
+    assert len(s["decisions"]) == 3 and sum(s["calls"].values()) == 3 and not s["fallbacks"], s
+    assert y.device.type == "cpu"
+    for _, layer in xconv._layers.values():      # the same layers and shifts, on the CPU route
+        layer.device = "cpu"
+    y_cpu = run(net, x, policy="auto", fallback="eager")
+    assert _stats()["calls"] == {"cpu": 3}
+    assert torch.equal(y, y_cpu), "policy auto and the CPU route's integers differ"
+
+
 def test_fusion(gpu):
     torch.manual_seed(4)
     net = Attn().eval().to(gpu)

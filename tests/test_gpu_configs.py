@@ -1,12 +1,11 @@
 """BASELINE.json configs C1-C5 on the MI355X through the public ops, against the oracle.
 
-C1, C2, C3, the VGG16 layers of C4 and the decode / M=256 GEMMs of C5 are compared in full (int32
-sums from the C oracle, the rest from the numpy oracle). The full-size 256-channel C4 convs and the
-M=8192 C5 GEMMs are too large for a CPU oracle within seconds, so they are checked by
-size-independent properties: exact row and column checksums
-of the int32 GEMM (sum_n C = A (sum_n W), sum_m C = (sum_m A) W^T, in int64), and exact values at a
-few thousand random positions (int64 dot products / conv sums on the CPU), for the int32 output and
-for the fused bf16 / requantized outputs.
+Every config is compared in full. C1, C2, C3, the VGG16 layers of C4 and the decode / M=256 GEMMs
+of C5 against the C oracle's int32 sums and the numpy oracle; the full-size 256-channel C4 convs and
+the M = 2048 / 8192 C5 GEMMs against the reference's own CPU kernels on the same integers (torch's
+exact float conv of the int8 values, torch._int_mm), which finish in seconds at these sizes, with
+size-independent checks beside them: exact int64 row and column checksums of the int32 GEMM
+(sum_n C = A (sum_n W), sum_m C = (sum_m A) W^T) and int64 conv sums at random positions.
 """
 import numpy as np
 import pytest
@@ -76,9 +75,9 @@ def test_c3_conv_chain(gpu):
 
     torch.manual_seed(0)
     net = VGGBlock(256, 4).eval()
-    for c in net.convs:
+    for i, c in enumerate(net.convs):           # distinct weights per layer
         with torch.no_grad():
-            c.weight.copy_(torch.randn(c.weight.shape, generator=_gen(11)) * 0.02)
+            c.weight.copy_(torch.randn(c.weight.shape, generator=_gen(11 + i)) * 0.02)
     x = torch.randn(1, 256, 64, 64, generator=_gen(12))
     y = run(net.to(gpu), x.to(gpu), policy="gpu", fallback="eager")
     s = _stats()
@@ -153,25 +152,37 @@ def _sampled_conv_check(xq_nchw, wq, q_nhwc, shift, relu, n_samples, seed):
 
 
 @pytest.mark.parametrize("shape", [(1, 256, 1536, 64), (8, 256, 256, 256)])
-def test_c4_large_conv_sampled(gpu, shape):
+def test_c4_large_conv(gpu, shape):
+    """C4's 256-channel convs at full size: the quantized images, the calibration max and every
+    requantized output against the reference's CPU route (torch's exact float conv of the integers,
+    oracle/cpu_route.py), plus sampled int64 sums as an independent check."""
+    from oracle import cpu_route
     from torch_xdna import kernels
 
     nb, c, h, w = shape
-    x = torch.randn(*shape, generator=_gen(21)).to(gpu)
-    wt = (torch.randn(c, c, 3, 3, generator=_gen(22)) * 0.02).to(gpu)
-    xq, sx = kernels.conv_quant(x, c)
-    wq, sw = kernels.conv_weight_pack(wt, c)
+    x = torch.randn(*shape, generator=_gen(21))
+    wt = torch.randn(c, c, 3, 3, generator=_gen(22)) * 0.02
+    xq, sx = kernels.conv_quant(x.to(gpu), c)
+    wq, sw = kernels.conv_weight_pack(wt.to(gpu), c)
     top = kernels.conv3x3_calibrate(xq[:1], wq, True)
     shift = O.shift_from_top(float(top), True)
     q = kernels.conv3x3(xq, wq, shift, True)
-    xq_nchw = xq.permute(0, 3, 1, 2).cpu().numpy()
-    wq_ref = wq.cpu().numpy().reshape(c, 3, 3, c).transpose(0, 3, 1, 2)
-    # the calibration max is reached somewhere and bounds every sampled |acc|
-    assert top > 0
-    _sampled_conv_check(xq_nchw, wq_ref, q.cpu().numpy(), shift, True, 3000, seed=1)
-    # quantize parity on the full tensor (cheap in numpy)
-    xq_r, sx_r = O.conv_quant_images(x.cpu().numpy())
-    assert np.array_equal(xq_nchw, xq_r) and np.array_equal(sx.cpu().numpy(), sx_r)
+    xq_nchw = xq.permute(0, 3, 1, 2).cpu()
+    # quantize parity in full (numpy oracle)
+    xq_r, sx_r = O.conv_quant_images(x.numpy())
+    assert np.array_equal(xq_nchw.numpy(), xq_r) and np.array_equal(sx.cpu().numpy(), sx_r)
+    # the reference's CPU route on the same integers: calibration max of image 0, then every output
+    ref = cpu_route.ConvLayerCPU(wt, True)
+    assert torch.equal(ref.wq, wq.view(c, 3, 3, c).permute(0, 3, 1, 2).cpu())
+    acc0 = ref.acc(xq_nchw[:1])
+    assert top == int(acc0.clamp(min=0).max())
+    ref.calibrate(xq_nchw[0])
+    assert ref.shift == shift
+    want = ref(xq_nchw)
+    got = q.permute(0, 3, 1, 2).cpu()
+    assert torch.equal(got, want), f"{int((got != want).sum())} of {want.numel()} differ"
+    wq_ref = ref.wq.numpy()
+    _sampled_conv_check(xq_r, wq_ref, q.cpu().numpy(), shift, True, 500, seed=1)
 
 
 # VGG16's thirteen 3x3 convs have these nine distinct (Ci, Co, H=W) shapes
@@ -206,8 +217,13 @@ def test_c4_vgg16_layer(gpu, ci, co, hw):
     assert np.array_equal(q.permute(0, 3, 1, 2).cpu().numpy(), O.requant(acc, shift, True))
 
 
-@pytest.mark.parametrize("M,N,K", [(8192, 14336, 4096), (8192, 4096, 14336), (2048, 4096, 4096)])
-def test_c5_large_gemm_properties(gpu, M, N, K):
+@pytest.mark.parametrize("M,N,K", [(8192, 14336, 4096), (8192, 4096, 14336), (8192, 4096, 4096),
+                                   (2048, 14336, 4096), (2048, 4096, 14336), (2048, 4096, 4096)])
+def test_c5_large_gemm(gpu, M, N, K):
+    """C5's M = 2048 / 8192 GEMMs at full size: the quantized activation in full (numpy oracle), every
+    int32 sum against torch._int_mm on the CPU (the reference's CPU kernel, runtime.py:162-163), every
+    fused bf16 output against the reference's CPU dequantize of those sums, and exact int64 row /
+    column checksums as an independent check of the sums."""
     from torch_xdna import kernels
 
     g = _gen(M + N + K)
@@ -219,24 +235,26 @@ def test_c5_large_gemm_properties(gpu, M, N, K):
     wq, sw = kernels.quant_rows(w.to(gpu))
     acc = kernels.mm_i8(xq, wq)
     y = kernels.mm_i8_dequant(xq, sx, wq, sw, b.to(gpu), torch.bfloat16)
-    # quantize parity in full
     xq_r, sx_r = O.quant_rows(x.float().numpy())
+    wq_r, sw_r = O.quant_rows(w.numpy())
     assert np.array_equal(xq.cpu().numpy(), xq_r) and np.array_equal(sx.cpu().numpy(), sx_r)
-    A = xq.cpu().numpy().astype(np.int64)
-    W = wq.cpu().numpy().astype(np.int64)
-    # exact checksums in int64
-    row = acc.to(torch.int64).sum(1).cpu().numpy()
-    col = acc.to(torch.int64).sum(0).cpu().numpy()
-    assert np.array_equal(row, A @ W.sum(0)), "row checksums differ"
-    assert np.array_equal(col, W @ A.sum(0)), "column checksums differ"
-    # exact entries at random positions, for the int32 and the fused bf16 outputs
-    rng = np.random.default_rng(0)
-    ms, ns = rng.integers(0, M, 4000), rng.integers(0, N, 4000)
-    want = np.einsum("ik,ik->i", A[ms], W[ns])
-    accc = acc.cpu().numpy()
-    assert np.array_equal(accc[ms, ns], want)
-    yw = O.to_bf16(((want.astype(np.float32) * sx_r[ms]) * sw.cpu().numpy()[ns]) + b.numpy()[ns])
-    assert np.array_equal(y.float().cpu().numpy()[ms, ns], yw)
+    assert np.array_equal(wq.cpu().numpy(), wq_r) and np.array_equal(sw.cpu().numpy(), sw_r)
+    A, Wt = torch.from_numpy(xq_r), torch.from_numpy(wq_r)
+    acc_r = torch._int_mm(A, Wt.t().contiguous())
+    accg = acc.cpu()
+    assert torch.equal(accg, acc_r), f"{int((accg != acc_r).sum())} int32 sums differ"
+    row = accg.to(torch.int64).sum(1)
+    col = accg.to(torch.int64).sum(0)
+    assert torch.equal(row, A.long() @ Wt.long().sum(0)), "row checksums differ"
+    assert torch.equal(col, Wt.long() @ A.long().sum(0)), "column checksums differ"
+    # every bf16 output against the reference's CPU dequantize (torch ops, runtime.py:350-353) of the
+    # exact sums; the numpy oracle's dequantize on a band of rows as an independent check
+    sxt, swt = torch.from_numpy(sx_r), torch.from_numpy(sw_r)
+    want = ((acc_r.float() * sxt[:, None]) * swt[None, :] + b[None, :]).to(torch.bfloat16)
+    got = y.cpu()
+    assert torch.equal(got, want), f"{int((got != want).sum())} bf16 outputs differ"
+    r = slice(M // 2, M // 2 + 64)
+    assert np.array_equal(got[r].float().numpy(), O.to_bf16(O.dequant(acc_r[r].numpy(), sx_r[r], sw_r, b.numpy())))
 
 
 @pytest.mark.parametrize("M", [1, 16, 256])

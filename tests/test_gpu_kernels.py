@@ -420,9 +420,14 @@ def test_tiles_tail_split(gpu, tile, tile_table):
         yb = kernels.mm_bf16(kernels.bf16_rows(x.to(gpu), k), kernels.bf16_rows(wf.to(gpu), k), None, torch.float32)
         want, bound = O.gemm_bf16(x.numpy(), wf.numpy())
         _bf16_bracket(_f32(yb), want, bound, "f32")
-    # conv: h * w pixels make 1.25 rounds of row tiles, less a partial last tile
+    # conv: h * w pixels make about 1.25 rounds of row tiles; w = 317 is not a multiple of any tile
+    # height, so the head ends and the tail starts mid-image and both have a partial last tile
     ci, co = 64, bn
-    h, w_ = bm * (cus + cus // 4) // 320, 319
+    w_ = 317
+    h = (bm * (cus + cus // 4) - 100) // w_
+    h -= (h * w_) % bm == 0
+    tiles = -(-(h * w_) // bm)
+    assert tiles // cus == 1 and 0 < 2 * (tiles % cus) <= cus and (h * w_) % bm and (bm * cus) % w_
     kernels.tile_set("conv", h * w_, co, 9 * ci, tile)
     xq, wq = _i8((1, ci, h, w_), seed=h), _i8((co, ci, 3, 3), seed=co)
     packed = wq.permute(0, 2, 3, 1).reshape(co, 9, ci).contiguous()

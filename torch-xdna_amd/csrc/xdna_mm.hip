@@ -1119,32 +1119,46 @@ int launch_tiles_once(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw
 // 256 CUs) as 256 of them plus 256 tiles of 128 x 256 over the last third of the rows. Row r of the tail
 // launch is row m1 + r of the problem; for the conv that is a pixel offset (ConvGeom::m0) into the same
 // images.
-template <int CONVM, int EPI>
-int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
-                 ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
+struct TilePlan {
+  int head;       // tile of rows [0, m1) (all rows when m1 == 0)
+  int64_t m1;     // first row of the tail launch; 0: one launch
+  int tail;       // tile of rows [m1, M) when m1 > 0
+};
+
+// kind: the table's kind of the launch; kbytes: K as the engine counts it (bytes of an operand row);
+// ktab: K as the table keys it (bf16 elements for the bf16 GEMM).
+TilePlan plan_tiles(int kind, int64_t M, int64_t N, int64_t kbytes, int64_t ktab, int tile) {
+  const TilePlan one{tile, 0, T_AUTO};
+  if (is_small(tile) || is_gemv(tile) || is_seg4(tile)) return one;
   const TileCfg t = tile_cfg(tile);
   const bool one_per_cu = t.kg == 1 && t.bm >= 128 && t.bn >= 128 && !(t.bm == 128 && t.bn == 128);
-  if (!one_per_cu) return launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, M, N, K, cg, e, tile, st);
+  if (!one_per_cu) return one;
   const int64_t cus = device_cus();
   const int64_t tm = (M + t.bm - 1) / t.bm, tn = (N + t.bn - 1) / t.bn;
   const int64_t rounds = (tm * tn) / cus, rem = (tm * tn) % cus;
   const int64_t tm_head = rounds * cus / tn;
-  if (!(rounds >= 1 && rem > 0 && 2 * rem <= cus && tm_head >= 1 && tm_head < tm))
-    return launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, M, N, K, cg, e, tile, st);
+  if (!(rounds >= 1 && rem > 0 && 2 * rem <= cus && tm_head >= 1 && tm_head < tm)) return one;
   const int64_t m1 = tm_head * t.bm;
   // the tail's tile: the table's entry for the tail's own shape if it lists an engine tile; else after
   // 256 x 256 tiles the 8-wave 128 x 256 tile, else the rule. C4 (1 x 256 x 1536 x 64) measured 79.8 us
   // unsplit, 72.7 us with a 128 x 128 tail (the rule's) and 69.4 us with the 128 x 256 one.
-  const int kind = CONVM != 0 ? XDNA_KIND_CONV : epi_bf(EPI) ? XDNA_KIND_BF16 : XDNA_KIND_I8;
-  int tail = tile_lookup(kind, M - m1, N, epi_bf(EPI) ? K / 2 : K);
+  int tail = tile_lookup(kind, M - m1, N, ktab);
   if (is_small(tail) || is_gemv(tail) || is_seg4(tail)) tail = T_AUTO;
-  if (tail == T_AUTO) tail = tile == T_256x256W8 ? T_128x256W8 : rule_tile(M - m1, N, K, false);
+  if (tail == T_AUTO) tail = tile == T_256x256W8 ? T_128x256W8 : rule_tile(M - m1, N, kbytes, false);
   // only when the leftover rows fit one round of the tail's tiles (8192 x 3072 in 256 x 256 tiles leaves
   // 2816 rows, 264 tiles of 128 x 256: measured slower split than not)
   const TileCfg tt = tile_cfg(tail);
-  if (((M - m1 + tt.bm - 1) / tt.bm) * ((N + tt.bn - 1) / tt.bn) > cus)
-    return launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, M, N, K, cg, e, tile, st);
+  if (((M - m1 + tt.bm - 1) / tt.bm) * ((N + tt.bn - 1) / tt.bn) > cus) return one;
+  return TilePlan{tile, m1, tail};
+}
 
+template <int CONVM, int EPI>
+int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                 ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
+  const int kind = CONVM != 0 ? XDNA_KIND_CONV : epi_bf(EPI) ? XDNA_KIND_BF16 : XDNA_KIND_I8;
+  const TilePlan p = plan_tiles(kind, M, N, K, epi_bf(EPI) ? K / 2 : K, tile);
+  if (p.m1 == 0) return launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, M, N, K, cg, e, tile, st);
+  const int64_t m1 = p.m1;
   int rc = launch_tiles_once<CONVM, EPI>(a, lda, w, ldw, m1, N, K, cg, e, tile, st);
   if (rc) return rc;
   ConvGeom ct = cg;
@@ -1154,9 +1168,10 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
   const EpiArgs et = shift_epi(e, out_bytes<EPI>(), m1, 0);
   // the tail's tile may split K over groups: CONVM 1 needs c_pad to be a multiple of its groups' slices
   if constexpr (CONVM != 0) {
-    if (cg.c_pad % (64 * tt.kg) != 0) return launch_tiles_once<2, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, tail, st);
+    if (cg.c_pad % (64 * tile_cfg(p.tail).kg) != 0)
+      return launch_tiles_once<2, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, p.tail, st);
   }
-  return launch_tiles_once<CONVM, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, tail, st);
+  return launch_tiles_once<CONVM, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, p.tail, st);
 }
 
 template <int EPI>
@@ -1393,6 +1408,31 @@ int xdna_tile_get(int kind, int64_t m, int64_t n, int64_t k) {
   XDNA_REQUIRE(kind == XDNA_KIND_I8 || kind == XDNA_KIND_BF16 || kind == XDNA_KIND_CONV, "unknown kind");
   XDNA_REQUIRE(m >= 1 && n >= 1 && k >= 1, "bad sizes");
   return choose_tile(kind, m, n, k, kind == XDNA_KIND_BF16 ? 2 * k : k);
+}
+
+int xdna_tile_plan(int kind, int64_t m, int64_t n, int64_t k, int* head, int64_t* m1, int* tail) {
+  XDNA_REQUIRE(kind == XDNA_KIND_I8 || kind == XDNA_KIND_BF16 || kind == XDNA_KIND_CONV, "unknown kind");
+  XDNA_REQUIRE(m >= 1 && n >= 1 && k >= 1, "bad sizes");
+  XDNA_REQUIRE(head && m1 && tail, "null output pointer");
+  const int64_t kbytes = kind == XDNA_KIND_BF16 ? 2 * k : k;
+  int t = choose_tile(kind, m, n, k, kbytes);
+  // the launchers' own substitutions: the one-row and few-row kernels take only their row counts, and
+  // the small-M kernel addresses the whole activation with one buffer resource
+  if (kind != XDNA_KIND_CONV) {
+    if (is_gemv(t) && m != 1) t = rule_tile(m, n, kbytes, m > 1);
+    if (is_seg4(t) && m > 16) t = rule_tile(m, n, kbytes, true);
+    if (is_small(t) && (m * kbytes > MAX_BUF || (m + 15) / 16 >= 65536)) t = rule_tile(m, n, kbytes, false);
+  }
+  // GEMM operands above one buffer resource run in row chunks (with dense rows, lda = k): the plan of
+  // the first chunk
+  int64_t mc = m;
+  if (kind != XDNA_KIND_CONV && !(is_small(t) || is_gemv(t) || is_seg4(t)))
+    mc = std::min(m, std::max<int64_t>(256, (MAX_BUF / kbytes) / 256 * 256));
+  const TilePlan p = plan_tiles(kind, mc, n, kbytes, k, t);
+  *head = p.head;
+  *m1 = p.m1;
+  *tail = p.tail;
+  return XDNA_OK;
 }
 
 int xdna_tile_clear(void) {

@@ -1,24 +1,33 @@
 """torch.compile(model, backend="xdna"): GEMMs and 3x3 convs against parameters run int8 on an MI355X.
 
-The pass rewrites Dynamo's FX graph the way the reference's backend does (torch_xdna/backend.py:59-256
-in the reference), so the same nodes are offloaded:
+The pass works on Dynamo's FX graph and takes the same nodes the reference's pass takes
+(torch_xdna/backend.py:59-226 in the reference), so a model offloads the same work:
 
-  * `F.linear(x, W, b)`, `x @ W` / `torch.mm` / `torch.matmul` / `x.matmul(W)` and
-    `torch.addmm(b, x, W)` (HF Conv1D) with W a static 2-D float parameter -> xdna::linear;
-  * xdna::linear nodes reading the same input (q/k/v, gate/up) -> one xdna::linear_cat + narrows;
-  * with precision "int8" and cpu_kernel "int8", linear / linear_cat -> runtime.linear_int8, which
-    on a CPU graph is quantize -> xdna::linear_i8 -> dequantize as graph ops and on a GPU graph the
-    single fused HIP op;
-  * conv2d 3x3 / stride 1 / padding 1 or "same" / dilation 1 / groups 1 with a static weight ->
-    conv.conv3x3_int8, fusing the ReLU of a bias-free conv whose only user it is (only when the GPU
-    route is usable and policy != "cpu").
+  GEMM sites    `F.linear(x, W, b)`; `x @ W`, `torch.mm`, `torch.matmul`, `x.matmul(W)` / `x.mm(W)`
+                with exactly two positional operands; `torch.addmm(b, x, W)` (HF Conv1D) with
+                alpha = beta = 1 and b absent or a 1-D parameter. W must be a 2-D float parameter
+                (or buffer). Each becomes xdna::linear.
+  shared input  with `fuse`, the xdna::linear nodes of one input (q/k/v, gate/up) become one
+                xdna::linear_cat whose output is narrowed back into the members' values.
+  int8 lowering with precision "int8" and cpu_kernel "int8", every linear / linear_cat becomes
+                runtime.linear_int8: on a CPU graph quantize -> xdna::linear_i8 -> dequantize as
+                graph ops, on a GPU graph the one fused HIP op.
+  conv sites    (GPU route usable, policy != "cpu") conv2d 3x3 / stride 1 / padding 1 or "same" /
+                dilation 1 / groups 1 of a 4-D float input and a parameter weight within the conv
+                op's channel limit -> conv.conv3x3_int8; with `fuse`, a ReLU that is the only user
+                of a bias-free conv is folded in (the requantize saturates to [0, 255]).
+  conv chains   with `fuse`, on GPU graphs: conv3x3_int8 -> [ReLU] [2x2 max-pool] -> conv3x3_int8
+                ... with single-use intermediates -> one xdna::conv3x3_chain (int8 NHWC between
+                the convs).
 
-Activation x activation GEMMs (attention) are left alone. What runs where is decided per call at
-run time (runtime.py, conv.py). The rest of the graph goes to Inductor or runs eagerly.
+Activation x activation products (attention) are left alone. Which device runs each op is decided
+per call at run time (runtime.py, conv.py). The rest of the graph goes to Inductor or runs eagerly.
 """
 
 import logging
 import operator
+from dataclasses import dataclass
+from typing import Any, Optional
 
 import torch
 import torch.nn.functional as F
@@ -28,174 +37,223 @@ from . import kernels, ops
 
 log = logging.getLogger("torch_xdna")
 
-LINEAR = {torch._C._nn.linear, F.linear}
-CONV2D = {torch.conv2d, F.conv2d}
-RELU = {torch.relu, F.relu, torch.relu_}
-MATMUL = {operator.matmul, torch.matmul}
 FLOATS = (torch.float32, torch.bfloat16, torch.float16)
 
-
-def _static_placeholders(gm, example_inputs):
-    """Placeholders that hold parameters or buffers (weights worth quantizing once)."""
-    found = set()
-    phs = [n for n in gm.graph.nodes if n.op == "placeholder"]
-    for node, ex in zip(phs, example_inputs):
-        if isinstance(ex, torch.nn.Parameter) or "_parameters_" in node.name or "_buffers_" in node.name:
-            found.add(node)
-    return found
+_LINEAR_FNS = frozenset({torch._C._nn.linear, F.linear})
+_MM_FNS = frozenset({operator.matmul, torch.matmul, torch.mm})
+_MM_METHODS = frozenset({"matmul", "mm", "__matmul__"})
+_CONV_FNS = frozenset({torch.conv2d, F.conv2d})
+_RELU_FNS = frozenset({torch.relu, F.relu, torch.relu_})
+_RELU_METHODS = frozenset({"relu", "relu_"})
+_POOL_FNS = frozenset({F.max_pool2d, torch.max_pool2d})
 
 
-def _example(node, attr):
-    if node.op == "get_attr":
-        return attr(node.target)
-    if node.op == "placeholder":
-        return node.meta.get("example_value")
-    return None
+def _calls(n, fns=frozenset(), methods=frozenset()):
+    """Whether FX node n calls one of `fns` (call_function) or one of `methods` (call_method)."""
+    return (n.op == "call_function" and n.target in fns) or (n.op == "call_method" and n.target in methods)
 
 
-def _gemm_args(node):
-    """(x, w, b, transposed) when `node` is one of the GEMM forms the pass takes, else None."""
-    if node.op == "call_function" and node.target in LINEAR:
-        x = node.args[0] if node.args else node.kwargs.get("input")
-        w = node.args[1] if len(node.args) > 1 else node.kwargs.get("weight")
-        b = node.args[2] if len(node.args) > 2 else node.kwargs.get("bias")
-        return x, w, b, False
-    is_mm = ((node.op == "call_function" and node.target in MATMUL | {torch.mm})
-             or (node.op == "call_method" and node.target in ("matmul", "mm", "__matmul__")))
-    if is_mm and len(node.args) == 2 and not node.kwargs:
-        return node.args[0], node.args[1], None, True           # x @ W with W [K, N]
-    if (node.op == "call_function" and node.target is torch.addmm and len(node.args) == 3
-            and set(node.kwargs) <= {"beta", "alpha"} and all(node.kwargs.get(k, 1) == 1 for k in ("beta", "alpha"))):
-        b, x, w = node.args                                      # bias + x @ W (HF Conv1D)
-        return x, w, b, True
-    return None
-
-
-def offload_gemms(gm: torch.fx.GraphModule, example_inputs, cfg) -> int:
-    """Rewrite offloadable GEMMs and 3x3 convs in place; return how many."""
-    static = _static_placeholders(gm, example_inputs)
-
-    def attr(target):
-        obj = gm
-        for part in target.split("."):
-            obj = getattr(obj, part)
-        return obj
-
-    def is_param(n):
-        return isinstance(n, torch.fx.Node) and (n in static or n.op == "get_attr")
-
-    def is_weight(n):
-        if not is_param(n):
-            return False
-        t = _example(n, attr)
-        return isinstance(t, torch.Tensor) and t.dim() == 2 and t.dtype in FLOATS
-
-    def is_bias_vector(n):
-        t = n.meta.get("example_value") if isinstance(n, torch.fx.Node) else None
-        return is_param(n) and isinstance(t, torch.Tensor) and t.dim() == 1
-
-    cid = ops.config_id(cfg)
-    count = 0
-    for node in list(gm.graph.nodes):
-        m = _gemm_args(node)
-        if m is None:
-            continue
-        x, w, b, transposed = m
-        if node.target is torch.addmm and not (b is None or is_bias_vector(b)):
-            continue
-        if not is_weight(w):
-            continue
-        with gm.graph.inserting_after(node):
-            new = gm.graph.call_function(torch.ops.xdna.linear.default, (x, w, b, transposed, cid))
-        new.meta.update(node.meta)
-        node.replace_all_uses_with(new)
-        gm.graph.erase_node(node)
-        count += 1
-    if cfg.fuse:
-        _fuse_shared_input(gm, cid)
-    if cfg.precision == "int8" and cfg.cpu_kernel == "int8":
-        _quantize_in_graph(gm, cid)
-    count += _offload_convs(gm, static, cid, attr, cfg)
-    if cfg.fuse:
-        _chain_convs(gm, cid)
-    gm.graph.lint()
-    gm.recompile()
-    return count
-
-
-def _conv_args(node):
-    """(x, weight, bias, stride, padding, dilation, groups) of a conv2d call."""
-    names = ("input", "weight", "bias", "stride", "padding", "dilation", "groups")
-    defaults = dict(bias=None, stride=1, padding=0, dilation=1, groups=1)
-    args = dict(zip(names, node.args), **node.kwargs)
-    return [args.get(k, defaults.get(k)) for k in names]
+def _is_relu(n):
+    return _calls(n, _RELU_FNS, _RELU_METHODS)
 
 
 def _pair(v):
     return tuple(v) if isinstance(v, (tuple, list)) else (v, v)
 
 
-def _is_relu(n):
-    return ((n.op == "call_function" and n.target in RELU)
-            or (n.op == "call_method" and n.target in ("relu", "relu_")))
+def _bound(n, names, defaults):
+    """The call's arguments by parameter name (positional ones first), defaults filled in."""
+    got = dict(defaults)
+    got.update(zip(names, n.args))
+    got.update(n.kwargs)
+    return got
 
 
-def _offload_convs(gm, static, cid, attr, cfg):
-    """3x3 / stride 1 / padding 1 / groups 1 convs of a parameter weight -> conv3x3_int8 (with a lone
-    ReLU of a bias-free conv fused into the requantize as unsigned saturation)."""
-    from .conv import conv3x3_int8, supported
+@dataclass
+class _Gemm:
+    """One GEMM site: y = x @ W^T + b, or x @ W (+ b) when `transposed` (W given as [K, N])."""
+    node: torch.fx.Node
+    x: Any
+    weight: Any
+    bias: Any
+    transposed: bool
 
-    # int8 convs only pay off on the GPU: without it, or with policy "cpu", convs stay as they are
+
+class _Graph:
+    """An FX graph under rewrite: which values are parameters (quantized once, so worth offloading),
+    the example tensor of a value, and node replacement."""
+
+    def __init__(self, gm, example_inputs):
+        self.gm = gm
+        self.graph = gm.graph
+        placeholders = [n for n in gm.graph.nodes if n.op == "placeholder"]
+        # Dynamo lifts module parameters and buffers to placeholders named *_parameters_* / *_buffers_*
+        self.params = {n for n, ex in zip(placeholders, example_inputs)
+                       if isinstance(ex, torch.nn.Parameter) or "_parameters_" in n.name or "_buffers_" in n.name}
+
+    def is_param(self, v) -> bool:
+        return isinstance(v, torch.fx.Node) and (v.op == "get_attr" or v in self.params)
+
+    def tensor(self, v, meta_only=False) -> Optional[torch.Tensor]:
+        """The example tensor of graph value v: a get_attr's attribute itself, else the node's
+        recorded example value."""
+        if not isinstance(v, torch.fx.Node):
+            return None
+        if v.op == "get_attr" and not meta_only:
+            obj = self.gm
+            for part in v.target.split("."):
+                obj = getattr(obj, part)
+            t = obj
+        elif v.op in ("placeholder", "get_attr") or meta_only:
+            t = v.meta.get("example_value")
+        else:
+            t = None
+        return t if isinstance(t, torch.Tensor) else None
+
+    def param(self, v, ndim, meta_only=False) -> Optional[torch.Tensor]:
+        """v's example tensor when v is a parameter of `ndim` dimensions."""
+        t = self.tensor(v, meta_only) if self.is_param(v) else None
+        return t if t is not None and t.dim() == ndim else None
+
+    def substitute(self, old, target, args):
+        """A call of `target` on `args` takes over the value (and metadata) of node `old`, which is erased."""
+        with self.graph.inserting_after(old):
+            new = self.graph.call_function(target, args)
+        new.meta.update(old.meta)
+        old.replace_all_uses_with(new)
+        self.graph.erase_node(old)
+        return new
+
+
+# ------------------------------------------------------------------------------ GEMMs
+def _gemm_site(g: _Graph, n) -> Optional[_Gemm]:
+    """n as a GEMM against a parameter, or None."""
+    if _calls(n, _LINEAR_FNS):
+        a = _bound(n, ("input", "weight", "bias"), {"bias": None})
+        site = _Gemm(n, a.get("input"), a.get("weight"), a["bias"], False)
+    elif _calls(n, _MM_FNS, _MM_METHODS) and len(n.args) == 2 and not n.kwargs:
+        site = _Gemm(n, n.args[0], n.args[1], None, True)
+    elif (n.op == "call_function" and n.target is torch.addmm and len(n.args) == 3
+          and set(n.kwargs) <= {"alpha", "beta"} and all(v == 1 for v in n.kwargs.values())):
+        b, x, w = n.args
+        if b is not None and g.param(b, 1, meta_only=True) is None:
+            return None
+        site = _Gemm(n, x, w, b, True)
+    else:
+        return None
+    wt = g.param(site.weight, 2)
+    return site if wt is not None and wt.dtype in FLOATS else None
+
+
+def _rewrite_gemms(g: _Graph, cid) -> int:
+    sites = [s for s in (_gemm_site(g, n) for n in list(g.graph.nodes)) if s is not None]
+    for s in sites:
+        g.substitute(s.node, torch.ops.xdna.linear.default, (s.x, s.weight, s.bias, s.transposed, cid))
+    return len(sites)
+
+
+def _merge_shared_inputs(g: _Graph, cid):
+    """xdna::linear nodes (F.linear form) reading one input -> one xdna::linear_cat + narrows: one launch
+    and one quantize of the input instead of several."""
+    by_input = {}
+    for n in g.graph.nodes:
+        if n.op == "call_function" and n.target is torch.ops.xdna.linear.default and not n.args[3]:
+            by_input.setdefault(n.args[0], []).append(n)
+    for x, members in by_input.items():
+        widths = [g.tensor(m.args[1], meta_only=True) for m in members]
+        if len(members) < 2 or any(t is None for t in widths):
+            continue
+        with g.graph.inserting_before(members[0]):
+            cat = g.graph.call_function(torch.ops.xdna.linear_cat.default,
+                                        (x, [m.args[1] for m in members], [m.args[2] for m in members], cid))
+            offset = 0
+            for m, t in zip(members, widths):
+                part = g.graph.call_function(torch.narrow, (cat, -1, offset, int(t.shape[0])))
+                part.meta.update(m.meta)
+                m.replace_all_uses_with(part)
+                offset += int(t.shape[0])
+        for m in members:
+            g.graph.erase_node(m)
+
+
+def _lower_to_int8(g: _Graph, cid):
+    """linear / linear_cat -> runtime.linear_int8 (quantize, integer GEMM, dequantize)."""
+    from .runtime import linear_int8
+
+    for n in list(g.graph.nodes):
+        if n.op != "call_function":
+            continue
+        if n.target is torch.ops.xdna.linear.default:
+            x, w, b, transposed, _ = n.args
+            args = (x, [w], [b], transposed, cid)
+        elif n.target is torch.ops.xdna.linear_cat.default:
+            x, ws, bs, _ = n.args
+            args = (x, list(ws), list(bs), False, cid)
+        else:
+            continue
+        g.substitute(n, linear_int8, args)
+
+
+# ------------------------------------------------------------------------------ convs
+_CONV_ARGS = ("input", "weight", "bias", "stride", "padding", "dilation", "groups")
+_CONV_DEFAULTS = {"bias": None, "stride": 1, "padding": 0, "dilation": 1, "groups": 1}
+
+
+def _conv_eligible(g: _Graph, a) -> bool:
+    from .conv import supported
+
+    plain = (_pair(a["stride"]) == (1, 1) and _pair(a["dilation"]) == (1, 1) and a["groups"] == 1
+             and (a["padding"] == "same" or _pair(a["padding"]) == (1, 1)))
+    if not plain:
+        return False
+    wt = g.param(a["weight"], 4)
+    xt = g.tensor(a["input"], meta_only=True)
+    if wt is None or tuple(wt.shape[2:]) != (3, 3) or xt is None or xt.dim() != 4 or xt.dtype not in FLOATS:
+        return False
+    return supported(int(wt.shape[1]), int(wt.shape[0]), int(xt.shape[2]), int(xt.shape[3]))
+
+
+def _rewrite_convs(g: _Graph, cid, cfg) -> int:
+    """3x3 stride-1 convs of a parameter weight -> conv3x3_int8, with a lone ReLU of a bias-free conv
+    folded into the requantize (unsigned saturation)."""
+    from .conv import conv3x3_int8
+
+    # int8 convs pay off only on the GPU: without it, or with policy "cpu", they stay float convs
     if cfg.policy == "cpu" or not kernels.available():
         return 0
     count = 0
-    for node in list(gm.graph.nodes):
-        if node.op != "call_function" or node.target not in CONV2D:
+    for n in list(g.graph.nodes):
+        if not _calls(n, _CONV_FNS):
             continue
-        x, w, b, stride, padding, dilation, groups = _conv_args(node)
-        if (_pair(stride) != (1, 1) or (padding != "same" and _pair(padding) != (1, 1))
-                or _pair(dilation) != (1, 1) or groups != 1):
+        a = _bound(n, _CONV_ARGS, _CONV_DEFAULTS)
+        if not _conv_eligible(g, a):
             continue
-        if not (isinstance(w, torch.fx.Node) and (w in static or w.op == "get_attr")):
-            continue
-        wt = _example(w, attr)
-        xt = x.meta.get("example_value") if isinstance(x, torch.fx.Node) else None
-        if not (isinstance(wt, torch.Tensor) and wt.dim() == 4 and tuple(wt.shape[2:]) == (3, 3)
-                and isinstance(xt, torch.Tensor) and xt.dim() == 4 and xt.dtype in FLOATS):
-            continue
-        if not supported(int(wt.shape[1]), int(wt.shape[0]), int(xt.shape[2]), int(xt.shape[3])):
-            continue
-        users = list(node.users)
-        relu = users[0] if (cfg.fuse and b is None and len(users) == 1 and _is_relu(users[0])) else None
-        last = relu or node
-        with gm.graph.inserting_after(last):
-            new = gm.graph.call_function(conv3x3_int8, (x, w, b, relu is not None, cid))
+        users = list(n.users)
+        fold = cfg.fuse and a["bias"] is None and len(users) == 1 and _is_relu(users[0])
+        last = users[0] if fold else n
+        with g.graph.inserting_after(last):
+            new = g.graph.call_function(conv3x3_int8, (a["input"], a["weight"], a["bias"], fold, cid))
         new.meta.update(last.meta)
         last.replace_all_uses_with(new)
-        if relu is not None:
-            gm.graph.erase_node(relu)
-        gm.graph.erase_node(node)
+        if fold:
+            g.graph.erase_node(users[0])
+        g.graph.erase_node(n)
         count += 1
     return count
 
 
-MAXPOOL2D = {F.max_pool2d, torch.max_pool2d}
-
-
 def _is_pool2(n):
     """A 2x2 / stride-2 max-pool without padding, dilation, ceil mode or returned indices."""
-    if n.op != "call_function" or n.target not in MAXPOOL2D:
+    if not _calls(n, _POOL_FNS):
         return False
-    names = ("input", "kernel_size", "stride", "padding", "dilation", "ceil_mode", "return_indices")
-    args = dict(zip(names, n.args), **n.kwargs)
-    k = args.get("kernel_size")
-    s = args.get("stride")
-    if s is None or (isinstance(s, (list, tuple)) and len(s) == 0):
-        s = k
+    a = _bound(n, ("input", "kernel_size", "stride", "padding", "dilation", "ceil_mode", "return_indices"),
+               {"stride": None, "padding": 0, "dilation": 1, "ceil_mode": False, "return_indices": False})
+    stride = a["stride"]
+    if stride is None or (isinstance(stride, (list, tuple)) and len(stride) == 0):
+        stride = a.get("kernel_size")
     try:
-        return (_pair(k) == (2, 2) and _pair(s) == (2, 2) and _pair(args.get("padding", 0)) == (0, 0)
-                and _pair(args.get("dilation", 1)) == (1, 1) and not args.get("ceil_mode", False)
-                and not args.get("return_indices", False))
+        return (_pair(a.get("kernel_size")) == (2, 2) and _pair(stride) == (2, 2) and _pair(a["padding"]) == (0, 0)
+                and _pair(a["dilation"]) == (1, 1) and not a["ceil_mode"] and not a["return_indices"])
     except TypeError:
         return False
 
@@ -210,7 +268,7 @@ def _chain_convs(gm, cid):
     """conv3x3_int8 -> [ReLU] [2x2 max-pool] -> conv3x3_int8 -> ... where every intermediate has that
     one use -> one xdna::conv3x3_chain, on GPU graphs: the activation stays NHWC int8 from conv to conv
     (the reference lists this as its next step, results/conv3x3_cascade.md:216-222). The ReLU is the
-    graph ReLU after a biased conv, which the conv rewrite does not fuse (backend.py:161-165)."""
+    graph ReLU after a biased conv, which the conv rewrite does not fold (backend.py:161-165)."""
     from .conv import conv3x3_int8
 
     def is_conv(n):
@@ -250,7 +308,7 @@ def _chain_convs(gm, cid):
             if nxt is None:
                 break
             conv_node, relu, pooled, mid = nxt
-            if relu and cur.args[3]:        # a fused ReLU already: a second one changes nothing
+            if relu and cur.args[3]:        # a folded ReLU already: a second one changes nothing
                 relu = False
             relus_after.append(relu)
             pools.append(pooled)
@@ -276,64 +334,30 @@ def _chain_convs(gm, cid):
     return count
 
 
-def _out_features(w):
-    t = w.meta.get("example_value") if isinstance(w, torch.fx.Node) else None
-    return int(t.shape[0]) if isinstance(t, torch.Tensor) else None
-
-
-def _fuse_shared_input(gm, cid):
-    """xdna::linear nodes reading the same input -> one xdna::linear_cat + narrows (one launch)."""
-    groups = {}
-    for node in gm.graph.nodes:
-        if node.op == "call_function" and node.target is torch.ops.xdna.linear.default and not node.args[3]:
-            groups.setdefault(node.args[0], []).append(node)
-    for x, members in groups.items():
-        if len(members) < 2:
-            continue
-        weights = [m.args[1] for m in members]
-        sizes = [_out_features(w) for w in weights]
-        if None in sizes:
-            continue
-        with gm.graph.inserting_before(members[0]):
-            cat = gm.graph.call_function(torch.ops.xdna.linear_cat.default,
-                                         (x, weights, [m.args[2] for m in members], cid))
-            start = 0
-            for m, n in zip(members, sizes):
-                part = gm.graph.call_function(torch.narrow, (cat, -1, start, n))
-                part.meta.update(m.meta)
-                m.replace_all_uses_with(part)
-                start += n
-        for m in members:
-            gm.graph.erase_node(m)
-
-
-def _quantize_in_graph(gm, cid):
-    """xdna::linear / linear_cat -> runtime.linear_int8 (quantize, integer GEMM, dequantize)."""
-    from .runtime import linear_int8
-
-    for node in list(gm.graph.nodes):
-        if node.op != "call_function":
-            continue
-        if node.target is torch.ops.xdna.linear.default:
-            x, w, b, transposed, _ = node.args
-            weights, biases = [w], [b]
-        elif node.target is torch.ops.xdna.linear_cat.default:
-            x, weights, biases, _ = node.args
-            transposed = False
-        else:
-            continue
-        with gm.graph.inserting_after(node):
-            new = gm.graph.call_function(linear_int8, (x, list(weights), list(biases), transposed, cid))
-        new.meta.update(node.meta)
-        node.replace_all_uses_with(new)
-        gm.graph.erase_node(node)
+# ------------------------------------------------------------------------------ entry points
+def offload_gemms(gm: torch.fx.GraphModule, example_inputs, cfg) -> int:
+    """Rewrite the graph's offloadable GEMMs and 3x3 convs in place; return how many sites were taken."""
+    g = _Graph(gm, example_inputs)
+    cid = ops.config_id(cfg)
+    taken = _rewrite_gemms(g, cid)
+    if cfg.fuse:
+        _merge_shared_inputs(g, cid)
+    if cfg.precision == "int8" and cfg.cpu_kernel == "int8":
+        _lower_to_int8(g, cid)
+    taken += _rewrite_convs(g, cid, cfg)
+    if cfg.fuse:
+        _chain_convs(gm, cid)
+    gm.graph.lint()
+    gm.recompile()
+    return taken
 
 
 def _compile(gm, example_inputs, cfg):
-    n = offload_gemms(gm, example_inputs, cfg)
+    """The rewritten graph, run eagerly (fallback "eager") or compiled by Inductor."""
+    taken = offload_gemms(gm, example_inputs, cfg)
     if cfg.verbose:
-        log.warning("torch_xdna: %d GEMMs / convs offloadable in a graph of %d nodes (policy=%s, fallback=%s)",
-                    n, len(gm.graph.nodes), cfg.policy, cfg.fallback)
+        log.warning("torch_xdna: %d GEMM / conv sites offloadable in a graph of %d nodes (policy=%s, fallback=%s)",
+                    taken, len(gm.graph.nodes), cfg.policy, cfg.fallback)
     if cfg.fallback == "eager":
         return gm.forward
     from torch._inductor.compile_fx import compile_fx
@@ -342,13 +366,15 @@ def _compile(gm, example_inputs, cfg):
 
 
 def xdna_backend(gm: torch.fx.GraphModule, example_inputs, options=None, mode=None):
-    """The torch.compile backend; `options` are torch_xdna.Config fields."""
+    """The torch.compile backend registered as "xdna"; `options` are torch_xdna.Config fields. A
+    transformer stack the GPU runs as one op (stack.py) is split off first: the graph is then
+    compiled twice, as the fused stack and as above, and a dispatcher picks per call."""
     cfg = _config.config.merged(options)
+    stack_plan = None
     if cfg.stacks and cfg.policy != "cpu" and kernels.available():
         from . import stack
 
-        plan = stack.find(gm, example_inputs)
-        if plan is not None:
-            # the graph twice: the stack as one GPU op, and as usual; a dispatcher picks per call
-            return stack.compile_fused(gm, example_inputs, cfg, ops.config_id(cfg), plan, _compile)
-    return _compile(gm, example_inputs, cfg)
+        stack_plan = stack.find(gm, example_inputs)
+    if stack_plan is None:
+        return _compile(gm, example_inputs, cfg)
+    return stack.compile_fused(gm, example_inputs, cfg, ops.config_id(cfg), stack_plan, _compile)

@@ -106,6 +106,7 @@ def _declare(L):
         "xdna_nhwc_to_nchw_i8": ([p, i64, i64, i64, i64, p, p], i),
         "xdna_tile_set": ([i, i64, i64, i64, i], i),
         "xdna_tile_get": ([i, i64, i64, i64], i),
+        "xdna_tile_plan": ([i, i64, i64, i64, p, p, p], i),
         "xdna_tile_clear": ([], i),
         "xdna_rmsnorm_bf16": ([p, i64, i64, p, i, ctypes.c_float, p, p], i),
         "xdna_qk_norm_rope": ([p, i64, i, i, p, p, i, p, p, p, ctypes.c_float, p, p, p, i64, p], i),
@@ -121,7 +122,7 @@ def _declare(L):
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
            "xdna_gemm_i8_dequant", "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc", "xdna_conv_weight_pack",
            "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8", "xdna_nhwc_to_nchw_i8",
-           "xdna_tile_set", "xdna_tile_get", "xdna_tile_clear", "xdna_rmsnorm_bf16", "xdna_qk_norm_rope",
+           "xdna_tile_set", "xdna_tile_get", "xdna_tile_plan", "xdna_tile_clear", "xdna_rmsnorm_bf16", "xdna_qk_norm_rope",
            "xdna_attention_bf16", "xdna_silu_mul_bf16", "xdna_add_f32")
 
 
@@ -209,10 +210,22 @@ def tile_clear():
     _check(lib().xdna_tile_clear(), "tile_clear")
 
 
+def tile_plan(dev, kind, M, N, K):
+    """(head tile, m1, tail tile) of the next launch of (kind, M, N, K) on dev: rows [0, m1) with the
+    head tile and rows [m1, M) with the tail tile, or (head, 0, "auto") for one launch."""
+    head, m1, tail = ctypes.c_int(), ctypes.c_int64(), ctypes.c_int()
+    with _on(dev):
+        _check(lib().xdna_tile_plan(KINDS.get(kind, kind), M, N, K, ctypes.byref(head), ctypes.byref(m1),
+                                    ctypes.byref(tail)), "tile_plan")
+    return TILES[head.value], m1.value, TILES[tail.value]
+
+
 def gemm_variant(dev, M, N, K, kind=KIND_I8) -> str:
-    """Which GEMM kernel runs for M x N x K (the library's choice): one NPU-program key of the
-    reference (runtime.py:207) corresponds to one (variant, N, K) here."""
-    return tile_get(dev, kind, M, N, K)
+    """The kernels a GEMM of M x N x K runs (the library's plan): the head tile, and after a tail split
+    "+<tail tile>@<first tail row>". One NPU-program key of the reference (runtime.py:207)
+    corresponds to one (variant, N, K) here."""
+    head, m1, tail = tile_plan(dev, kind, M, N, K)
+    return head if m1 == 0 else f"{head}+{tail}@{m1}"
 
 
 TUNED_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tuned", "mi355x.json")

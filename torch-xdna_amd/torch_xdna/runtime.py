@@ -198,7 +198,6 @@ def _cpu_linear(x2d, qw, bias, dtype):
 
 # ------------------------------------------------------------------------------ the GPU route
 _verified = {}    # program key -> True once a launch of it matched the CPU
-VERIFY = "first"  # set from Config.verify per call: "first" | "always" | "off"
 
 
 class GPUResultMismatch(RuntimeError):
@@ -208,11 +207,21 @@ class GPUResultMismatch(RuntimeError):
 NPUResultMismatch = GPUResultMismatch   # the reference's name
 
 
-def _check(key, got, want, exact=True):
-    """Compare one launch with the CPU route unless this program was already verified: bit for bit,
-    or (exact=False, the bf16 GEMM) to the reference's 5e-2 relative norm with finite values
-    (runtime.py:174-188)."""
-    if VERIFY == "off" or (VERIFY == "first" and _verified.get(key)):
+def _program(cfg, kind, dev, R, qw, dtype=None):
+    """The verify key of a GPU GEMM call: what the reference's key names for an NPU program
+    (runtime.py:207: dtype, row bucket, Np, Kp, tiling), here the kernel kind, the library's launch
+    plan for these rows (head tile, and a tail split's first row and tile), the row bucket, N, K and
+    the output dtype."""
+    tk = kernels.KIND_BF16 if kind == "bf16" else kernels.KIND_I8
+    plan = kernels.gemm_variant(dev, R, qw.N, qw.Kp, tk)
+    return (kind, plan, _bucket(R, cfg.row_buckets), qw.N, qw.K, None if dtype is None else str(dtype))
+
+
+def _check(cfg, key, got, want, exact=True):
+    """Compare one launch with the CPU route unless this program was already verified (Config.verify
+    "first"; "always" checks every launch, "off" none): bit for bit, or (exact=False, the bf16 GEMM)
+    to the reference's 5e-2 relative norm with finite values (runtime.py:174-188)."""
+    if cfg.verify == "off" or (cfg.verify == "first" and _verified.get(key)):
         return
     want = want()
     got = got.cpu()
@@ -233,7 +242,7 @@ def _check(key, got, want, exact=True):
     _verified[key] = True
 
 
-def _gpu_linear(x2d, qw, bias, dtype):
+def _gpu_linear(cfg, x2d, qw, bias, dtype):
     """y [R, N] = W8A8(x2d) on the GPU: quantize kernel, then the GEMM with the fused dequantize."""
     dev = kernels.gpu_device(x2d)
     xg = x2d.to(dev)
@@ -242,12 +251,11 @@ def _gpu_linear(x2d, qw, bias, dtype):
     b = None if bias is None else bias.to(dev, torch.float32).contiguous()
     y = kernels.mm_i8_dequant(xq, sx, wq, sw, b, dtype)
     stats.launches += 1
-    key = ("dq", kernels.gemm_variant(dev, x2d.shape[0], qw.N, qw.Kp), qw.N, qw.K, str(dtype))
-    _check(key, y, lambda: _cpu_linear(x2d, qw, bias, dtype))
+    _check(cfg, _program(cfg, "dq", dev, x2d.shape[0], qw, dtype), y, lambda: _cpu_linear(x2d, qw, bias, dtype))
     return y
 
 
-def _gpu_bf16(x2d, qw, bias, dtype):
+def _gpu_bf16(cfg, x2d, qw, bias, dtype):
     """y [R, N] of precision "bf16" on the GPU: bf16 operands, float32 accumulation and bias, cast to
     dtype, one kernel (runtime.py:212-237, :299-313)."""
     dev = kernels.gpu_device(x2d)
@@ -256,14 +264,13 @@ def _gpu_bf16(x2d, qw, bias, dtype):
     b = None if bias is None else bias.to(dev, torch.float32).contiguous()
     y = kernels.mm_bf16(xb, wb, b, dtype)
     stats.launches += 1
-    key = ("bf16", kernels.gemm_variant(dev, x2d.shape[0], qw.N, qw.Kp, kernels.KIND_BF16), qw.N, qw.K, str(dtype))
 
     def want():     # the reference's check: the bf16 operands multiplied in float32 (runtime.py:233-234)
         yb = xb[:, :qw.K].cpu().float() @ wb[:, :qw.K].cpu().float().t()
         if bias is not None:
             yb += bias.cpu().float()
         return yb.to(dtype)
-    _check(key, y, want, exact=False)
+    _check(cfg, _program(cfg, "bf16", dev, x2d.shape[0], qw, dtype), y, want, exact=False)
     return y
 
 
@@ -275,15 +282,14 @@ def _cpu_bf16(x2d, w_fp, bias, dtype):
     return y.to(dtype)
 
 
-def _gpu_acc(xq, qw):
+def _gpu_acc(cfg, xq, qw):
     """int32 [R, N] on the GPU from int8 [R, K] (xdna::linear_i8)."""
     dev = kernels.gpu_device(xq)
     wq, _ = qw.gpu(dev)
     a = kernels.pad_k(xq.to(dev), qw.Kp)
     acc = kernels.mm_i8(a, wq)
     stats.launches += 1
-    key = ("i8", kernels.gemm_variant(dev, xq.shape[0], qw.N, qw.Kp), qw.N, qw.K)
-    _check(key, acc, lambda: _cpu_acc(xq, qw))
+    _check(cfg, _program(cfg, "i8", dev, xq.shape[0], qw), acc, lambda: _cpu_acc(xq, qw))
     return acc
 
 
@@ -374,8 +380,6 @@ def _fp_only(cfg):
 # ------------------------------------------------------------------------------ the ops
 def _linear_impl(cfg, x, qw, bias, w_fp_fn):
     """Shared body of linear / linear_cat (runtime.py:326-355, :402-434)."""
-    global VERIFY
-    VERIFY = cfg.verify
     shape = x.shape[:-1]
     x2d = x.reshape(-1, x.shape[-1])
     R = x2d.shape[0]
@@ -384,12 +388,12 @@ def _linear_impl(cfg, x, qw, bias, w_fp_fn):
     if cfg.precision == "bf16":
         # runtime.py:299-313 / :340-345: the bf16 GEMM on the GPU, the float32 GEMM on the CPU
         with _lock:
-            device = _choose(cfg, R, qw, on_gpu, lambda: _gpu_bf16(x2d, qw, bias, x.dtype),
+            device = _choose(cfg, R, qw, on_gpu, lambda: _gpu_bf16(cfg, x2d, qw, bias, x.dtype),
                              lambda: _cpu_bf16(x2d, w_fp_fn(), bias, x.dtype))
             y = None
             if device == "gpu":
                 try:
-                    y = _gpu_bf16(x2d, qw, bias, x.dtype)
+                    y = _gpu_bf16(cfg, x2d, qw, bias, x.dtype)
                 except Exception as e:
                     _gpu_failed(cfg, R, qw, e)
                     device = "cpu"
@@ -398,12 +402,12 @@ def _linear_impl(cfg, x, qw, bias, w_fp_fn):
         _account(device, t0, R, qw)
         return y.to(x.device).reshape(*shape, qw.N)
     with _lock:
-        device = _choose(cfg, R, qw, on_gpu, lambda: _gpu_linear(x2d, qw, bias, x.dtype),
+        device = _choose(cfg, R, qw, on_gpu, lambda: _gpu_linear(cfg, x2d, qw, bias, x.dtype),
                          lambda: _cpu_linear(x2d, qw, bias, x.dtype))
         y = None
         if device == "gpu":
             try:
-                y = _gpu_linear(x2d, qw, bias, x.dtype)
+                y = _gpu_linear(cfg, x2d, qw, bias, x.dtype)
             except Exception as e:  # launch failure or mismatch: this shape moves to the CPU
                 _gpu_failed(cfg, R, qw, e)
                 device = "cpu"
@@ -470,8 +474,6 @@ def linear_int8(x, weights, biases, transposed: bool, cfg_id: int):
 
 def linear_i8(cfg, xq, weights, transposed):
     """(int32 acc [R, N], weight scales [N]) of xdna::linear_i8 (runtime.py:377-399)."""
-    global VERIFY
-    VERIFY = cfg.verify
     t0 = time.perf_counter()
     qw = qweight(weights[0] if len(weights) == 1 else list(weights), transposed)
     dev = xq.device
@@ -479,11 +481,11 @@ def linear_i8(cfg, xq, weights, transposed):
         return xq.new_zeros((0, qw.N), dtype=torch.int32), qw.sw(dev).to(dev).clone()
     on_gpu = dev.type == "cuda"
     with _lock:
-        device = _choose(cfg, xq.shape[0], qw, on_gpu, lambda: _gpu_acc(xq, qw), lambda: _cpu_acc(xq, qw))
+        device = _choose(cfg, xq.shape[0], qw, on_gpu, lambda: _gpu_acc(cfg, xq, qw), lambda: _cpu_acc(xq, qw))
         acc = None
         if device == "gpu":
             try:
-                acc = _gpu_acc(xq, qw)
+                acc = _gpu_acc(cfg, xq, qw)
             except Exception as e:  # launch failure or mismatch: this shape moves to the CPU
                 _gpu_failed(cfg, xq.shape[0], qw, e)
                 device = "cpu"
