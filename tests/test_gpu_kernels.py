@@ -7,6 +7,8 @@ compares with oracle/ (numpy restatement; the C restatement for the larger integ
     for bit after the round-to-nearest-even cast (the 1e-6 relative / 1 ulp bound of the contract
     is not needed: the fused epilogue rounds exactly like the reference's CPU ops).
 """
+import re
+
 import numpy as np
 import pytest
 import torch
@@ -344,7 +346,7 @@ def tile_table():
 @pytest.mark.parametrize("tile", ["t256x256w8", "t256x256w4", "t256x128", "t128x256", "t128x128", "t64x64",
                                   "t192x256", "t256x192", "t64x32", "t32x64", "t32x32",
                                   "t64x64k2", "t64x64k4", "t32x64k4", "t32x32k4", "t128x128k2", "t128x256w8",
-                                  "t256x128w8"])
+                                  "t256x128w8", "t256x256pp"])
 def test_tiles_forced(gpu, tile, tile_table):
     """Each tile configuration of the engine, forced through the library's tile table: int32 and
     fused bf16 GEMMs with partial tiles and K both a multiple of 64 and not (for the K-group tiles:
@@ -389,7 +391,7 @@ def test_tiles_forced(gpu, tile, tile_table):
             assert kernels.conv3x3_calibrate(x_nhwc, packed.to(gpu), False) == int(np.abs(acc).max())
 
 
-@pytest.mark.parametrize("tile", ["t256x256w8", "t256x128w8", "t128x256"])
+@pytest.mark.parametrize("tile", ["t256x256w8", "t256x128w8", "t128x256", "t256x256pp"])
 def test_tiles_tail_split(gpu, tile, tile_table):
     """A one-workgroup-per-CU tile whose last round of tiles would fill at most half of the CUs runs the
     whole rounds with that tile and the leftover rows as a second launch (for the conv, from a pixel
@@ -401,7 +403,7 @@ def test_tiles_tail_split(gpu, tile, tile_table):
     from torch_xdna import kernels
 
     cus = kernels.num_cus(gpu)
-    bm, bn = (int(v) for v in tile[1:].split("w")[0].split("x"))
+    bm, bn = (int(v) for v in re.match(r"t(\d+)x(\d+)", tile).groups())
     n, k = bn, 64
     for m, tail in [(bm * (cus + cus // 4), None), (bm * (cus + cus // 4) - 100, None),
                     (bm * (cus + cus // 4) - 100, "t128x128k2")]:
@@ -438,6 +440,35 @@ def test_tiles_tail_split(gpu, tile, tile_table):
         kernels.tile_set("conv", h * w_ - bm * cus, co, 9 * ci, tail or "auto")
         q = kernels.conv3x3(x_nhwc, packed.to(gpu), 9, True)
         assert np.array_equal(_np(q).transpose(0, 3, 1, 2), want), (tile, tail, h, w_)
+
+
+@pytest.mark.parametrize("m,n,k", [(4100, 4100, 208), (2600, 7000, 1040), (8192, 2304, 4096), (300, 520, 4160),
+                                   (2600, 7000, 256), (2600, 7000, 192), (2600, 7000, 112), (2600, 7000, 64)])
+def test_pp_tile(gpu, m, n, k, tile_table):
+    """The ping-pong tile (t256x256pp: two groups of four waves alternating memory and MFMA phases):
+    more tiles than CUs with partial last row / column tiles, K not a multiple of 64, fewer tiles than
+    CUs, and K of a few slices (fewer slices than LDS stages). int32 sums against torch._int_mm on the CPU (the reference's CPU kernel),
+    the fused bf16 dequant against the CPU dequantize of those sums, and the bf16 GEMM bit for bit against
+    the 8-wave tile, which sums the same products in the same order."""
+    from torch_xdna import kernels
+
+    for kind, kk in (("i8", k), ("bf16", k // 2)):
+        kernels.tile_set(kind, m, n, kk, "t256x256pp")
+    assert kernels.tile_plan(gpu, "i8", m, n, k)[0] == "t256x256pp"
+    a, w = _i8((m, k), seed=m + k), _i8((n, k), seed=n + k)
+    acc = kernels.mm_i8(a.to(gpu), w.to(gpu)).cpu()
+    want = torch._int_mm(a, w.t().contiguous())
+    assert torch.equal(acc, want), f"{int((acc != want).sum())} sums differ"
+    sx, sw, b = torch.rand(m) + 0.01, torch.rand(n) * 0.01, torch.randn(n)
+    y = kernels.mm_i8_dequant(a.to(gpu), sx.to(gpu), w.to(gpu), sw.to(gpu), b.to(gpu), torch.bfloat16).cpu()
+    assert torch.equal(y, ((want.float() * sx[:, None]) * sw[None, :] + b[None, :]).to(torch.bfloat16))
+    x = _rand((m, k // 2), torch.float32, seed=m).to(gpu)
+    wf = _rand((n, k // 2), torch.float32, seed=n, scale=0.05).to(gpu)
+    xb, wb = kernels.bf16_rows(x, k // 2), kernels.bf16_rows(wf, k // 2)
+    yp = kernels.mm_bf16(xb, wb, None, torch.float32)
+    kernels.tile_set("bf16", m, n, k // 2, "t256x256w8")
+    yw = kernels.mm_bf16(xb, wb, None, torch.float32)
+    assert torch.equal(yp, yw), "ping-pong and 8-wave bf16 sums differ"
 
 
 @pytest.mark.parametrize("tile", ["small_w1", "small_w2", "small_w4", "small_w8", "small_w16", "t64x64", "t128x128"])

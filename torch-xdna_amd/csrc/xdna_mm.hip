@@ -292,6 +292,9 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
+// Wait for every LDS access of this wave (no vector-memory wait).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+
 // Scheduling groups for __builtin_amdgcn_sched_group_barrier.
 constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100;
 
@@ -336,7 +339,7 @@ struct PinTwo {
 // barriers; at the end groups 1 .. KG-1 leave their accumulators in LDS and group 0 adds them before
 // the epilogue. It multiplies the loads in flight and the MFMA streams of a tile for shapes with few
 // tiles and deep K (integer sums are exact in any order).
-template <int BM, int BN, int WM, int WN, int S, int CONVM, int EPI, bool KFULL, int KG = 1>
+template <int BM, int BN, int WM, int WN, int S, int CONVM, int EPI, bool KFULL, int KG = 1, bool PP = false>
 __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t* __restrict__ a, int64_t lda,
                                                                const int8_t* __restrict__ w, int64_t ldw, int64_t M,
                                                                int64_t N, int64_t K, ConvGeom cg, EpiArgs e) {
@@ -531,6 +534,53 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
       }
   };
 
+  if constexpr (PP) {
+    // Ping-pong schedule: the 8 waves form two groups of 4 (group = wm: waves 0-3 own rows [0, BM/2),
+    // waves 4-7 rows [BM/2, BM)); wave w runs on SIMD w % 4, so every SIMD holds one wave of each
+    // group. The workgroup steps through phases separated by barriers; in each phase one group runs a
+    // memory phase (its share of the DMA of slice t + S - 1, then all 2 x (FM + FN) fragments of slice
+    // t from LDS) while the other runs the 2 x FM x FN MFMAs of the slice it read in the phase before,
+    // as one uninterrupted stream. Group 1 runs one phase behind group 0, so each SIMD's MFMA pipe
+    // always has one wave feeding it while the other waits on memory.
+    //   phase 2t:     group 0 memory (slice t)   group 1 MFMAs (slice t - 1)
+    //   phase 2t + 1: group 0 MFMAs (slice t)    group 1 memory (slice t)
+    // Slice t + S - 1 goes into the stage of slice t - 1, which both groups finished reading by the end
+    // of phase 2t - 1. Before the barrier that ends phase 2t + 1 every wave has waited for its share of
+    // slice t + 1 (issued at least S - 2 slices earlier), so group 0 reads a complete slice in phase
+    // 2t + 2. Every wave passes 2 nk + 2 barriers.
+    static_assert(NW == 8 && WM == 2 && KG == 1, "ping-pong: two groups of four waves");
+    const int grp = wm;
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) dma_slice(s, lds + s * STAGE);
+    wait_vmcnt<(S - 2) * NDMA>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (grp == 1) {
+      __builtin_amdgcn_s_barrier();      // group 1 starts one phase behind
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    int cur_s = 0;
+    for (int64_t t = 0; t < nk; ++t) {
+      const int prev_s = cur_s == 0 ? S - 1 : cur_s - 1;
+      dma_slice(t + S - 1, lds + prev_s * STAGE);
+      const int8_t* cur = lds + cur_s * STAGE;
+      read_frags(cur, 0, 0);
+      read_frags(cur, 1, 1);
+      if (grp == 1) wait_vmcnt_lgkm0<(S - 2) * NDMA>();
+      else wait_lgkm0();
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(0);
+      mfmas(1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (grp == 0) wait_vmcnt<(S - 2) * NDMA>();
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      cur_s = cur_s + 1 == S ? 0 : cur_s + 1;
+    }
+    if (grp == 0) __builtin_amdgcn_s_barrier();
+  } else {
   // prologue: the group's slices 0 .. S-1 into stages 0 .. S-1, then wait for slice 0
 #pragma unroll
   for (int s = 0; s < S; ++s) dma_slice(kg + (int64_t)KG * s, lds + s * STAGE);
@@ -564,6 +614,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
     PinTwo<SG_VMEM_READ, NDMA, SG_DS_READ, NRD, NMF>::emit();
     __builtin_amdgcn_sched_barrier(0);
     cur_s = nxt_s;
+  }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -925,7 +976,8 @@ constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128
               T_64x64 = 6, T_SMALL1 = 7, T_SMALL2 = 8, T_SMALL4 = 9, T_SMALL8 = 10, T_SMALL16 = 11,
               T_192x256 = 12, T_256x192 = 13, T_64x32 = 14, T_32x64 = 15, T_32x32 = 16, T_GEMV4 = 17,
               T_GEMV2 = 18, T_GEMV8 = 19, T_SEG4R2 = 20, T_SEG4R4 = 21, T_64x64K2 = 22, T_64x64K4 = 23,
-              T_32x64K4 = 24, T_32x32K4 = 25, T_128x128K2 = 26, T_128x256W8 = 27, T_256x128W8 = 28, T_COUNT = 29;
+              T_32x64K4 = 24, T_32x32K4 = 25, T_128x128K2 = 26, T_128x256W8 = 27, T_256x128W8 = 28,
+              T_256x256PP = 29, T_COUNT = 30;
 
 static_assert(T_SMALL2 == T_SMALL1 + 1 && T_SMALL4 == T_SMALL1 + 2 && T_SMALL8 == T_SMALL1 + 3 &&
                   T_SMALL16 == T_SMALL1 + 4,
@@ -955,6 +1007,7 @@ inline TileCfg tile_cfg(int t) {
     case T_128x128K2: return {128, 128, 4, 2};
     case T_128x256W8: return {128, 256, 8, 1};
     case T_256x128W8: return {256, 128, 8, 1};
+    case T_256x256PP: return {256, 256, 8, 1};
     default: return {64, 64, 4, 1};
   }
 }
@@ -1067,7 +1120,11 @@ int launch_tiles_once(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw
   else mm_tile_kernel<BM_, BN_, WM_, WN_, S_, CONVM, EPI, false, KG_><<<grid, WM_ * WN_ * KG_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
 #define XDNA_TILE_W(BM_, BN_, WM_, WN_, S_) XDNA_TILE_WK(BM_, BN_, WM_, WN_, S_, 1)
 #define XDNA_TILE(BM_, BN_, S_) XDNA_TILE_W(BM_, BN_, 2, 2, S_)
-  if (t.kg > 1) {
+  if (tile == T_256x256PP) {
+    // the ping-pong schedule: 4 stages (S - 2 = 2 slices between a DMA and its use)
+    if (kfull) mm_tile_kernel<256, 256, 2, 4, 4, CONVM, EPI, true, 1, true><<<grid, 512, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
+    else mm_tile_kernel<256, 256, 2, 4, 4, CONVM, EPI, false, 1, true><<<grid, 512, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
+  } else if (t.kg > 1) {
     // K groups (in-workgroup split-K) for tiles with few tiles and deep K
     if (t.bm == 128) {
       XDNA_TILE_WK(128, 128, 2, 2, 4, 2)
@@ -1144,7 +1201,8 @@ TilePlan plan_tiles(int kind, int64_t M, int64_t N, int64_t kbytes, int64_t ktab
   // unsplit, 72.7 us with a 128 x 128 tail (the rule's) and 69.4 us with the 128 x 256 one.
   int tail = tile_lookup(kind, M - m1, N, ktab);
   if (is_small(tail) || is_gemv(tail) || is_seg4(tail)) tail = T_AUTO;
-  if (tail == T_AUTO) tail = tile == T_256x256W8 ? T_128x256W8 : rule_tile(M - m1, N, kbytes, false);
+  if (tail == T_AUTO)
+    tail = (tile == T_256x256W8 || tile == T_256x256PP) ? T_128x256W8 : rule_tile(M - m1, N, kbytes, false);
   // only when the leftover rows fit one round of the tail's tiles (8192 x 3072 in 256 x 256 tiles leaves
   // 2816 rows, 264 tiles of 128 x 256: measured slower split than not)
   const TileCfg tt = tile_cfg(tail);

@@ -258,6 +258,74 @@ __global__ __launch_bounds__(256) void quant_rows_wave_kernel(const void* __rest
   for (int64_t c = k + t; c < k_pad; c += 64) qr[c] = 0;
 }
 
+// The same quantize with persistent waves: wave i of the grid walks rows i, i + W, i + 2W, ... (W waves in
+// the grid), and the 16-byte loads of its next row are issued before the current row's max, quantize and
+// stores, so loads, arithmetic and stores of different rows overlap (with one row per wave they run in
+// three bursts). Two register sets alternate between the rows.
+template <int DT, int G, bool NT>
+__global__ __launch_bounds__(256) void quant_rows_pipe_kernel(const void* __restrict__ x, int64_t rows, int64_t k,
+                                                              int64_t ld_x, int8_t* __restrict__ q, int64_t ld_q,
+                                                              int64_t k_pad, float* __restrict__ s) {
+  using V = Vec16<DT>;
+  constexpr int VEC = V::N;
+  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
+  constexpr int LPG = 16 / VEC;
+  const int t = threadIdx.x & 63;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  const int ng = (int)(k / 16);
+  const uint32_t row_bytes = (uint32_t)(k * ESZ);
+  auto load = [&](int64_t row, V (&v)[G][LPG]) {
+    // rows past the end read zeros (out-of-range resource); the row as its own buffer resource
+    const __amdgpu_buffer_rsrc_t rr =
+        make_rsrc(reinterpret_cast<const char*>(x) + (row < rows ? row : 0) * ld_x * ESZ, row < rows ? row_bytes : 0u);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const uint32_t off = (uint32_t)(t + j * 64) * (16 * ESZ);
+#pragma unroll
+      for (int l = 0; l < LPG; ++l) v[j][l].raw = buf_load_u4<NT>(rr, off + l * 16);
+    }
+  };
+  auto process = [&](int64_t row, const V (&v)[G][LPG]) {
+    AbsMaxBits<DT> am;
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int l = 0; l < LPG; ++l) am.add(v[j][l]);
+    const float amax = bits_to_abs<DT>(wave_max_i(am.lane_bits()));
+    const float sc = scale_from_amax(amax);
+    const float rc = 1.0f / sc;
+    if (t == 0) s[row] = sc;
+    int8_t* qr = q + row * ld_q;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const int gi = t + j * 64;
+      if (gi < ng) {
+        float f[16];
+#pragma unroll
+        for (int l = 0; l < LPG; ++l)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) f[l * VEC + e] = v[j][l].get(e);
+        uint32_t w[4];
+        quant_pack<16>(f, sc, rc, w);
+        *reinterpret_cast<uint4*>(qr + (int64_t)gi * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+    for (int64_t c = k + t; c < k_pad; c += 64) qr[c] = 0;
+  };
+  V va[G][LPG], vb[G][LPG];
+  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  load(row, va);
+  while (row < rows) {                   // wave-uniform: no barrier in the loop
+    load(row + stride, vb);
+    process(row, va);
+    row += stride;
+    if (row >= rows) break;
+    load(row + stride, va);
+    process(row, vb);
+    row += stride;
+  }
+}
+
 // Long rows (more than 512 vectors): persistent blocks of 256 threads walk rows with a grid stride;
 // each thread holds up to MAXV 16-byte vectors of a row, and the loads of the block's next row are
 // issued before this row's reduction and quantize, so HBM sees a continuous stream. The partial
@@ -345,15 +413,15 @@ __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(const void* __re
 }
 
 // Blocks of a persistent streaming kernel: as many as are resident at once (the runtime's occupancy
-// for 256 threads, cached per kernel and device), at most one per row.
-template <typename F>
-unsigned stream_blocks(F kernel, int64_t rows) {
+// for 256 threads, cached per kernel and device), at most `rows`.
+template <auto KERNEL>
+unsigned stream_blocks(int64_t rows) {
   static int per_cu[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   if (per_cu[dev] == 0) {
     int n = 0;
-    per_cu[dev] = (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) == hipSuccess && n > 0) ? n : 1;
+    per_cu[dev] = (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, KERNEL, 256, 0) == hipSuccess && n > 0) ? n : 1;
   }
   return (unsigned)std::max<int64_t>(1, std::min<int64_t>(rows, (int64_t)per_cu[dev] * device_cus()));
 }
@@ -377,6 +445,31 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
   if (k % 16 == 0 && k < (int64_t(1) << 31) && gpl <= (DT == XDNA_F32 ? 8 : 16) && !(few && gpl > 2)) {
     const bool nt = rows * k * (DT == XDNA_F32 ? 4 : 2) >= (int64_t(128) << 20);   // half the Infinity Cache
     const dim3 grid((unsigned)cdiv(rows, 4));
+    // rows of up to 4096 elements, at least 8 per CU: one round of resident workgroups whose waves take the
+    // rows beyond it, so the loads of a wave's next row overlap this row's arithmetic (a sweep of 1, 2, 4,
+    // 8 and 16 rows per wave on MI355X: 4.5 TB/s at one or two on 8192 x 4096 bf16, against 2.7 TB/s for
+    // two rounds of one-row waves; more rows per wave leave too few waves in flight)
+    if (gpl <= 4 && k * (DT == XDNA_F32 ? 4 : 2) < (int64_t(1) << 31) && rows >= 8 * (int64_t)device_cus()) {
+      const int64_t want = cdiv(rows, 4);
+      const unsigned pb = gpl <= 1 ? stream_blocks<quant_rows_pipe_kernel<DT, 1, false>>(want)
+                          : gpl <= 2 ? stream_blocks<quant_rows_pipe_kernel<DT, 2, false>>(want)
+                                     : stream_blocks<quant_rows_pipe_kernel<DT, 4, false>>(want);
+      {
+        const dim3 pg(pb);
+#define XDNA_QP(G_)                                                                                        \
+  if (nt) quant_rows_pipe_kernel<DT, G_, true><<<pg, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s); \
+  else quant_rows_pipe_kernel<DT, G_, false><<<pg, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
+        if (gpl <= 1) {
+          XDNA_QP(1)
+        } else if (gpl <= 2) {
+          XDNA_QP(2)
+        } else {
+          XDNA_QP(4)
+        }
+#undef XDNA_QP
+        return launch_status("quant_rows");
+      }
+    }
 #define XDNA_QW(G_)                                                                                     \
   if (nt) quant_rows_wave_kernel<DT, G_, true><<<grid, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s); \
   else quant_rows_wave_kernel<DT, G_, false><<<grid, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
@@ -397,10 +490,10 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
   if (nvec <= 64 * 8 && !few) {  // one wavefront per row, four rows per block
     quant_rows_vec_kernel<DT, 64, 8><<<dim3((unsigned)cdiv(rows, 4)), 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
   } else if (nvec <= 256 * 8) {
-    quant_rows_stream_kernel<DT, 8><<<dim3(stream_blocks(quant_rows_stream_kernel<DT, 8>, rows)), 256, 0, st>>>(
+    quant_rows_stream_kernel<DT, 8><<<dim3(stream_blocks<quant_rows_stream_kernel<DT, 8>>(rows)), 256, 0, st>>>(
         x, rows, k, ld_x, q, ld_q, k_pad, s);
   } else if (nvec <= 256 * 16) {
-    quant_rows_stream_kernel<DT, 16><<<dim3(stream_blocks(quant_rows_stream_kernel<DT, 16>, rows)), 256, 0, st>>>(
+    quant_rows_stream_kernel<DT, 16><<<dim3(stream_blocks<quant_rows_stream_kernel<DT, 16>>(rows)), 256, 0, st>>>(
         x, rows, k, ld_x, q, ld_q, k_pad, s);
   } else {               // one block per row, the row read twice
     quant_rows_vec_kernel<DT, 256, 16><<<dim3((unsigned)rows), 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
@@ -441,22 +534,89 @@ __global__ __launch_bounds__(256) void image_absmax_kernel(const void* __restric
   constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
   const char* xb = reinterpret_cast<const char*>(x) + b * per * ESZ;
   float m = 0.0f;
-  const bool vec_ok = ((per * ESZ) % 16 == 0) && aligned(x, 16);
+  const bool vec_ok = ((per * ESZ) % 16 == 0) && aligned(x, 16) && per * ESZ < (int64_t(1) << 31);
   if (vec_ok) {
+    // U 16-byte loads per lane in flight per step (a branch-free buffer resource over the image: past its
+    // end they read zeros); magnitude bits keep a NaN as torch.amax does
+    constexpr int U = 16;
     using V = Vec16<DT>;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(xb, (uint32_t)(per * ESZ));
     const int64_t nvec = per * ESZ / 16;
-    for (int64_t iv = (int64_t)blockIdx.x * 256 + threadIdx.x; iv < nvec; iv += (int64_t)gridDim.x * 256) {
-      V u;
-      u.raw = *reinterpret_cast<const uint4*>(xb + iv * 16);
+    AbsMaxBits<DT> am;
+    for (int64_t base = (int64_t)blockIdx.x * 256 * U + threadIdx.x; base < nvec; base += (int64_t)gridDim.x * 256 * U) {
+      V u[U];
 #pragma unroll
-      for (int e = 0; e < V::N; ++e) m = fmaxf(m, fabsf(u.get(e)));
+      for (int j = 0; j < U; ++j) {
+        const int64_t iv = base + j * 256;
+        u[j].raw = buf_load_u4(r, iv < nvec ? (uint32_t)(iv * 16) : OOB);
+      }
+#pragma unroll
+      for (int j = 0; j < U; ++j) am.add(u[j]);
     }
+    m = bits_to_abs<DT>(am.lane_bits());
   } else {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < per; i += (int64_t)gridDim.x * 256)
       m = fmaxf(m, fabsf(load_as_f32<DT>(xb, i)));
   }
   m = group_max<256>(m, red);
   if (threadIdx.x == 0) parts[b * AMAX_PARTS + blockIdx.x] = m;
+}
+
+// Quantize + NCHW -> NHWC with 16-byte accesses on both sides: a block (256 threads) covers 256
+// channels x TP = 16 * PPL pixels (PPL = pixels per 16-byte load: 4 float32, 8 bf16 / fp16). Wave w owns
+// channels c0 + 64 w .. + 63; in load i lane l reads channel c0 + 64 w + 16 (l / 16) + i at pixels
+// PPL (l % 16) .. + PPL (16 lanes read a channel's 16 PPL contiguous pixels), so each lane ends with 16
+// consecutive channels of PPL pixels, quantizes each pixel's 16 channels into one 16-byte LDS word of the
+// tile [TP][256] and the tile leaves as 16-byte stores, 256 contiguous channel bytes per pixel.
+// Channels past ch read as zeros (quantized 0); needs hw % PPL == 0 and an image below 2 GB.
+template <int DT>
+__global__ __launch_bounds__(256) void conv_quant_nhwc_vec_kernel(const void* __restrict__ x, int64_t ch, int64_t hw,
+                                                                  const float* __restrict__ parts, int nparts,
+                                                                  int8_t* __restrict__ q, int64_t c_pad,
+                                                                  float* __restrict__ sx) {
+  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
+  constexpr int PPL = 16 / ESZ, TP = 16 * PPL;
+  // tile [TP][256] bytes; 16-byte chunk c of row p at chunk c ^ ((p / PPL) % 16): the 16 rows one write
+  // instruction spans (PPL apart) and the 16 chunks of a row one read spans hit distinct bank groups
+  __shared__ __attribute__((aligned(16))) uint8_t tile[TP * 256];
+  __shared__ float red[4];
+  using V = Vec16<DT>;
+  const int64_t b = blockIdx.z;
+  const int64_t p0 = (int64_t)blockIdx.x * TP;
+  const int64_t c0 = (int64_t)blockIdx.y * 256;
+  const float sc = scale_from_amax(image_amax(parts, b, nparts, red));
+  const float rc = 1.0f / sc;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) sx[b] = sc;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cl = 64 * wave + 16 * (lane >> 4);             // the lane's first channel within the tile
+  const int pl = PPL * (lane & 15);                        // the lane's first pixel within the tile
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(reinterpret_cast<const char*>(x) + b * ch * hw * ESZ,
+                                             (uint32_t)(ch * hw * ESZ));
+  V v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t c = c0 + cl + i;
+    v[i].raw = buf_load_u4(r, c < ch ? (uint32_t)((c * hw + p0 + pl) * ESZ) : OOB);
+  }
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    float f[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) f[i] = v[i].get(j);
+    uint32_t w[4];
+    quant_pack<16>(f, sc, rc, w);
+    *reinterpret_cast<uint4*>(&tile[(pl + j) * 256 + (((cl >> 4) ^ (lane & 15)) << 4)]) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < TP / 16; ++j) {
+    const int k = threadIdx.x + 256 * j;                    // 16-byte chunk of the tile
+    const int pix = k >> 4, part = k & 15;
+    const int64_t p = p0 + pix, c = c0 + part * 16;
+    if (p < hw && c < c_pad)
+      *reinterpret_cast<uint4*>(q + (b * hw + p) * c_pad + c) =
+          *reinterpret_cast<const uint4*>(&tile[pix * 256 + ((part ^ ((pix / PPL) & 15)) << 4)]);
+  }
 }
 
 // Quantize + NCHW -> NHWC: tile of 64 channels x 64 pixels per block (256 threads). Wave w
@@ -522,6 +682,79 @@ __global__ __launch_bounds__(256) void conv_weight_pack_kernel(const void* __res
   for (int64_t i = threadIdx.x; i < 9 * ci_pad; i += 256) {
     const int64_t tap = i / ci_pad, c = i % ci_pad;
     out[i] = c < ci ? (int8_t)quant1(load_as_f32<DT>(w, base + c * 9 + tap), sc, rc) : (int8_t)0;
+  }
+}
+
+// NHWC q (int8 / uint8) -> NCHW float with 16-byte accesses on both sides: a block covers 256 channels x
+// TP = 16 * PPL pixels (PPL = output pixels per 16-byte store: 4 float32, 8 bf16 / fp16). The tile's NHWC
+// bytes come in as 16-byte loads into LDS [TP][256]; lane l of wave w then takes channels
+// 64 w + 16 (l / 16) .. + 15 of pixels PPL (l % 16) .. + PPL (PPL 16-byte LDS reads) and writes, per
+// channel, PPL contiguous outputs as one 16-byte store: y = (float)q * (scale[o] * sx[b]) (+ bias[o]).
+// Needs hw % PPL == 0.
+template <int DT, bool RELU>
+__global__ __launch_bounds__(256) void conv_dequant_vec_kernel(const void* __restrict__ qv, int64_t hw, int64_t co,
+                                                               const float* __restrict__ scale,
+                                                               const float* __restrict__ sx,
+                                                               const float* __restrict__ bias, void* __restrict__ y) {
+  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
+  constexpr int PPL = 16 / ESZ, TP = 16 * PPL;
+  __shared__ __attribute__((aligned(16))) uint8_t tile[TP * 256];   // swizzled as in conv_quant_nhwc_vec_kernel
+  const int64_t b = blockIdx.z;
+  const int64_t p0 = (int64_t)blockIdx.x * TP;
+  const int64_t c0 = (int64_t)blockIdx.y * 256;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(reinterpret_cast<const uint8_t*>(qv) + b * hw * co, (uint32_t)(hw * co));
+  const bool co16 = co % 16 == 0;
+#pragma unroll
+  for (int j = 0; j < TP / 16; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    const int pix = k >> 4, part = k & 15;
+    const int64_t p = p0 + pix, c = c0 + part * 16;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (co16) {
+      v = buf_load_u4(r, (p < hw && c < co) ? (uint32_t)(p * co + c) : OOB);
+    } else if (p < hw) {        // rows not 16-byte aligned: bytes
+      uint8_t by[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) by[e] = c + e < co ? reinterpret_cast<const uint8_t*>(qv)[(b * hw + p) * co + c + e] : 0;
+      v = *reinterpret_cast<const uint4*>(by);
+    }
+    *reinterpret_cast<uint4*>(&tile[pix * 256 + ((part ^ ((pix / PPL) & 15)) << 4)]) = v;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cl = 64 * wave + 16 * (lane >> 4);
+  const int pl = PPL * (lane & 15);
+  const float sxb = sx[b];
+  uint4 bytes[PPL];
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) bytes[j] = *reinterpret_cast<const uint4*>(&tile[(pl + j) * 256 + (((cl >> 4) ^ (lane & 15)) << 4)]);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t o = c0 + cl + i;
+    if (o >= co) break;
+    const float f = scale[o] * sxb;
+    const float bo = bias ? bias[o] : 0.0f;
+    float v[PPL];
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+      const uint8_t raw = reinterpret_cast<const uint8_t*>(&bytes[j])[i];
+      const float qf = RELU ? (float)raw : (float)(int8_t)raw;
+      float t = qf * f;
+      if (bias) t = t + bo;
+      v[j] = t;
+    }
+    const int64_t p = p0 + pl;
+    if (p >= hw) continue;
+    char* out = reinterpret_cast<char*>(y) + ((b * co + o) * hw + p) * ESZ;
+    if constexpr (DT == XDNA_F32) {
+      *reinterpret_cast<f32x4*>(out) = f32x4{v[0], v[1], v[2], v[3]};
+    } else {
+      uint32_t h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        h[e] = DT == XDNA_BF16 ? f32x2_to_bf16x2_bits(v[2 * e], v[2 * e + 1]) : f32x2_to_f16x2_bits(v[2 * e], v[2 * e + 1]);
+      *reinterpret_cast<uint4*>(out) = make_uint4(h[0], h[1], h[2], h[3]);
+    }
   }
 }
 
@@ -847,19 +1080,20 @@ int xdna_conv_quant_nhwc(const void* x, int x_dtype, int64_t nb, int64_t ch, int
   dim3 g1((unsigned)parts, (unsigned)nb, 1);
   dim3 g2((unsigned)cdiv(hw, 64), (unsigned)cdiv(c_pad, 64), (unsigned)nb);
   XDNA_REQUIRE(cdiv(hw, 64) < (1ll << 31) && cdiv(c_pad, 64) < 65536, "image too large");
+  const int esz = x_dtype == XDNA_F32 ? 4 : 2;
+  // the 16-byte path: pixel rows in whole 16-byte loads, an image's bytes addressable by one buffer resource
+  const bool vec = hw % (16 / esz) == 0 && aligned(x, 16) && per * esz < (int64_t(1) << 31);
+  const dim3 gv((unsigned)cdiv(hw, 16 * (16 / esz)), (unsigned)cdiv(c_pad, 256), (unsigned)nb);
+#define XDNA_CQ(DT)                                                                                        \
+  image_absmax_kernel<DT><<<g1, 256, 0, st>>>(x, per, amax_ws);                                             \
+  if (vec) conv_quant_nhwc_vec_kernel<DT><<<gv, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);     \
+  else conv_quant_nhwc_kernel<DT><<<g2, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);
   switch (x_dtype) {
-    case XDNA_F32:
-      image_absmax_kernel<XDNA_F32><<<g1, 256, 0, st>>>(x, per, amax_ws);
-      conv_quant_nhwc_kernel<XDNA_F32><<<g2, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);
-      break;
-    case XDNA_BF16:
-      image_absmax_kernel<XDNA_BF16><<<g1, 256, 0, st>>>(x, per, amax_ws);
-      conv_quant_nhwc_kernel<XDNA_BF16><<<g2, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);
-      break;
-    default:
-      image_absmax_kernel<XDNA_F16><<<g1, 256, 0, st>>>(x, per, amax_ws);
-      conv_quant_nhwc_kernel<XDNA_F16><<<g2, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);
+    case XDNA_F32: XDNA_CQ(XDNA_F32) break;
+    case XDNA_BF16: XDNA_CQ(XDNA_BF16) break;
+    default: XDNA_CQ(XDNA_F16)
   }
+#undef XDNA_CQ
   return launch_status("conv_quant_nhwc");
 }
 
@@ -887,8 +1121,14 @@ int xdna_conv_dequant(const void* q, int relu, int64_t nb, int64_t h, int64_t w,
   XDNA_REQUIRE(cdiv(co, 64) < 65536, "too many channels");
   dim3 g((unsigned)cdiv(hw, 64), (unsigned)cdiv(co, 64), (unsigned)nb);
   hipStream_t st = as_stream(stream);
+  const int esz = y_dtype == XDNA_F32 ? 4 : 2;
+  // the 16-byte path: output rows in whole 16-byte stores, an image's int8 addressable by one resource
+  const bool vec = hw % (16 / esz) == 0 && aligned(y, 16) && hw * co < (int64_t(1) << 31);
+  const dim3 gv((unsigned)cdiv(hw, 16 * (16 / esz)), (unsigned)cdiv(co, 256), (unsigned)nb);
 #define XDNA_DQ(DT)                                                                                   \
-  if (relu) conv_dequant_kernel<DT, true><<<g, 256, 0, st>>>(q, hw, co, scale, sx, bias, y);       \
+  if (vec && relu) conv_dequant_vec_kernel<DT, true><<<gv, 256, 0, st>>>(q, hw, co, scale, sx, bias, y); \
+  else if (vec) conv_dequant_vec_kernel<DT, false><<<gv, 256, 0, st>>>(q, hw, co, scale, sx, bias, y);   \
+  else if (relu) conv_dequant_kernel<DT, true><<<g, 256, 0, st>>>(q, hw, co, scale, sx, bias, y);       \
   else conv_dequant_kernel<DT, false><<<g, 256, 0, st>>>(q, hw, co, scale, sx, bias, y);
   switch (y_dtype) {
     case XDNA_F32: XDNA_DQ(XDNA_F32) break;
