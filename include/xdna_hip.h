@@ -174,6 +174,18 @@ int xdna_pad_rows_i8(const int8_t* src, int64_t rows, int64_t cols, int64_t ld_s
 int xdna_conv_quant_nhwc(const void* x, int x_dtype, int64_t nb, int64_t ch, int64_t h, int64_t w,
                          int8_t* q, int64_t c_pad, float* sx, float* amax_ws, void* stream);
 
+/* xdna_conv_quant_nhwc without the caller workspace, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference. The per-image block maxima go to a file-scope device array of the library
+ * (XDNA_NOALLOC_MAX_IMAGES x XDNA_AMAX_WS_PER_IMAGE floats, 1 MB, held on each device until the process
+ * ends; its address is looked up once per device on the first call). nb above XDNA_NOALLOC_MAX_IMAGES is
+ * rejected (XDNA_EINVAL). Every call on a device shares that array: calls that overlap on one device
+ * (other streams, other threads) race and must be serialized by the caller. Nothing is allocated: no
+ * hipMalloc / hipFree. Same results as xdna_conv_quant_nhwc. */
+#define XDNA_NOALLOC_MAX_IMAGES 1024
+int xdna_conv_quant_nhwc_noalloc(const void* x, int x_dtype, int64_t nb, int64_t ch, int64_t h, int64_t w, int8_t* q,
+                                 int64_t c_pad, float* sx, void* stream);
+
 /* Conv weight quantize-once (torch_xdna/conv.py:58-60, `ConvLayer.__init__`):
  *   sw[o] = max(amax |w[o]|, 1e-8f) / 127 over (Ci, 3, 3); wq = clamp(round(w / sw), +-127),
  * written in the kernel's layout wq[o][ky*3+kx][c] with ci_pad channels (zeros past ci).

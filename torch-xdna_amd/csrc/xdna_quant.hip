@@ -1006,6 +1006,39 @@ __global__ __launch_bounds__(256) void nhwc_to_nchw_i8_kernel(const int8_t* __re
 
 inline bool float_dtype(int dt) { return dt == XDNA_F32 || dt == XDNA_BF16 || dt == XDNA_F16; }
 
+// ------------------------------------------------------------------------------ no-allocation scratch
+// The per-image block maxima of xdna_conv_quant_nhwc_noalloc live in this file-scope device array instead
+// of a caller workspace: XDNA_NOALLOC_MAX_IMAGES images x XDNA_AMAX_WS_PER_IMAGE floats (1 MB), held on
+// every device the library runs on until the process ends. Host code never passes the array's name (a
+// host-side stand-in): it passes the device address hipGetSymbolAddress returns, looked up once per
+// device with that device current. The kernels write every slot they read, so nothing is cleared.
+static __device__ __align__(256) float scratch[XDNA_NOALLOC_MAX_IMAGES * XDNA_AMAX_WS_PER_IMAGE];
+
+namespace {
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[64] = {nullptr};
+}  // namespace
+
+// The current device's address of `scratch`, or nullptr with the error set.
+float* scratch_ptr() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("no-alloc scratch: no current device (or a device index above 63)");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || ptr == nullptr) {
+      set_error(std::string("no-alloc scratch: hipGetSymbolAddress failed: ") + hipGetErrorString(rc));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace xdna
 
 using namespace xdna;
@@ -1095,6 +1128,16 @@ int xdna_conv_quant_nhwc(const void* x, int x_dtype, int64_t nb, int64_t ch, int
   }
 #undef XDNA_CQ
   return launch_status("conv_quant_nhwc");
+}
+
+int xdna_conv_quant_nhwc_noalloc(const void* x, int x_dtype, int64_t nb, int64_t ch, int64_t h, int64_t w, int8_t* q,
+                                 int64_t c_pad, float* sx, void* stream) {
+  XDNA_REQUIRE(nb >= 0 && nb <= XDNA_NOALLOC_MAX_IMAGES,
+               "xdna_conv_quant_nhwc_noalloc takes at most XDNA_NOALLOC_MAX_IMAGES (1024) images per call");
+  if (nb == 0) return XDNA_OK;
+  float* ws = scratch_ptr();
+  if (ws == nullptr) return XDNA_ENODEV;
+  return xdna_conv_quant_nhwc(x, x_dtype, nb, ch, h, w, q, c_pad, sx, ws, stream);
 }
 
 int xdna_conv_weight_pack(const void* w, int w_dtype, int64_t co, int64_t ci, int8_t* wq, int64_t ci_pad, float* sw,

@@ -98,6 +98,7 @@ def _declare(L):
         "xdna_gemm_bf16": ([p, i64, p, i64, p, p, i, i64, i64, i64, i64, p], i),
         "xdna_pad_rows_i8": ([p, i64, i64, i64, p, i64, i64, p], i),
         "xdna_conv_quant_nhwc": ([p, i, i64, i64, i64, i64, p, i64, p, p, p], i),
+        "xdna_conv_quant_nhwc_noalloc": ([p, i, i64, i64, i64, i64, p, i64, p, p], i),
         "xdna_conv_weight_pack": ([p, i, i64, i64, p, i64, p, p], i),
         "xdna_conv3x3_i8": ([p, i64, i64, i64, i64, p, i64, i, i, p, p, p], i),
         "xdna_conv_dequant": ([p, i, i64, i64, i64, i64, p, p, p, p, i, p], i),
@@ -120,7 +121,8 @@ def _declare(L):
 
 
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
-           "xdna_gemm_i8_dequant", "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc", "xdna_conv_weight_pack",
+           "xdna_gemm_i8_dequant", "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc",
+           "xdna_conv_quant_nhwc_noalloc", "xdna_conv_weight_pack",
            "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8", "xdna_nhwc_to_nchw_i8",
            "xdna_tile_set", "xdna_tile_get", "xdna_tile_plan", "xdna_tile_clear", "xdna_rmsnorm_bf16", "xdna_qk_norm_rope",
            "xdna_attention_bf16", "xdna_silu_mul_bf16", "xdna_add_f32")
