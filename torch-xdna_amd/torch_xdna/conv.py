@@ -191,9 +191,7 @@ def _first_call(cfg, layer, run_gpu, run_cpu, on_gpu):
 
 
 def _account(device, t0, n, layer):
-    stats.calls[device] += 1
-    stats.seconds[device] += time.perf_counter() - t0
-    stats.macs[device] += n * layer.co * layer.ci * layer.h * layer.w * 9
+    stats.record(device, t0, n * layer.co * layer.ci * layer.h * layer.w * 9)
 
 
 def conv3x3(cfg, xq, weight, relu):

@@ -17,11 +17,12 @@ compared bit for bit with the CPU route; a mismatch raises GPUResultMismatch, wh
 to the CPU (`_gpu_failed`, runtime.py:275-282); three failing shapes retire the GPU.
 """
 
+import bisect
 import logging
 import threading
 import time
 import weakref
-from collections import defaultdict
+from collections import Counter, defaultdict
 
 import torch
 
@@ -33,28 +34,40 @@ _lock = threading.RLock()
 
 # ------------------------------------------------------------------------------ stats
 class Stats:
+    """Where the offloaded work went, for report(): per device ("gpu" / "cpu") the op calls, the wall
+    seconds inside the ops and the multiply-accumulates; GPU kernel launches; the shapes that fell back
+    to the CPU and why; whole-stack dispatches and their first-call checks. reset() clears it (the
+    autotune decisions below are kept)."""
+
     def __init__(self):
         self.reset()
 
     def reset(self):
-        self.calls = defaultdict(int)       # device -> op calls (GEMMs and convs)
-        self.seconds = defaultdict(float)   # device -> wall seconds inside the op
-        self.macs = defaultdict(int)        # device -> multiply-accumulates
-        self.launches = 0                   # GPU GEMM / conv launches
-        self.fallbacks = []                 # (shape, error) when the GPU failed
-        self.stacks = defaultdict(int)
-        self.checks = []
+        self.calls, self.seconds, self.macs = Counter(), defaultdict(float), Counter()
+        self.launches = 0
+        self.fallbacks = []             # (shape or layer, error text)
+        self.stacks = Counter()         # (stack name, "gpu" fused / "cpu" plain graph) -> graph calls
+        self.checks = []                # (stack, relative error) of first fused calls
+
+    def record(self, device, since, macs):
+        """One op call on `device` that started at perf_counter() value `since`."""
+        self.calls[device] += 1
+        self.seconds[device] += time.perf_counter() - since
+        self.macs[device] += macs
 
     def as_dict(self):
-        ok = kernels.available()
-        reason = kernels.unavailable_reason()
-        return dict(calls=dict(self.calls), seconds={k: round(v, 4) for k, v in self.seconds.items()},
-                    gmacs={k: round(v / 1e9, 3) for k, v in self.macs.items()},
-                    gpu_launches=self.launches, npu_launches=self.launches, fallbacks=list(self.fallbacks),
-                    stacks={f"{k[0]} on {k[1]}": v for k, v in self.stacks.items()}, checks=list(self.checks),
-                    decisions={"x".join(map(str, k)): v for k, v in decisions.items()},
-                    gpu_available=ok, gpu_unavailable_reason=reason,
-                    npu_available=ok, npu_unavailable_reason=reason)
+        ok, why = kernels.available(), kernels.unavailable_reason()
+        d = {"calls": dict(self.calls),
+             "seconds": {dev: round(t, 4) for dev, t in self.seconds.items()},
+             "gmacs": {dev: round(m / 1e9, 3) for dev, m in self.macs.items()},
+             "gpu_launches": self.launches, "fallbacks": list(self.fallbacks),
+             "stacks": {f"{name} on {dev}": n for (name, dev), n in self.stacks.items()},
+             "checks": list(self.checks),
+             "decisions": {"x".join(str(p) for p in key): v for key, v in decisions.items()},
+             "gpu_available": ok, "gpu_unavailable_reason": why}
+        # the reference's names for the same figures
+        d.update(npu_launches=d["gpu_launches"], npu_available=ok, npu_unavailable_reason=why)
+        return d
 
 
 # Autotune results outlive stats.reset(): key -> (device, gpu_ms, cpu_ms)
@@ -138,28 +151,50 @@ class QWeight:
         return ws[0] if len(ws) == 1 else torch.cat(ws)
 
 
-_weights = {}  # key -> (weakrefs to the source tensors, QWeight)
+class _WeightCache:
+    """QWeights by their source weights' identity: (data_ptr, shape, _version) of every weight and the
+    transposed flag (runtime.py:99-110), so an in-place update (a new _version) quantizes again. An
+    entry also checks that its weights are the very tensors it was made from (a freed tensor's memory
+    can be reused by another) and is dropped when one of them is garbage-collected."""
+
+    def __init__(self):
+        self.entries = {}
+
+    def clear(self):
+        self.entries.clear()
+
+    def __len__(self):
+        return len(self.entries)
+
+    def get(self, ws, transposed):
+        key = (tuple((w.data_ptr(), tuple(w.shape), w._version) for w in ws), transposed)
+        hit = self.entries.get(key)
+        if hit is not None and all(alive() is w for alive, w in zip(hit[0], ws)):
+            return hit[1]
+        qw = QWeight(ws, transposed)
+
+        def drop(_, key=key, qw=qw):    # only this entry: the key may have been reused since
+            if self.entries.get(key, (None, None))[1] is qw:
+                del self.entries[key]
+
+        alive = []
+        for w in ws:
+            try:
+                alive.append(weakref.ref(w, drop))
+            except TypeError:           # not weak-referenceable: kept alive by the entry
+                alive.append(lambda w=w: w)
+        self.entries[key] = (alive, qw)
+        return qw
 
 
-def _ref(t):
-    try:
-        return weakref.ref(t)
-    except TypeError:
-        return lambda: t
+_weights = _WeightCache()
 
 
 def qweight(ws, transposed: bool = False) -> QWeight:
-    """The cached QWeight of one weight or of several concatenated on N (runtime.py:99-110): keyed by
-    (data_ptr, shape, _version) per weight, so an in-place update re-quantizes."""
+    """The cached QWeight of one weight, or of several concatenated on N (the fused linears)."""
     ws = list(ws) if isinstance(ws, (list, tuple)) else [ws]
-    key = (tuple((w.data_ptr(), tuple(w.shape), w._version) for w in ws), transposed)
     with _lock:
-        hit = _weights.get(key)
-        if hit is not None and all(r() is w for r, w in zip(hit[0], ws)):
-            return hit[1]
-        qw = QWeight(ws, transposed)
-        _weights[key] = ([_ref(w) for w in ws], qw)
-        return qw
+        return _weights.get(ws, transposed)
 
 
 # ------------------------------------------------------------------------------ the CPU route
@@ -171,10 +206,10 @@ def _quant_rows(x2d):
 
 
 def _bucket(rows, buckets):
-    for b in buckets:
-        if b >= rows:
-            return b
-    return buckets[-1]
+    """The smallest row bucket that holds `rows` (the largest when none does): the row group of the
+    reference's autotune and verify keys."""
+    i = bisect.bisect_left(buckets, rows)
+    return buckets[min(i, len(buckets) - 1)]
 
 
 def _cpu_acc(xq, qw):
@@ -367,13 +402,8 @@ def _gpu_failed(cfg, R, qw, e):
         log.warning("torch_xdna: %d GPU failures, GPU retired for this process", len(_failed))
 
 
-def _account(device, t0, rows, qw):
-    stats.calls[device] += 1
-    stats.seconds[device] += time.perf_counter() - t0
-    stats.macs[device] += rows * qw.N * qw.K
-
-
-def _fp_only(cfg):
+def _float_only(cfg):
+    """cpu_kernel "fp" with no GPU route: the op is the float linear itself."""
     return cfg.cpu_kernel == "fp" and (cfg.policy == "cpu" or not kernels.available())
 
 
@@ -399,7 +429,7 @@ def _linear_impl(cfg, x, qw, bias, w_fp_fn):
                     device = "cpu"
             if y is None:
                 y = _cpu_bf16(x2d, w_fp_fn(), bias, x.dtype)
-        _account(device, t0, R, qw)
+        stats.record(device, t0, R * qw.N * qw.K)
         return y.to(x.device).reshape(*shape, qw.N)
     with _lock:
         device = _choose(cfg, R, qw, on_gpu, lambda: _gpu_linear(cfg, x2d, qw, bias, x.dtype),
@@ -417,7 +447,7 @@ def _linear_impl(cfg, x, qw, bias, w_fp_fn):
                                                None if bias is None else bias.cpu())
             else:
                 y = _cpu_linear(x2d, qw, bias, x.dtype)
-    _account(device, t0, R, qw)
+    stats.record(device, t0, R * qw.N * qw.K)
     return y.to(x.device).reshape(*shape, qw.N)
 
 
@@ -427,7 +457,7 @@ def linear(cfg, x, weight, bias, transposed):
     if x.numel() == 0 or x.reshape(-1, x.shape[-1]).shape[0] == 0:
         return x.new_zeros(*x.shape[:-1], N)
     w_fp = weight.t() if transposed else weight
-    if _fp_only(cfg):
+    if _float_only(cfg):
         return torch.nn.functional.linear(x, w_fp.to(x.dtype), bias)
     qw = qweight(weight, transposed)
     return _linear_impl(cfg, x, qw, bias, lambda: w_fp)
@@ -442,7 +472,7 @@ def linear_cat(cfg, x, weights, biases):
         bias = torch.cat([b if b is not None else w.new_zeros(w.shape[0]) for w, b in zip(weights, biases)])
     else:
         bias = None
-    if _fp_only(cfg):
+    if _float_only(cfg):
         return torch.nn.functional.linear(x, torch.cat(list(weights)).to(x.dtype), bias)
     qw = qweight(list(weights))
     return _linear_impl(cfg, x, qw, bias, lambda: torch.cat(list(weights)))
@@ -473,25 +503,26 @@ def linear_int8(x, weights, biases, transposed: bool, cfg_id: int):
 
 
 def linear_i8(cfg, xq, weights, transposed):
-    """(int32 acc [R, N], weight scales [N]) of xdna::linear_i8 (runtime.py:377-399)."""
+    """(int32 acc [R, N], weight scales [N]) of xdna::linear_i8 (runtime.py:377-399): the integer GEMM of
+    an already quantized activation, on the device _choose picks; a GPU failure moves the shape to the
+    CPU. The scales are a fresh tensor: Inductor may reuse an extern op's output buffer once it is dead."""
     t0 = time.perf_counter()
-    qw = qweight(weights[0] if len(weights) == 1 else list(weights), transposed)
+    qw = qweight(list(weights), transposed)
     dev = xq.device
-    if xq.shape[0] == 0:
+    R = xq.shape[0]
+    if R == 0:
         return xq.new_zeros((0, qw.N), dtype=torch.int32), qw.sw(dev).to(dev).clone()
-    on_gpu = dev.type == "cuda"
     with _lock:
-        device = _choose(cfg, xq.shape[0], qw, on_gpu, lambda: _gpu_acc(cfg, xq, qw), lambda: _cpu_acc(xq, qw))
+        device = _choose(cfg, R, qw, dev.type == "cuda", lambda: _gpu_acc(cfg, xq, qw), lambda: _cpu_acc(xq, qw))
         acc = None
         if device == "gpu":
             try:
                 acc = _gpu_acc(cfg, xq, qw)
-            except Exception as e:  # launch failure or mismatch: this shape moves to the CPU
-                _gpu_failed(cfg, xq.shape[0], qw, e)
+            except Exception as e:      # launch failure or mismatch
+                _gpu_failed(cfg, R, qw, e)
                 device = "cpu"
         if acc is None:
             acc = _cpu_acc(xq, qw)
-    _account(device, t0, xq.shape[0], qw)
-    # a fresh tensor: Inductor may reuse an extern op's output buffer once it is dead
+    stats.record(device, t0, R * qw.N * qw.K)
     sw = qw.gpu(kernels.gpu_device(xq))[1] if device == "gpu" else qw.cpu()[1]
     return acc.to(dev), sw.to(dev).clone()

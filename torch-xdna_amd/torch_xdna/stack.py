@@ -1,39 +1,40 @@
 """xdna::qwen3_stack: a Qwen3-0.6B-width transformer stack and its linear head as one op on the GPU.
 
-Mirrors the reference's whole-stack op (torch_xdna/stack.py in the reference). The backend looks in
-Dynamo's graph for a transformers `Qwen3Model` whose last hidden states feed only a linear layer,
-with Qwen3-0.6B's widths (hidden 1024, 16 query / 8 key-value heads of 128, MLP 3072), any depth,
-and bidirectional attention under a 4-D mask that is an input of the graph (stack.py:111-241). Such
-a graph is compiled twice (stack.py:463-473):
+The reference fuses one kind of subgraph into a single device op (torch_xdna/stack.py in the
+reference): a transformers `Qwen3Model` of Qwen3-0.6B's widths (hidden 1024, 16 query and 8 key-value
+heads of 128, MLP 3072), any depth, with bidirectional attention under a 4-D mask that is an input of
+the graph, whose last hidden states feed only a linear layer (OmniVoice's backbone and audio heads).
+The same subgraphs are taken here (the rules of stack.py:111-241): every linear of the stack is a
+q/k/v/o or gate/up/down projection of a layer, without bias; every other parameter is a layer's
+input / post-attention / q / k RMSNorm weight, the final norm's or the RoPE frequencies; RMSNorm eps
+1e-6 and RoPE without attention scaling; one scaled_dot_product_attention per layer, all under the
+same mask placeholder, no dropout, not causal, scale 1/sqrt(128); the hidden states the one other
+tensor input; the head a linear of a parameter [N, 1024] (optional bias) that alone consumes the
+stack's output.
 
-  fused  the stack and its head replaced by xdna::qwen3_stack
-  plain  the graph as the backend compiles any other
+The graph is then compiled twice, once with the stack and head replaced by xdna::qwen3_stack and
+once as any other graph, and a dispatcher picks per call (stack.py:412-446): the fused graph when
+every sequence's mask is a prefix block of 1 .. MAX_TOKENS positions followed by padding positions
+that see themselves or nothing, the plain graph otherwise. The fused output's padding rows are zeros.
+The first fused call of each attention shape is checked against the original graph run eagerly
+(stack.py:448-460): its valid rows within 10% (relative norm) of the head's output, else, as after a
+launch failure, the stack keeps to the plain graph for the rest of the process.
 
-and a dispatcher picks one per call from the mask (stack.py:412-446): the fused graph when every
-sequence's mask is a prefix block of 1 .. MAX_TOKENS positions followed only by padding positions
-that see themselves or nothing (stack.py:328-352), the plain graph otherwise (a causal mask, for
-one). The fused graph's rows for padding positions are zeros.
-
-On the GPU the op packs the valid tokens of all sequences into one [T, 1024] float32 residual
-stream and runs every layer with the HIP kernels: RMSNorm to bf16, the q/k/v, o, gate/up and down
-projections on the tile engine's bf16 GEMM (float32 sums), q / k RMSNorm + RoPE, bidirectional
-grouped-query attention (bf16 MFMA, online softmax in float32), SiLU * up, the residual adds; then
-the final norm and the head (bias fused). The reference runs bfp16 operands on the NPU, one launch
-per pair of sequences.
-
-The first fused call of each attention shape (query blocks per sequence) is checked against the
-original graph run eagerly (stack.py:448-460): the valid rows of the head's output must be within
-10% (relative norm). A mismatch or a launch failure sends the stack to the plain graph for the rest
-of the process.
+On the GPU the op packs the valid tokens of all sequences into one [T, 1024] float32 residual stream
+and runs every layer with the HIP kernels: RMSNorm to bf16, the q|k|v, o, gate|up and down projections
+on the tile engine's bf16 GEMM (float32 sums), q / k RMSNorm + RoPE, bidirectional grouped-query
+attention (bf16 MFMA, online softmax in float32), SiLU * up and the residual adds; then the final norm
+and the head (bias fused). Each call shape is captured as a HIP graph on its second call.
 """
 
 import copy
 import logging
 import operator
-import re
 import threading
 import time
 import weakref
+from dataclasses import dataclass, field
+from typing import Any, Optional
 
 import torch
 import torch.nn.functional as F
@@ -44,225 +45,249 @@ from .runtime import GPUResultMismatch, stats
 log = logging.getLogger("torch_xdna")
 _lock = threading.RLock()
 
-LINEAR = {torch._C._nn.linear, F.linear}
-SDPA = {torch._C._nn.scaled_dot_product_attention, F.scaled_dot_product_attention}
-ADD = {operator.add, torch.add}
-MUL = {operator.mul, torch.mul}
-ROOTS = ("Qwen3Model",)
+# Qwen3-0.6B's widths: hidden, query heads, key-value heads, head dim, MLP width; RMSNorm eps
 D, NH, NKV, DH, INTER, EPS = 1024, 16, 8, 128, 3072, 1e-6
-LAYER_KEYS = ("q", "k", "v", "o", "gate", "up", "down", "input_norm", "post_norm", "q_norm", "k_norm")
-SHAPES = dict(q=(NH * DH, D), k=(NKV * DH, D), v=(NKV * DH, D), o=(D, NH * DH), gate=(INTER, D), up=(INTER, D),
-              down=(D, INTER), input_norm=(D,), post_norm=(D,), q_norm=(DH,), k_norm=(DH,))
-VERIFY_TOL = 0.1
+# a layer's weights in the order Plan.tensors() lists them, and their shapes
+LAYER_SHAPES = {"q": (NH * DH, D), "k": (NKV * DH, D), "v": (NKV * DH, D), "o": (D, NH * DH),
+                "gate": (INTER, D), "up": (INTER, D), "down": (D, INTER),
+                "input_norm": (D,), "post_norm": (D,), "q_norm": (DH,), "k_norm": (DH,)}
+LAYER_KEYS = tuple(LAYER_SHAPES)
+VERIFY_TOL = 0.1               # relative norm error of the first fused call against the original graph
 # Longest sequence the fused op takes. The reference's NPU program stops at 384 positions; the GPU
 # attention streams the keys, so the cap only bounds the work of one call.
 MAX_TOKENS = 4096
 QBLOCK = 32                    # queries per attention wave
 
-_PROJ = re.compile(r"layers\.(\d+)\.(?:self_attn\.(q|k|v|o)_proj|mlp\.(gate|up|down)_proj)")
-_NORMS = {"input_layernorm": "input_norm", "post_attention_layernorm": "post_norm",
-          "self_attn.q_norm": "q_norm", "self_attn.k_norm": "k_norm"}
-_NORM = re.compile(r"layers\.(\d+)\.(" + "|".join(re.escape(k) for k in _NORMS) + ")")
+_ROOT_CLASS = "Qwen3Model"
+_LINEAR = frozenset({torch._C._nn.linear, F.linear})
+_SDPA = frozenset({torch._C._nn.scaled_dot_product_attention, F.scaled_dot_product_attention})
+_ADD = frozenset({operator.add, torch.add})
+_MUL = frozenset({operator.mul, torch.mul})
+
+# Module paths below the Qwen3Model, split on ".": a layer's sub-path -> the role of the weight its
+# linear uses, or of the parameter its norm uses; the stack-level paths of the final norm and RoPE.
+_LINEAR_ROLE = {("self_attn", "q_proj"): "q", ("self_attn", "k_proj"): "k", ("self_attn", "v_proj"): "v",
+                ("self_attn", "o_proj"): "o", ("mlp", "gate_proj"): "gate", ("mlp", "up_proj"): "up",
+                ("mlp", "down_proj"): "down"}
+_PARAM_ROLE = {("input_layernorm",): "input_norm", ("post_attention_layernorm",): "post_norm",
+               ("self_attn", "q_norm"): "q_norm", ("self_attn", "k_norm"): "k_norm"}
+_STACK_ROLE = {("norm",): "norm", ("rotary_emb",): "inv_freq"}
 
 
-# ------------------------------------------------------------------ finding a stack
-class _NoStack(Exception):
-    pass
+def _layer_path(rel):
+    """(layer index, the rest of the path) for `layers.<i>.<...>`, else (None, the whole path)."""
+    parts = tuple(rel.split(".")) if rel else ()
+    if len(parts) >= 2 and parts[0] == "layers" and parts[1].isdigit():
+        return int(parts[1]), parts[2:]
+    return None, parts
 
 
-class Plan:
-    """A stack found in a graph. Nodes are kept by name, so the plan applies to copies."""
-
-    def __init__(self, region, x, mask, mask_index, head, weights, bias, layers, out_features, max_tokens):
-        self.region, self.x, self.mask, self.mask_index, self.head = region, x, mask, mask_index, head
-        self.weights, self.bias = weights, bias       # role -> tensor; the head's bias or None
-        self.layers, self.out_features, self.max_tokens = layers, out_features, max_tokens
-
-    def tensors(self):
-        """Every weight, in a fixed order: per layer LAYER_KEYS, then norm, head, inv_freq."""
-        return [self.weights[(i, k)] for i in range(self.layers) for k in LAYER_KEYS] + \
-            [self.weights["norm"], self.weights["head"], self.weights["inv_freq"]]
-
-
-def _cls_name(c):
+def _class_name(c):
     return c.__name__ if isinstance(c, type) else str(c).rsplit(".", 1)[-1].strip("'>")
-
-
-def _module_of(node):
-    """(path, class name) of the innermost module a node ran in."""
-    path, cls = list(node.meta["nn_module_stack"].values())[-1]
-    return path, _cls_name(cls)
-
-
-def _linear_operands(node):
-    names = ("input", "weight", "bias")
-    got = dict(zip(names, node.args), **{k: v for k, v in node.kwargs.items() if k in names})
-    return got.get("input"), got.get("weight"), got.get("bias")
-
-
-class _Params:
-    """Role -> weight tensor of one stack: (layer, LAYER_KEYS name), "norm", "inv_freq", "head"."""
-
-    def __init__(self, value):
-        self.value, self.by_role = value, {}
-
-    def is_param(self, node):
-        return node.op == "placeholder" and (isinstance(self.value.get(node), torch.nn.Parameter)
-                                             or "_parameters_" in node.name or "_buffers_" in node.name)
-
-    def add(self, role, node):
-        t = self.value.get(node)
-        if not isinstance(t, torch.Tensor):
-            raise _NoStack(f"{role}: no tensor")
-        if self.by_role.setdefault(role, t) is not t:
-            raise _NoStack(f"two tensors for {role}")
-
-    def layer_count(self):
-        idx = [r[0] for r in self.by_role if isinstance(r, tuple)]
-        return max(idx) + 1 if idx else 0
-
-    def check_shapes(self, layers):
-        for i in range(layers):
-            for key, shape in SHAPES.items():
-                t = self.by_role.get((i, key))
-                if t is None or tuple(t.shape) != shape:
-                    raise _NoStack(f"layer {i} {key}: {None if t is None else tuple(t.shape)}, need {shape}")
-        if tuple(getattr(self.by_role.get("norm"), "shape", ())) != (D,) or \
-                tuple(getattr(self.by_role.get("inv_freq"), "shape", ())) != (DH // 2,):
-            raise _NoStack("final norm / RoPE frequencies")
-
-
-def _param_role(rel):
-    """The role of a parameter used by a node of module path `rel` (relative to the Qwen3Model)."""
-    m = _NORM.fullmatch(rel)
-    if m:
-        return int(m[1]), _NORMS[m[2]]
-    return {"norm": "norm", "rotary_emb": "inv_freq"}.get(rel)
-
-
-def _check_constants(node, cls, rel):
-    """The op has RMSNorm's eps and RoPE without attention scaling built in."""
-    consts = [a for a in node.args if isinstance(a, float)]
-    if node.op != "call_function" or not consts:
-        return
-    if node.target in ADD and cls.endswith("RMSNorm") and any(abs(c - EPS) > 1e-12 for c in consts):
-        raise _NoStack(f"RMSNorm eps {consts} (the op has {EPS})")
-    if node.target in MUL and rel == "rotary_emb" and any(c != 1.0 for c in consts):
-        raise _NoStack(f"RoPE attention scaling {consts}")
-
-
-def _attention_mask(attn_nodes, layers, value):
-    """The one 4-D mask input every attention uses, bidirectionally at head_dim ** -0.5."""
-    masks = set()
-    for n in attn_nodes:
-        kw = dict(zip(("query", "key", "value", "attn_mask", "dropout_p", "is_causal", "scale"), n.args), **n.kwargs)
-        scale = kw.get("scale")
-        if kw.get("dropout_p", 0.0) != 0.0 or kw.get("is_causal", False) or \
-                (scale is not None and abs(scale - DH ** -0.5) > 1e-6):
-            raise _NoStack("attention: dropout, causal or another scale")
-        masks.add(kw.get("attn_mask"))
-    if len(attn_nodes) != layers or len(masks) != 1:
-        raise _NoStack(f"{len(attn_nodes)} attentions for {layers} layers, {len(masks)} masks")
-    mask = next(iter(masks))
-    mv = value.get(mask)
-    if not (isinstance(mask, torch.fx.Node) and mask.op == "placeholder" and isinstance(mv, torch.Tensor)
-            and mv.dim() == 4 and (mv.dtype == torch.bool or mv.is_floating_point())):
-        raise _NoStack("the attention mask is not a 4-D input of the graph")
-    return mask
-
-
-def _hidden_input(nodes, inside, mask, params, value):
-    """The region's one tensor input besides the mask and the weights: GPU hidden states [B, L, 1024]."""
-    ext = {a: None for n in nodes for a in n.all_input_nodes
-           if a not in inside and a is not mask and not params.is_param(a)}
-    tensors = [a for a in ext if not (a.op == "placeholder" and isinstance(value.get(a), (int, torch.SymInt)))]
-    if len(tensors) != 1:
-        raise _NoStack(f"inputs {[a.name for a in tensors]}")
-    xv = tensors[0].meta.get("example_value")
-    if not (isinstance(xv, torch.Tensor) and xv.dim() == 3 and xv.shape[-1] == D and xv.is_floating_point()):
-        raise _NoStack("hidden states are not [B, L, 1024]")
-    if not _on_gpu(xv):
-        raise _NoStack("hidden states are not on the GPU")
-    return tensors[0]
 
 
 def _on_gpu(t):
     return t.device.type == "cuda"
 
 
-def _head_of(nodes, inside, params):
-    """The linear [N, 1024] of a parameter that alone consumes the region's one output."""
-    outs = [n for n in nodes if any(u not in inside for u in n.users)]
-    if len(outs) != 1 or len(outs[0].users) != 1:
-        raise _NoStack("the stack's output has other users than one head")
-    head = next(iter(outs[0].users))
-    if not (head.op == "call_function" and head.target in LINEAR):
-        raise _NoStack(f"the stack's output goes to {head.target}")
-    hx, hw, hb = _linear_operands(head)
-    W = params.value.get(hw) if params.is_param(hw) else None
-    B = params.value.get(hb) if hb is not None and params.is_param(hb) else None
-    if hx is not outs[0] or not isinstance(W, torch.Tensor) or W.dim() != 2 or W.shape[1] != D or \
-            (hb is not None and not (isinstance(B, torch.Tensor) and tuple(B.shape) == (W.shape[0],))):
-        raise _NoStack("the head is not a linear of a parameter [N, 1024]")
-    return head, W, B
+# ------------------------------------------------------------------ finding a stack
+class _NoStack(Exception):
+    """Why a Qwen3Model region is not a stack the op takes."""
+
+
+@dataclass
+class Plan:
+    """A stack found in a graph; nodes are named, so the plan applies to copies of the graph.
+
+    region: the names of the stack's nodes in graph order; x / mask / head: the names of the hidden
+    states, the mask placeholder and the head; mask_index: the mask's position among the graph's
+    inputs; weights: role -> tensor, a role being (layer, LAYER_KEYS entry), "norm", "inv_freq" or
+    "head"; bias: the head's bias or None."""
+    region: list
+    x: Optional[str]
+    mask: Optional[str]
+    mask_index: int
+    head: Optional[str]
+    weights: dict
+    bias: Any
+    layers: int
+    out_features: int
+    max_tokens: int
+
+    def tensors(self):
+        """Every weight in a fixed order: each layer's LAYER_KEYS, then norm, head, inv_freq."""
+        per_layer = [self.weights[(i, k)] for i in range(self.layers) for k in LAYER_KEYS]
+        return per_layer + [self.weights[r] for r in ("norm", "head", "inv_freq")]
+
+
+class _Matcher:
+    """Checks one Qwen3Model region (the nodes that ran inside module path `root`) against the rules
+    in the module docstring and builds its Plan."""
+
+    def __init__(self, root, nodes, example_of, placeholders):
+        self.root, self.nodes, self.inside = root, nodes, set(nodes)
+        self.example_of, self.placeholders = example_of, placeholders
+        self.roles = {}
+        self.attention = []
+
+    def is_param(self, n):
+        return n.op == "placeholder" and (isinstance(self.example_of.get(n), torch.nn.Parameter)
+                                          or "_parameters_" in n.name or "_buffers_" in n.name)
+
+    def bind(self, role, node):
+        t = self.example_of.get(node)
+        if not isinstance(t, torch.Tensor):
+            raise _NoStack(f"{role}: no tensor")
+        if self.roles.setdefault(role, t) is not t:
+            raise _NoStack(f"two tensors for {role}")
+
+    def rel_path(self, n):
+        """Path (below the root) and class of the innermost module node n ran in."""
+        path, cls = list(n.meta["nn_module_stack"].values())[-1]
+        return (path[len(self.root) + 1:] if path != self.root else ""), _class_name(cls)
+
+    def scan(self):
+        for n in self.nodes:
+            rel, cls = self.rel_path(n)
+            layer, sub = _layer_path(rel)
+            weight = None
+            if n.op == "call_function" and n.target in _LINEAR:
+                x, weight, bias = _linear_operands(n)
+                role = _LINEAR_ROLE.get(sub) if layer is not None else None
+                if role is None or bias is not None or not self.is_param(weight):
+                    raise _NoStack(f"a linear in {rel or 'the root'}")
+                self.bind((layer, role), weight)
+            elif n.op == "call_function" and n.target in _SDPA:
+                self.attention.append(n)
+            for a in n.all_input_nodes:
+                if a is weight or not self.is_param(a):
+                    continue
+                if layer is not None and sub in _PARAM_ROLE:
+                    self.bind((layer, _PARAM_ROLE[sub]), a)
+                elif layer is None and sub in _STACK_ROLE:
+                    self.bind(_STACK_ROLE[sub], a)
+                else:
+                    raise _NoStack(f"parameter {a.name} used in {rel or 'the root'}")
+            self.check_constants(n, cls, rel)
+
+    @staticmethod
+    def check_constants(n, cls, rel):
+        """The op has RMSNorm's eps and RoPE without attention scaling built in."""
+        floats = [a for a in n.args if isinstance(a, float)]
+        if n.op != "call_function" or not floats:
+            return
+        if n.target in _ADD and cls.endswith("RMSNorm") and any(abs(c - EPS) > 1e-12 for c in floats):
+            raise _NoStack(f"RMSNorm eps {floats} (the op has {EPS})")
+        if n.target in _MUL and rel == "rotary_emb" and any(c != 1.0 for c in floats):
+            raise _NoStack(f"RoPE attention scaling {floats}")
+
+    def layer_count(self):
+        layers = 1 + max((r[0] for r in self.roles if isinstance(r, tuple)), default=-1)
+        if layers < 1:
+            raise _NoStack("no layers")
+        for i in range(layers):
+            for key, shape in LAYER_SHAPES.items():
+                t = self.roles.get((i, key))
+                if t is None or tuple(t.shape) != shape:
+                    raise _NoStack(f"layer {i} {key}: {None if t is None else tuple(t.shape)}, need {shape}")
+        for role, shape in (("norm", (D,)), ("inv_freq", (DH // 2,))):
+            if tuple(getattr(self.roles.get(role), "shape", ())) != shape:
+                raise _NoStack("final norm / RoPE frequencies")
+        return layers
+
+    def mask(self, layers):
+        """The one 4-D mask placeholder that every layer's attention uses, bidirectionally at 1/sqrt(128)."""
+        names = ("query", "key", "value", "attn_mask", "dropout_p", "is_causal", "scale")
+        used = set()
+        for n in self.attention:
+            a = dict(zip(names, n.args))
+            a.update(n.kwargs)
+            scale = a.get("scale")
+            if a.get("dropout_p", 0.0) != 0.0 or a.get("is_causal", False) or \
+                    (scale is not None and abs(scale - DH ** -0.5) > 1e-6):
+                raise _NoStack("attention: dropout, causal or another scale")
+            used.add(a.get("attn_mask"))
+        if len(self.attention) != layers or len(used) != 1:
+            raise _NoStack(f"{len(self.attention)} attentions for {layers} layers, {len(used)} masks")
+        (m,) = used
+        t = self.example_of.get(m)
+        if not (isinstance(m, torch.fx.Node) and m.op == "placeholder" and isinstance(t, torch.Tensor)
+                and t.dim() == 4 and (t.dtype == torch.bool or t.is_floating_point())):
+            raise _NoStack("the attention mask is not a 4-D input of the graph")
+        return m
+
+    def hidden_states(self, mask):
+        """The region's one tensor input besides the mask and the weights: GPU hidden states [B, L, 1024]."""
+        outside = []
+        for n in self.nodes:
+            for a in n.all_input_nodes:
+                if a in self.inside or a is mask or self.is_param(a) or a in outside:
+                    continue
+                if a.op == "placeholder" and isinstance(self.example_of.get(a), (int, torch.SymInt)):
+                    continue        # sizes
+                outside.append(a)
+        if len(outside) != 1:
+            raise _NoStack(f"inputs {[a.name for a in outside]}")
+        t = outside[0].meta.get("example_value")
+        if not (isinstance(t, torch.Tensor) and t.dim() == 3 and t.shape[-1] == D and t.is_floating_point()):
+            raise _NoStack("hidden states are not [B, L, 1024]")
+        if not _on_gpu(t):
+            raise _NoStack("hidden states are not on the GPU")
+        return outside[0]
+
+    def head(self):
+        """The linear [N, 1024] of a parameter that alone consumes the region's one output."""
+        leaving = [n for n in self.nodes if any(u not in self.inside for u in n.users)]
+        if len(leaving) != 1 or len(leaving[0].users) != 1:
+            raise _NoStack("the stack's output has other users than one head")
+        head = next(iter(leaving[0].users))
+        if not (head.op == "call_function" and head.target in _LINEAR):
+            raise _NoStack(f"the stack's output goes to {head.target}")
+        hx, hw, hb = _linear_operands(head)
+        w = self.example_of.get(hw) if self.is_param(hw) else None
+        b = self.example_of.get(hb) if hb is not None and self.is_param(hb) else None
+        ok = hx is leaving[0] and isinstance(w, torch.Tensor) and w.dim() == 2 and w.shape[1] == D
+        if not ok or (hb is not None and not (isinstance(b, torch.Tensor) and tuple(b.shape) == (w.shape[0],))):
+            raise _NoStack("the head is not a linear of a parameter [N, 1024]")
+        return head, w, b
+
+    def plan(self):
+        self.scan()
+        layers = self.layer_count()
+        mask = self.mask(layers)
+        x = self.hidden_states(mask)
+        head, w, b = self.head()
+        weights = dict(self.roles, head=w)
+        return Plan([n.name for n in self.nodes], x.name, mask.name, self.placeholders.index(mask), head.name,
+                    weights, b, layers, int(w.shape[0]), MAX_TOKENS)
+
+
+def _linear_operands(node):
+    names = ("input", "weight", "bias")
+    got = dict(zip(names, node.args))
+    got.update({k: v for k, v in node.kwargs.items() if k in names})
+    return got.get("input"), got.get("weight"), got.get("bias")
 
 
 def find(gm, example_inputs):
     """The first stack + head in ``gm`` the GPU op takes, as a Plan, or None. Only graphs whose hidden
     states live on the GPU are fused (host tensors keep the plain graph)."""
     placeholders = [n for n in gm.graph.nodes if n.op == "placeholder"]
-    value = dict(zip(placeholders, example_inputs))
+    example_of = dict(zip(placeholders, example_inputs))
     regions = {}
     for n in gm.graph.nodes:
-        if n.op in ("call_function", "call_method", "call_module"):   # inputs carry their first user's module
-            root = next((path for path, cls in (n.meta.get("nn_module_stack") or {}).values()
-                         if _cls_name(cls) in ROOTS), None)
-            if root is not None:
-                regions.setdefault(root, []).append(n)
+        if n.op not in ("call_function", "call_method", "call_module"):
+            continue                    # inputs carry the module of their first user
+        stack_ = n.meta.get("nn_module_stack") or {}
+        root = next((path for path, cls in stack_.values() if _class_name(cls) == _ROOT_CLASS), None)
+        if root is not None:
+            regions.setdefault(root, []).append(n)
     for root, nodes in regions.items():
         try:
-            return _match(root, nodes, value, placeholders)
+            return _Matcher(root, nodes, example_of, placeholders).plan()
         except _NoStack as e:
             log.info("torch_xdna: %s is not a stack the GPU op takes: %s", root, e)
     return None
-
-
-def _match(root, nodes, value, placeholders):
-    """A Plan for the Qwen3Model call `nodes` (module path `root`), or _NoStack with the reason."""
-    inside = set(nodes)
-    params = _Params(value)
-    attn = []
-    for n in nodes:
-        path, cls = _module_of(n)
-        rel = path[len(root) + 1:] if path != root else ""
-        skip = None
-        if n.op == "call_function" and n.target in LINEAR:
-            _, w, b = _linear_operands(n)
-            m = _PROJ.fullmatch(rel)
-            if m is None or b is not None or not params.is_param(w):
-                raise _NoStack(f"a linear in {rel or 'the root'}")
-            params.add((int(m[1]), m[2] or m[3]), w)
-            skip = w
-        elif n.op == "call_function" and n.target in SDPA:
-            attn.append(n)
-        for a in n.all_input_nodes:
-            if a is skip or not params.is_param(a):
-                continue
-            role = _param_role(rel)
-            if role is None:
-                raise _NoStack(f"parameter {a.name} used in {rel or 'the root'}")
-            params.add(role, a)
-        _check_constants(n, cls, rel)
-    layers = params.layer_count()
-    if layers < 1:
-        raise _NoStack("no layers")
-    params.check_shapes(layers)
-    mask = _attention_mask(attn, layers, value)
-    x = _hidden_input(nodes, inside, mask, params, value)
-    head, W, B = _head_of(nodes, inside, params)
-    params.by_role["head"] = W
-    return Plan([n.name for n in nodes], x.name, mask.name, placeholders.index(mask), head.name, params.by_role, B,
-                layers, int(W.shape[0]), MAX_TOKENS)
 
 
 # ------------------------------------------------------------------ the fused graph
@@ -288,26 +313,48 @@ def fuse(gm, plan, stack_id, cfg_id):
     gm.recompile()
 
 
+def _truncated(gm, name):
+    """A copy of ``gm`` that returns the value of node `name` (and computes nothing after it)."""
+    probe = copy_module(gm)
+    target = next(n for n in probe.graph.nodes if n.name == name)
+    out = next(n for n in probe.graph.nodes if n.op == "output")
+    probe.graph.erase_node(out)
+    probe.graph.output(target)
+    probe.graph.eliminate_dead_code()
+    probe.recompile()
+    return probe
+
+
 # ------------------------------------------------------------------ run time
 class StackUnsupported(RuntimeError):
     pass
 
 
+@dataclass(eq=False)
 class _Stack:
-    """One stack found by the backend: its weights (weakly), their GPU copies, the checks done."""
+    """A registered stack: its weights (weakly), their packed GPU copies, the check state, the call
+    shapes (static buffers, HIP graph)."""
+    refs: list
+    bias: Any
+    layers: int
+    N: int
+    max_tokens: int
+    name: str = ""
+    verified: set = field(default_factory=set)   # attention shapes whose first fused call matched
+    failed: Optional[str] = None                 # why the stack keeps to the plain graph
+    capture: bool = False                        # keep a copy of the next output (for the check)
+    captured: Any = None
+    shapes: dict = field(default_factory=dict)   # call shape -> _Shape, least recently used first
+    lens_hint: Any = None                        # (mask, lengths) parsed by the dispatcher for this call
+    _packed: Any = None                          # (weakrefs, versions, device, packed weights)
 
-    def __init__(self, plan):
-        self.refs = [weakref.ref(t) for t in plan.tensors()]
-        self.bias = weakref.ref(plan.bias) if plan.bias is not None else None
-        self.layers, self.N, self.max_tokens = plan.layers, plan.out_features, plan.max_tokens
-        self.name = f"qwen3 stack {self.layers} layers -> {self.N}"
-        self.verified = set()   # attention shapes whose first launch matched the model
-        self.failed = None      # why the stack runs in the plain graph from now on
-        self.capture = False    # keep a copy of the next output (for the check)
-        self.captured = None
-        self._packed = None     # (weakrefs, versions, device, packed weights)
-        self.shapes = {}        # call shape -> _Shape (static buffers, HIP graph)
-        self.lens_hint = None   # (mask, lengths) the dispatcher parsed for the call in flight
+    @classmethod
+    def of(cls, plan):
+        st = cls([weakref.ref(t) for t in plan.tensors()],
+                 weakref.ref(plan.bias) if plan.bias is not None else None,
+                 plan.layers, plan.out_features, plan.max_tokens)
+        st.name = f"qwen3 stack {st.layers} layers -> {st.N}"
+        return st
 
     def packed(self, dev):
         """The GEMM weights as bf16 [N, K] on dev (q|k|v and gate|up concatenated), the norms and
@@ -330,10 +377,10 @@ class _Stack:
 
         layers = []
         for i in range(self.layers):
-            L = dict(zip(LAYER_KEYS, ts[i * n:(i + 1) * n]))
-            layers.append(dict(qkv=bf(L["q"], L["k"], L["v"]), o=bf(L["o"]), gu=bf(L["gate"], L["up"]),
-                               down=bf(L["down"]), input_norm=vec(L["input_norm"]), post_norm=vec(L["post_norm"]),
-                               q_norm=vec(L["q_norm"]), k_norm=vec(L["k_norm"])))
+            Lw = dict(zip(LAYER_KEYS, ts[i * n:(i + 1) * n]))
+            layers.append(dict(qkv=bf(Lw["q"], Lw["k"], Lw["v"]), o=bf(Lw["o"]), gu=bf(Lw["gate"], Lw["up"]),
+                               down=bf(Lw["down"]), input_norm=vec(Lw["input_norm"]), post_norm=vec(Lw["post_norm"]),
+                               q_norm=vec(Lw["q_norm"]), k_norm=vec(Lw["k_norm"])))
         norm, head, inv_freq = ts[self.layers * n:]
         bias = self.bias().detach().to(dev, torch.float32).contiguous() if self.bias is not None else None
         pk = dict(layers=layers, norm=vec(norm), head=bf(head), inv_freq=inv_freq.detach().to(dev, torch.float32),
@@ -342,10 +389,14 @@ class _Stack:
         return pk
 
     def macs(self, lens):
-        per_token = self.layers * (D * (NH + 2 * NKV) * DH + NH * DH * D + 3 * D * INTER) + D * self.N
-        return per_token * sum(lens) + self.layers * sum(2 * NH * DH * n * n for n in lens)
+        """Multiply-accumulates of a call: per token, each layer's four projections (q|k|v, o, gate|up,
+        down) and the head; per sequence and layer, the attention's two [n x n x 128] products per head."""
+        proj = D * (NH + 2 * NKV) * DH + NH * DH * D + 2 * D * INTER + INTER * D
+        tokens = sum(lens)
+        attn = sum(n * n for n in lens) * 2 * NH * DH
+        return tokens * (self.layers * proj + D * self.N) + self.layers * attn
 
-    def fail(self, e):
+    def give_up(self, e):
         self.failed = f"{type(e).__name__}: {e}"[:300]
         stats.fallbacks.append((self.name, self.failed))
         log.warning("torch_xdna: GPU %s failed (%s); it runs as the plain graph from now on", self.name, self.failed)
@@ -355,8 +406,9 @@ _stacks = []    # stack id -> _Stack
 
 
 def register(plan):
+    """A stack id for the plan (its index in the process-wide registry)."""
     with _lock:
-        _stacks.append(_Stack(plan))
+        _stacks.append(_Stack.of(plan))
         return len(_stacks) - 1
 
 
@@ -366,9 +418,9 @@ def out_features(stack_id):
 
 def lengths(mask):
     """Each sequence's length n when ``mask`` [B, H, L, L] (bool, or float with 0 for "sees" and a
-    large negative value for "does not") is a prefix block: query positions < n see exactly the key
-    positions < n, and every later position sees only itself or nothing (stack.py:328-352). None for
-    any other mask (causal, heads that differ, ...)."""
+    large negative value for "does not", the same for every head) is a prefix block: query positions
+    below n see exactly the key positions below n, and every later position sees only itself or
+    nothing (stack.py:328-352). None for any other mask (causal, heads that differ, ...)."""
     if not isinstance(mask, torch.Tensor) or mask.dim() != 4 or mask.shape[-1] != mask.shape[-2]:
         return None
     if mask.dtype == torch.bool:
@@ -376,24 +428,24 @@ def lengths(mask):
     elif mask.is_floating_point():
         sees = mask == 0
         if not bool((sees | (mask <= -1e4)).all()):
-            return None
+            return None              # neither "sees" nor "does not"
     else:
         return None
-    if sees.shape[1] > 1 and not bool((sees == sees[:, :1]).all()):
-        return None
-    sees = sees[:, 0]                                   # [B, L, L]
-    n = sees[:, 0].sum(-1)                              # what position 0 sees fixes the length
-    i = torch.arange(sees.shape[-1], device=sees.device)
-    valid_q = i[None, :, None] < n[:, None, None]       # [B, L, 1]
-    block = valid_q & (i[None, None, :] < n[:, None, None])
-    pad_ok = (sees == (i[:, None] == i[None, :])[None]) | ~sees.any(-1, keepdim=True)
-    if not bool(torch.where(valid_q, sees == block, pad_ok).all()):
-        return None
-    return n.tolist()
+    if not bool((sees == sees[:, :1]).all()):
+        return None                  # heads differ
+    sees = sees[:, 0]
+    L = sees.shape[-1]
+    n = sees[:, 0].sum(-1)           # how many keys position 0 sees: the length if anything
+    pos = torch.arange(L, device=sees.device)
+    valid = pos[None, :] < n[:, None]                               # [B, L]
+    block = valid[:, :, None] & valid[:, None, :]                   # the prefix block
+    own = torch.eye(L, dtype=torch.bool, device=sees.device)[None]  # a padding row seeing itself
+    rows_ok = torch.where(valid[:, :, None], sees == block, (sees == own) | ~sees.any(-1, keepdim=True))
+    return n.tolist() if bool(rows_ok.all()) else None
 
 
-def _groups(lens):
-    """The attention shapes of a call (query blocks per sequence): each is checked on its first call."""
+def _attention_shapes(lens):
+    """The attention shapes of a call (query blocks per sequence); each is checked on its first call."""
     return {-(-n // QBLOCK) for n in lens}
 
 
@@ -501,86 +553,57 @@ def run(cfg, stack_id, x, mask):
         stats.launches += 1
         if st.capture:
             st.captured = out.float().clone()
-    stats.calls["gpu"] += 1
-    stats.seconds["gpu"] += time.perf_counter() - t0
-    stats.macs["gpu"] += st.macs(lens)
+    stats.record("gpu", t0, st.macs(lens))
     return out
 
 
-class _Reached(Exception):
-    pass
-
-
-class _RunTo(torch.fx.Interpreter):
-    """Runs a graph eagerly until one named node has its value."""
-
-    def __init__(self, gm, target):
-        super().__init__(gm, garbage_collect_values=True)
-        self.extra_traceback = False
-        self.target, self.value = target, None
-
-    def run_node(self, n):
-        out = super().run_node(n)
-        if n.name == self.target:
-            self.value = out
-            raise _Reached()
-        return out
-
-
-def _value_at(gm, args, name):
-    runner = _RunTo(gm, name)
-    with torch.no_grad():
-        try:
-            runner.run(*args)
-        except _Reached:
-            pass
-    if runner.value is None:
-        raise RuntimeError(f"{name} not reached")
-    return runner.value
-
-
 class Dispatch:
-    """What the backend returns for a graph with a stack: the fused graph when the GPU op takes the
-    call, else the plain one; checks each attention shape's first fused call against the original
-    graph (stack.py:412-460)."""
+    """What the backend returns for a graph with a stack: calls the fused graph when the GPU op takes
+    the call (prefix-block mask, lengths within the cap, the stack not given up), else the plain one;
+    the first fused call of each attention shape is checked against the original graph's head output,
+    computed eagerly (stack.py:412-460)."""
 
     def __init__(self, plan, stack_id, cfg, fused, plain, orig):
         self.plan, self.stack_id, self.cfg = plan, stack_id, cfg
-        self.fused, self.plain, self.orig = fused, plain, orig
+        self.fused, self.plain = fused, plain
+        self.reference = _truncated(orig, plan.head)     # the original graph, up to the head's value
 
-    def _fusable(self, st, args):
-        """The call's sequence lengths when the fused graph takes it, else None."""
+    def _lengths(self, st, args):
         if st.failed is not None or not kernels.available():
             return None
         lens = lengths(args[self.plan.mask_index])
-        return lens if lens is not None and all(1 <= n <= st.max_tokens for n in lens) else None
+        if lens is None or not all(1 <= n <= st.max_tokens for n in lens):
+            return None
+        return lens
 
     def __call__(self, *args):
         st = _stacks[self.stack_id]
-        lens = self._fusable(st, args)
-        if lens is not None:
-            shapes = _groups(lens)
-            verify = self.cfg.verify == "always" or (self.cfg.verify == "first" and not shapes <= st.verified)
-            st.capture = verify
-            st.lens_hint = (args[self.plan.mask_index], lens)
-            try:
-                out = self.fused(*args)
-                if verify:
-                    self._verify(st, args, lens, shapes)
-                stats.stacks[(st.name, "gpu")] += 1
-                return out
-            except Exception as e:      # launch failure, or a mismatch
-                st.fail(e)
-            finally:
-                st.capture, st.captured, st.lens_hint = False, None, None
-        stats.stacks[(st.name, "cpu")] += 1
-        return self.plain(*args)
+        lens = self._lengths(st, args)
+        if lens is None:
+            stats.stacks[(st.name, "cpu")] += 1
+            return self.plain(*args)
+        shapes = _attention_shapes(lens)
+        check = self.cfg.verify == "always" or (self.cfg.verify == "first" and not shapes <= st.verified)
+        st.capture, st.lens_hint = check, (args[self.plan.mask_index], lens)
+        try:
+            out = self.fused(*args)
+            if check:
+                self._check(st, args, lens, shapes)
+        except Exception as e:          # a launch failure, or a mismatch
+            st.give_up(e)
+            stats.stacks[(st.name, "cpu")] += 1
+            return self.plain(*args)
+        finally:
+            st.capture, st.captured, st.lens_hint = False, None, None
+        stats.stacks[(st.name, "gpu")] += 1
+        return out
 
-    def _verify(self, st, args, lens, shapes):
-        """The fused output's valid rows vs the original graph's head output, run eagerly."""
+    def _check(self, st, args, lens, shapes):
+        """The fused output's valid rows against the original graph's head output, relative norm."""
         if st.captured is None:
             raise RuntimeError("the fused graph did not run the stack op")
-        want_all = _value_at(self.orig, args, self.plan.head)
+        with torch.no_grad():
+            want_all = self.reference(*args)
         per_seq = lens * st.captured.shape[0] if len(lens) == 1 else lens
         got = torch.cat([st.captured[b, :n] for b, n in enumerate(per_seq)]).double()
         want = torch.cat([want_all[b, :n] for b, n in enumerate(per_seq)]).double()
@@ -592,7 +615,8 @@ class Dispatch:
 
 
 def compile_fused(gm, example_inputs, cfg, cfg_id, plan, compile_graph):
-    """The Dispatch over the fused and the plain compilation of ``gm`` (which this rewrites)."""
+    """The Dispatch over the fused and the plain compilation of ``gm`` (which the plain compilation
+    rewrites in place)."""
     orig = copy_module(gm)
     fused = copy_module(gm)
     sid = register(plan)
