@@ -148,19 +148,28 @@ class ConvLayer:
 
 
 def _layer(weight, h, w, relu):
+    """The ConvLayer of one weight at one input size and ReLU flag (quantized weights, shift and device
+    choice are per layer, conv.py:106-113). The entry checks that its weight is still the tensor it was
+    made for (a freed tensor's id can be reused) and is dropped when that weight is garbage-collected."""
     key = (id(weight), h, w, relu)
-    hit = _layers.get(key)
-    if hit is not None and hit[0]() is weight:
-        return hit[1]
-    layer = ConvLayer(weight, h, w, relu)
-    _layers[key] = (weakref.ref(weight), layer)
-    return layer
+    entry = _layers.get(key)
+    if entry is None or entry[0]() is not weight:
+        layer = ConvLayer(weight, h, w, relu)
+
+        def drop(_, key=key, layer=layer):
+            if _layers.get(key, (None, None))[1] is layer:
+                del _layers[key]
+
+        entry = _layers[key] = (weakref.ref(weight, drop), layer)
+    return entry[1]
 
 
 def _failed(layer, e):
+    """A GPU launch of the layer raised or disagreed with the CPU: the layer stays on the CPU."""
     layer.device = "cpu"
-    stats.fallbacks.append((layer.name, f"{type(e).__name__}: {e}"[:300]))
-    log.warning("torch_xdna: GPU %s failed (%s); it runs on the CPU from now on", layer.name, e)
+    why = f"{type(e).__name__}: {e}"
+    stats.fallbacks.append((layer.name, why[:300]))
+    log.warning("torch_xdna: GPU %s failed (%s); the layer runs on the CPU from now on", layer.name, why)
 
 
 def _gpu_route(cfg, layer, on_gpu):
