@@ -41,6 +41,7 @@ median), with the thread count and the CPU model; each record says what its samp
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -69,6 +70,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="headline", choices=WORKLOADS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--tile", default=None,
+                    help="force this tile (a kernels.TILES name) on every GEMM shape of the c1/c2/c5/decode "
+                         "workloads instead of the built-in rule and the tuned table (results do not depend on it)")
     return ap.parse_args()
 
 
@@ -256,13 +260,29 @@ def gate(ms):
     torch.cuda._sleep(int(ms * _SLEEP_CYCLES_PER_MS))
 
 
+# GPU time of untimed work run behind the gate, right before a timed region. Under a sustained int8
+# load the card sits at its 1400 W board limit, and after the idle gate its power controller takes about
+# 15 ms to settle: the first few launches run fast, the next ones up to 25% slow, then the clock recovers
+# (per-dispatch durations of the M=8192 GEMM: 442 -> 569 -> ~450 us). The pre-heat keeps that transient,
+# which a continuously busy job does not see, out of the timed region.
+PREHEAT_MS = 50.0
+
+
+def preheat_count(ms_per_unit, cap=500):
+    """Units of work (steps or launches) that fill about PREHEAT_MS of GPU time."""
+    return int(min(cap, math.ceil(PREHEAT_MS / max(ms_per_unit, 1e-3))))
+
+
 def gated_timed_steps(a, step, timer, host_ms_per_step):
-    """The timed region: a gate covering the host's enqueue time of the K steps (1.5 x the measured
-    ungated time + 2 ms), then K eager steps between two events; step(i, t) records per-launch
-    events of the dominant kernel with t. Returns GPU seconds per step."""
+    """The timed region: a gate covering the host's enqueue time (1.5 x the measured ungated time + 2
+    ms), untimed pre-heat steps (about PREHEAT_MS of work), then K eager steps between two events;
+    step(i, t) records per-launch events of the dominant kernel with t. Returns GPU seconds per step."""
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    gate(1.5 * host_ms_per_step * a.steps + 2.0)
+    heat = preheat_count(host_ms_per_step)
+    gate(1.5 * host_ms_per_step * (a.steps + heat) + 2.0)
+    for i in range(heat):
+        step(i, None)
     e0.record()
     for i in range(a.steps):
         step(i, timer)
@@ -273,12 +293,20 @@ def gated_timed_steps(a, step, timer, host_ms_per_step):
 
 def back_to_back_us(calls, launches):
     """Microseconds per launch of `launches` calls (cycling through `calls`) queued behind a gate and
-    run back to back between two events (no events between the launches)."""
+    untimed pre-heat launches (about PREHEAT_MS of work), run back to back between two events (no
+    events between the launches)."""
     for fn in calls:
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for fn in calls:
+        fn()
+    torch.cuda.synchronize()
+    heat = preheat_count((time.perf_counter() - t0) * 1e3 / len(calls))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    gate(2.0 + 0.05 * launches)
+    gate(2.0 + 0.05 * (launches + heat))
+    for i in range(heat):
+        calls[i % len(calls)]()
     e0.record()
     for i in range(launches):
         calls[i % len(calls)]()
@@ -289,7 +317,7 @@ def back_to_back_us(calls, launches):
 
 def per_shape_us(sets, launches=10):
     """Microseconds per launch of each shape's fused GEMM: `launches` back-to-back launches of that
-    shape behind a gate, between two events. The launches cycle through enough copies of the weight
+    shape behind a gate and a pre-heat, between two events. The launches cycle through enough copies of the weight
     (the sets' own, then clones) that they span more than the 256 MB Infinity Cache, so a weight is
     never read from the cache a previous launch filled."""
     out = []
@@ -302,15 +330,8 @@ def per_shape_us(sets, launches=10):
         for i in range(launches):
             x, wq, sw, b, M, N, K = sets[i % len(sets)][j]
             ops.append((kernels.quant_rows(x), weights[i % ncopies], sw, b, x.dtype))
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        gate(2.0)
-        e0.record()
-        for (xq, sx), wq, sw, b, dt in ops:
-            kernels.mm_i8_dequant(xq, sx, wq, sw, b, dt)
-        e1.record()
-        torch.cuda.synchronize()
-        out.append(e0.elapsed_time(e1) * 1e3 / launches)
+        calls = [lambda o=o: kernels.mm_i8_dequant(o[0][0], o[0][1], o[1], o[2], o[3], o[4]) for o in ops]
+        out.append(back_to_back_us(calls, launches))
     return out
 
 
@@ -351,6 +372,10 @@ def roofline_us(ops, nbytes):
 
 
 def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
+    if a.tile:
+        for M, N, K in shapes:
+            kernels.tile_set("i8", M, N, kernels.round_up(K, 16), a.tile)
+        workload += f" (tile forced: {a.tile})"
     sets = gemm_sets(shapes, dev, x_dtype=x_dtype, bias=bias)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(a.steps)]
     step = lambda i, t: run_gemm_step_split(sets[i % len(sets)], ev[i] if t else None)   # noqa: E731
@@ -374,13 +399,14 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
     bound_us = sum(roofline_us(2 * M * N * K, gemm_bytes(M, N, K, xb, yb, bias)) for M, N, K in shapes)
     out = {"value": round(ops_step / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
            "host_ms_per_step": round(host * 1e3, 4),
-           "timing": "GPU time of K eager steps enqueued behind a gate (kernels back to back), each "
+           "timing": "GPU time of K eager steps enqueued behind a gate and about 50 ms of untimed pre-heat "
+                     "steps (kernels back to back), each "
                      "step's quantizes then its GEMMs with events between; host_ms_per_step: the same "
                      "steps launched without a gate, wall clock",
            "config": {"workload": workload, "shapes_mnk": shapes, "x_dtype": str(x_dtype).replace("torch.", ""),
                       "bias": bias, "rotating_sets": len(sets)},
            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                        "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic(label.lower()),
+                        "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None if a.tile else traffic(label.lower()),
                         "kernel": gemm_kernels(dev, shapes),
                         "launches": nshape * reps, "avg_launch_us": round(g_sec / (nshape * reps) * 1e6, 2),
                         "alg_bytes_per_launch": round(g_bytes / (nshape * reps)),

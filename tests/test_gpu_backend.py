@@ -259,8 +259,9 @@ def test_ops_direct(gpu):
     assert torch.equal(acc.cpu(), torch._int_mm(xq, wq.t().contiguous()))
     wc = torch.randn(48, 3, 3, 3, generator=g)
     xc = torch.randint(-127, 128, (2, 3, 13, 37), generator=g, dtype=torch.int8)
+    wg = wc.to(gpu)          # held: a layer is cached for as long as its weight lives
     for relu in (False, True):
-        q, scale = torch.ops.xdna.conv3x3(xc.to(gpu), wc.to(gpu), relu, cid)
+        q, scale = torch.ops.xdna.conv3x3(xc.to(gpu), wg, relu, cid)
         from torch_xdna import conv as xconv
 
         layer = next(L for _, L in xconv._layers.values() if L.relu == relu)

@@ -81,9 +81,10 @@ def test_quant_rows_ties_zero_rows_strided(gpu):
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("k", [1024, 200, 16384, 40000])
 def test_quant_rows_near_half(gpu, dtype, k):
-    """Quotients x / s placed within 6e-5 of half-integers, on both sides and exactly on them, under
-    irregular scales: the kernels round fl(x / s) like torch (the fast product with 1 / s is trusted only
-    farther than 2^-15 from a half-integer). Covers the 16-element-group, per-vector and long-row paths."""
+    """Quotients x / s placed within 6e-5 of half-integers, on both sides, exactly on them and at fractions
+    of the float spacing there, under irregular scales: the kernels round fl(x / s) like torch (the fast
+    product with 1 / s is trusted only farther than 2^-15 from a half-integer; nearer, the exact residual
+    x - h * s decides). Covers the 16-element-group, per-vector and long-row paths."""
     from torch_xdna import kernels
 
     rng = np.random.default_rng(k + len(dtype))
@@ -93,6 +94,11 @@ def test_quant_rows_near_half(gpu, dtype, k):
     half = rng.integers(-127, 127, (rows, k)).astype(np.float64) + 0.5
     d = rng.choice([0.0, 1e-7, -1e-7, 3e-6, -3e-6, 1.5e-5, -1.5e-5, 2.9e-5, -2.9e-5, 3.1e-5, -3.1e-5, 6e-5, -6e-5],
                    (rows, k))
+    # every other column: offsets in units of the float spacing at the half-integer, around the half-spacing
+    # boundary where fl(x / s) stops being the half-integer itself
+    ulp = np.spacing(np.abs(half).astype(np.float32)).astype(np.float64)
+    d_ulp = rng.choice([0.3, -0.3, 0.49, -0.49, 0.51, -0.51, 0.9, -0.9, 1.1, -1.1, 2.5, -2.5], (rows, k)) * ulp
+    d[:, 1::2] = d_ulp[:, 1::2]
     x = ((half + d) * s[:, None].astype(np.float64)).astype(np.float32)
     x[:, 0] = amax                                   # fixes the row's amax, hence s
     xt = torch.from_numpy(x).to(DT[dtype])
