@@ -595,6 +595,8 @@ def test_sweep_tool(gpu, tile_table, tmp_path):
     assert len(recs) == n_lines == want
     assert all(r["status"] == "ok" and r["exact"] and r["gpu_us"] > 0 for r in recs), recs
     assert {r["checked_against"] for r in recs} == {"cpu"}
+    # each record names the launch plan its time belongs to: the forced tile heads it
+    assert all(r["plan"][0] == r["tiling"] and len(r["rule_plan"]) == 3 for r in recs), recs
     out2 = str(tmp_path / "sweep_tiles.jsonl")           # --tiles: only the named tiles
     sweep.main(["--kind", "i8", "--rows", "300", "--shapes", "520x256", "--tiles", "t64x64", "t32x32k4", "--out", out2])
     assert sorted(json.loads(line)["tiling"] for line in open(out2)) == ["t32x32k4", "t64x64"]

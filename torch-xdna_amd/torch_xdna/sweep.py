@@ -164,15 +164,19 @@ def sweep_shape(kind, M, N, K, dev, case, done, out, tiles=None):
     bench, exact, want, how, ops = case
     kernels.tile_set(kind, M, N, K, "auto")
     rule = kernels.tile_get(dev, kind, M, N, K)
+    rule_plan = kernels.tile_plan(dev, kind, M, N, K)
     ref_kind = "cpu"
     if want is None:               # too large for the CPU: the rule's tile is the reference
         want, ref_kind = exact(), "rule"
     for tile in candidates(kind, M):
         if (kind, M, N, K, tile) in done or (tiles is not None and tile not in tiles):
             continue
-        rec = {"kind": kind, "M": M, "N": N, "K": K, "tiling": tile, "rule": rule, "checked_against": ref_kind}
+        rec = {"kind": kind, "M": M, "N": N, "K": K, "tiling": tile, "rule": rule, "rule_plan": list(rule_plan),
+               "checked_against": ref_kind}
         try:
             kernels.tile_set(kind, M, N, K, tile)
+            # the launch plan the time belongs to: rows [0, m1) with the head tile, the rest with the tail
+            rec["plan"] = list(kernels.tile_plan(dev, kind, M, N, K))
             got = exact()
             rec["exact"] = _agrees(got, want, how)
             us = gpu_us(bench)
