@@ -60,7 +60,7 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, TFLOP/s
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
 MALL_BYTES = 256 << 20
 METRIC = "W8A8 GEMM & int8 conv3x3 TOPS on 1 MI355X; % of int8 MFMA peak / HBM BW"
-WORKLOADS = ["headline", "c1", "c2", "c3", "c4", "c5", "decode", "quant", "bf16", "vgg16", "stack", "copy"]
+WORKLOADS = ["headline", "c1", "c2", "c3", "c4", "c5", "decode", "quant", "bf16", "vgg16", "stack", "copy", "libref"]
 
 
 def parse():
@@ -227,7 +227,7 @@ def main():
            "data": "synthetic (seed 0, randn)"}
     bench = {"headline": bench_headline, "c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4,
              "c5": bench_c5, "decode": bench_decode, "quant": bench_quant, "bf16": bench_bf16, "vgg16": bench_vgg16,
-             "stack": bench_stack, "copy": bench_copy}[a.workload]
+             "stack": bench_stack, "copy": bench_copy, "libref": bench_libref}[a.workload]
     res.update(bench(a, dev))
     print(json.dumps(res), flush=True)
 
@@ -549,6 +549,39 @@ def bench_copy(a, dev):
             "config": {"workload": "bitwise_not int32 [2^28]: reads 1 GiB, writes 1 GiB"},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": b, "kernel": "torch elementwise"}}
+
+
+def bench_libref(a, dev):
+    """Reference point, not this library: the vendor library's GEMMs on C5's shape 8192x14336x4096 with the
+    same gate and pre-heat. hipBLASLt's int8 GEMM (torch._int_mm: int8 operands, int32 out, no quantize,
+    dequantize or bias) and its fp8 GEMM (torch._scaled_mm, e4m3 operands, unit scales, bf16 out), each on
+    rotating weights that span more than the Infinity Cache."""
+    M, N, K = 8192, 14336, 4096
+    g = gen(0)
+    a8 = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+    nw = max(2, -(-(MALL_BYTES + (64 << 20)) // (N * K)))
+    ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev) for _ in range(nw)]
+    ops = 2 * M * N * K
+    i8_us = back_to_back_us([lambda w=w: torch._int_mm(a8, w.t()) for w in ws], max(20, a.steps))
+    out = {"metric": "vendor GEMM TOPS on 1 MI355X (reference point)", "unit": "TOPS", "dtype": "int8",
+           "value": round(ops / i8_us / 1e6, 1), "ms_per_step": round(i8_us / 1e3, 4),
+           "config": {"workload": "hipBLASLt via torch._int_mm, 8192x14336x4096 int8 -> int32 (no dequant)",
+                      "rotating_weights": nw},
+           "roofline": {"bound": "mfma", "achieved": round(ops / i8_us / 1e6, 1), "peak": PEAK_INT8_TOPS,
+                        "unit": "TFLOP/s", "frac": round(ops / i8_us / 1e6 / PEAK_INT8_TOPS, 4), "traffic": None,
+                        "kernel": "hipBLASLt int8", "avg_launch_us": round(i8_us, 2)}}
+    try:
+        f8 = torch.float8_e4m3fn
+        af = (torch.randn(M, K, generator=g) * 0.5).to(f8).to(dev)
+        wf = [(torch.randn(N, K, generator=g) * 0.5).to(f8).to(dev) for _ in range(nw)]
+        one = torch.ones((), device=dev)
+        f8_us = back_to_back_us([lambda w=w: torch._scaled_mm(af, w.t(), scale_a=one, scale_b=one,
+                                                              out_dtype=torch.bfloat16) for w in wf], max(20, a.steps))
+        out["fp8"] = {"kernel": "hipBLASLt fp8 e4m3 via torch._scaled_mm, bf16 out", "avg_launch_us": round(f8_us, 2),
+                      "TFLOPs": round(ops / f8_us / 1e6, 1)}
+    except (RuntimeError, TypeError) as e:           # fp8 GEMM unavailable in this torch build
+        out["fp8"] = {"error": f"{type(e).__name__}: {e}"[:200]}
+    return out
 
 
 def conv_layer_data(dev, n, c, h, w, seed=0):
