@@ -598,7 +598,7 @@ def conv_op_record(a, dev, shape, sample_shape):
     per-image quantize of the NCHW float32 input into NHWC int8, the implicit-GEMM conv with the
     calibrated shift and the requantize fused, dequantize back to NCHW float32. The layer's first call
     (weight quantize-once, shift calibration on image 0) runs in the warm-up. value: op-level TOPS
-    (GPU time of K op calls behind the gate); roofline: the conv kernel alone, its launches back to
+    (GPU time of K op calls behind the gate and a pre-heat); roofline: the conv kernel alone, its launches back to
     back on the same inputs (the op's own conv call, measured with events on its stream)."""
     from torch_xdna import Config, conv, ops
 
@@ -629,12 +629,13 @@ def conv_op_record(a, dev, shape, sample_shape):
            "config": {"workload": f"{label} + ReLU as the op xdna::conv3x3_fused: float32 NCHW in -> per-image "
                                   "quantize -> int8 implicit-GEMM conv (calibrated shift, round half up, uint8 "
                                   "saturate) -> dequantize -> float32 NCHW out", "shift": layer.shift,
-                      "tile": kernels.tile_get(dev, "conv", n * h * w, c, 9 * layer.ci_pad), "rotating_inputs": nsets},
+                      "plan": list(kernels.tile_plan(dev, "conv", n * h * w, c, 9 * layer.ci_pad)),
+                      "rotating_inputs": nsets},
            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic(f"c4_{n}x{c}x{h}x{w}"),
                         "kernel": "mm_tile_kernel (conv, EPI_REQUANT)", "avg_launch_us": round(conv_us, 2),
                         "alg_bytes_per_launch": conv_bytes,
-                        "timing": "conv kernel launches back to back behind the gate, events around them"}}
+                        "timing": "conv kernel launches back to back behind the gate and a pre-heat, events around them"}}
     if not a.no_cpu_baseline:
         sn, sc, sh, sw_ = sample_shape
         rec["cpu_baseline"] = cpu_baseline_conv(
