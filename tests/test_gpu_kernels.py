@@ -45,7 +45,7 @@ def _i8(shape, seed, lo=-127, hi=128):
 # ------------------------------------------------------------------------------ quantize
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,k", [(1, 16), (5, 200), (7, 300), (64, 1024), (33, 4096), (3, 14336), (2, 40000),
-                                    (9, 1), (2000, 8192), (1500, 14336), (4800, 14336)])
+                                    (9, 1), (2000, 8192), (1500, 14336), (4800, 14336), (700, 4112), (600, 20000)])
 def test_quant_rows(gpu, dtype, rows, k):
     x = _rand((rows, k), DT[dtype], seed=rows * 1000 + k, outliers=1e-3)
     from torch_xdna import kernels

@@ -326,6 +326,82 @@ __global__ __launch_bounds__(256) void quant_rows_pipe_kernel(const void* __rest
   }
 }
 
+// Rows of more than 4096 (up to 16 * 256 * G) elements with k % 16 == 0: persistent blocks of 256 threads
+// walk rows with a grid stride; thread t owns groups t, t + 256, ... of 16 consecutive elements, read as raw
+// buffer loads (past the row's end they read zeros; non-temporal under NT) and written as one 16-byte store
+// each. The loads of the block's next row are issued before this row's max, quantize and stores, and the
+// four waves' maxima meet in a double-buffered LDS slot: one barrier per row. (A wave per row holds such a
+// row in up to 224 registers, too many for a second row in flight.)
+template <int DT, int G, bool NT>
+__global__ __launch_bounds__(256) void quant_rows_block_kernel(const void* __restrict__ x, int64_t rows, int64_t k,
+                                                               int64_t ld_x, int8_t* __restrict__ q, int64_t ld_q,
+                                                               int64_t k_pad, float* __restrict__ s) {
+  using V = Vec16<DT>;
+  constexpr int VEC = V::N;
+  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
+  constexpr int LPG = 16 / VEC;
+  __shared__ int red[2][4];
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int64_t stride = gridDim.x;
+  const int ng = (int)(k / 16);          // at most 256 * G (checked by the launcher)
+  const uint32_t row_bytes = (uint32_t)(k * ESZ);
+  auto load = [&](int64_t row, V (&v)[G][LPG]) {
+    const __amdgpu_buffer_rsrc_t rr =
+        make_rsrc(reinterpret_cast<const char*>(x) + (row < rows ? row : 0) * ld_x * ESZ, row < rows ? row_bytes : 0u);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const uint32_t off = (uint32_t)(t + j * 256) * (16 * ESZ);
+#pragma unroll
+      for (int l = 0; l < LPG; ++l) v[j][l].raw = buf_load_u4<NT>(rr, off + l * 16);
+    }
+  };
+  auto process = [&](int64_t row, const V (&v)[G][LPG], int buf) {
+    AbsMaxBits<DT> am;
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int l = 0; l < LPG; ++l) am.add(v[j][l]);
+    const int wm = wave_max_i(am.lane_bits());
+    if (lane == 0) red[buf][wave] = wm;
+    __syncthreads();
+    const float amax = bits_to_abs<DT>(max(max(red[buf][0], red[buf][1]), max(red[buf][2], red[buf][3])));
+    const float sc = scale_from_amax(amax);
+    const float rc = 1.0f / sc;
+    if (t == 0) s[row] = sc;
+    int8_t* qr = q + row * ld_q;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const int gi = t + j * 256;
+      if (gi < ng) {
+        float f[16];
+#pragma unroll
+        for (int l = 0; l < LPG; ++l)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) f[l * VEC + e] = v[j][l].get(e);
+        uint32_t w[4];
+        quant_pack<16>(f, sc, rc, w);
+        *reinterpret_cast<uint4*>(qr + (int64_t)gi * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+    for (int64_t c = k + t; c < k_pad; c += 256) qr[c] = 0;
+  };
+  // red[buf] of row i is read right after the barrier of row i and written again for row i + 2 only
+  // after the barrier of row i + 1, which every wave reaches after its read
+  V va[G][LPG], vb[G][LPG];
+  int64_t row = blockIdx.x;              // block-uniform: every barrier is reached by the whole block
+  load(row, va);
+  while (row < rows) {
+    load(row + stride, vb);
+    process(row, va, 0);
+    row += stride;
+    if (row >= rows) break;
+    load(row + stride, va);
+    process(row, vb, 1);
+    row += stride;
+  }
+}
+
 // Long rows (more than 512 vectors): persistent blocks of 256 threads walk rows with a grid stride;
 // each thread holds up to MAXV 16-byte vectors of a row, and the loads of the block's next row are
 // issued before this row's reduction and quantize, so HBM sees a continuous stream. The partial
@@ -436,13 +512,37 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
     return launch_status("quant_rows_scalar");
   }
   const int64_t nvec = k / VEC;
-  // One wavefront per row with 16-element groups (16-bit inputs up to 16384 per row, float32 up to 8192),
-  // except for fewer than 512 rows longer than 2048 elements: a row's latency then dominates, and the
-  // 256-thread blocks below give each row four times the lanes (measured on the decode rows, 1 and 16
-  // rows of 4096 and 14336 bf16: 4.0 us per launch instead of 4.3 and 11.2 us).
-  const int64_t gpl = cdiv(k / 16, 64);  // groups per lane
+  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
+  // One wavefront per row with 16-element groups for rows of up to 4096 elements; longer rows (and, for
+  // fewer than 512 rows, rows longer than 2048 elements, where a row's latency dominates) take 256-thread
+  // blocks per row, persistent, with the next row's loads in flight (quant_rows_block_kernel; measured on
+  // 8192 x 14336 bf16: 71 us with 256-thread rows against 74.7 us with a wave per row, and 4.0 us for the
+  // decode rows, 1 and 16 rows of 4096 and 14336 bf16, against 4.3 and 11.2 us).
+  const int64_t gpl = cdiv(k / 16, 64);  // groups per lane of a wave
+  const int64_t ngr = k / 16;            // groups of the row
   const bool few = rows < 512;
-  if (k % 16 == 0 && k < (int64_t(1) << 31) && gpl <= (DT == XDNA_F32 ? 8 : 16) && !(few && gpl > 2)) {
+  if (k % 16 == 0 && (few ? gpl > 2 : gpl > 4) && ngr <= 256 * (DT == XDNA_F32 ? 4 : 8)) {
+    const bool nt = rows * k * ESZ >= (int64_t(128) << 20);   // half the Infinity Cache
+#define XDNA_QB(G_)                                                                                           \
+  {                                                                                                           \
+    const dim3 bg(nt ? stream_blocks<quant_rows_block_kernel<DT, G_, true>>(rows)                             \
+                     : stream_blocks<quant_rows_block_kernel<DT, G_, false>>(rows));                          \
+    if (nt) quant_rows_block_kernel<DT, G_, true><<<bg, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);   \
+    else quant_rows_block_kernel<DT, G_, false><<<bg, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);     \
+  }
+    if (ngr <= 256) {
+      XDNA_QB(1)
+    } else if (ngr <= 512) {
+      XDNA_QB(2)
+    } else if (ngr <= 1024) {
+      XDNA_QB(4)
+    } else if constexpr (DT != XDNA_F32) {
+      XDNA_QB(8)
+    }
+#undef XDNA_QB
+    return launch_status("quant_rows");
+  }
+  if (k % 16 == 0 && k < (int64_t(1) << 31) && gpl <= 4) {
     const bool nt = rows * k * (DT == XDNA_F32 ? 4 : 2) >= (int64_t(128) << 20);   // half the Infinity Cache
     const dim3 grid((unsigned)cdiv(rows, 4));
     // rows of up to 4096 elements, at least 8 per CU: one round of resident workgroups whose waves take the
@@ -477,12 +577,8 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
       XDNA_QW(1)
     } else if (gpl <= 2) {
       XDNA_QW(2)
-    } else if (gpl <= 4) {
+    } else {
       XDNA_QW(4)
-    } else if (gpl <= 8) {
-      XDNA_QW(8)
-    } else if constexpr (DT != XDNA_F32) {
-      XDNA_QW(16)
     }
 #undef XDNA_QW
     return launch_status("quant_rows");
