@@ -513,15 +513,16 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
   }
   const int64_t nvec = k / VEC;
   constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
-  // One wavefront per row with 16-element groups for rows of up to 4096 elements; longer rows (and, for
-  // fewer than 512 rows, rows longer than 2048 elements, where a row's latency dominates) take 256-thread
-  // blocks per row, persistent, with the next row's loads in flight (quant_rows_block_kernel; measured on
-  // 8192 x 14336 bf16: 71 us with 256-thread rows against 74.7 us with a wave per row, and 4.0 us for the
-  // decode rows, 1 and 16 rows of 4096 and 14336 bf16, against 4.3 and 11.2 us).
+  // One wavefront per row with 16-element groups for rows of up to 2048 elements; longer rows take
+  // 256-thread blocks per row, persistent, with the next row's loads in flight (quant_rows_block_kernel).
+  // Measured on MI355X, bf16, against a wave per row: 8192 x 14336 67.4 us against 74.9, 8192 x 4096 21.6
+  // against 24.6, 3000 x 3072 8.8 against 10.7, 1024 x 3072 4.8 against 6.3, the decode rows (1 and 16 of
+  // 4096 and 14336) 4.0 against 4.3 and 11.2 us; at 2048 elements the wave per row wins (14.0 against 15.9
+  // us on 8192 rows).
   const int64_t gpl = cdiv(k / 16, 64);  // groups per lane of a wave
   const int64_t ngr = k / 16;            // groups of the row
   const bool few = rows < 512;
-  if (k % 16 == 0 && (few ? gpl > 2 : gpl > 4) && ngr <= 256 * (DT == XDNA_F32 ? 4 : 8)) {
+  if (k % 16 == 0 && gpl > 2 && ngr <= 256 * (DT == XDNA_F32 ? 4 : 8)) {
     const bool nt = rows * k * ESZ >= (int64_t(128) << 20);   // half the Infinity Cache
 #define XDNA_QB(G_)                                                                                           \
   {                                                                                                           \
@@ -542,43 +543,35 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
 #undef XDNA_QB
     return launch_status("quant_rows");
   }
-  if (k % 16 == 0 && k < (int64_t(1) << 31) && gpl <= 4) {
+  if (k % 16 == 0 && k < (int64_t(1) << 31) && gpl <= 2) {
     const bool nt = rows * k * (DT == XDNA_F32 ? 4 : 2) >= (int64_t(128) << 20);   // half the Infinity Cache
     const dim3 grid((unsigned)cdiv(rows, 4));
-    // rows of up to 4096 elements, at least 8 per CU: one round of resident workgroups whose waves take the
-    // rows beyond it, so the loads of a wave's next row overlap this row's arithmetic (a sweep of 1, 2, 4,
-    // 8 and 16 rows per wave on MI355X: 4.5 TB/s at one or two on 8192 x 4096 bf16, against 2.7 TB/s for
-    // two rounds of one-row waves; more rows per wave leave too few waves in flight)
-    if (gpl <= 4 && k * (DT == XDNA_F32 ? 4 : 2) < (int64_t(1) << 31) && rows >= 8 * (int64_t)device_cus()) {
+    // at least 8 rows per CU: one round of resident workgroups whose waves take the rows beyond it, so the
+    // loads of a wave's next row overlap this row's arithmetic (a sweep of 1, 2, 4, 8 and 16 rows per wave
+    // on MI355X: 4.5 TB/s at one or two on 8192 x 4096 bf16, against 2.7 TB/s for two rounds of one-row
+    // waves; more rows per wave leave too few waves in flight)
+    if (rows >= 8 * (int64_t)device_cus()) {
       const int64_t want = cdiv(rows, 4);
-      const unsigned pb = gpl <= 1 ? stream_blocks<quant_rows_pipe_kernel<DT, 1, false>>(want)
-                          : gpl <= 2 ? stream_blocks<quant_rows_pipe_kernel<DT, 2, false>>(want)
-                                     : stream_blocks<quant_rows_pipe_kernel<DT, 4, false>>(want);
-      {
-        const dim3 pg(pb);
+      const dim3 pg(gpl <= 1 ? stream_blocks<quant_rows_pipe_kernel<DT, 1, false>>(want)
+                             : stream_blocks<quant_rows_pipe_kernel<DT, 2, false>>(want));
 #define XDNA_QP(G_)                                                                                        \
   if (nt) quant_rows_pipe_kernel<DT, G_, true><<<pg, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s); \
   else quant_rows_pipe_kernel<DT, G_, false><<<pg, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
-        if (gpl <= 1) {
-          XDNA_QP(1)
-        } else if (gpl <= 2) {
-          XDNA_QP(2)
-        } else {
-          XDNA_QP(4)
-        }
-#undef XDNA_QP
-        return launch_status("quant_rows");
+      if (gpl <= 1) {
+        XDNA_QP(1)
+      } else {
+        XDNA_QP(2)
       }
+#undef XDNA_QP
+      return launch_status("quant_rows");
     }
 #define XDNA_QW(G_)                                                                                     \
   if (nt) quant_rows_wave_kernel<DT, G_, true><<<grid, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s); \
   else quant_rows_wave_kernel<DT, G_, false><<<grid, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
     if (gpl <= 1) {
       XDNA_QW(1)
-    } else if (gpl <= 2) {
-      XDNA_QW(2)
     } else {
-      XDNA_QW(4)
+      XDNA_QW(2)
     }
 #undef XDNA_QW
     return launch_status("quant_rows");
