@@ -490,14 +490,14 @@ __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(const void* __re
 
 // Blocks of a persistent streaming kernel: as many as are resident at once (the runtime's occupancy
 // for 256 threads, cached per kernel and device), at most `rows`.
-template <auto KERNEL>
+template <auto KERNEL, int THREADS = 256>
 unsigned stream_blocks(int64_t rows) {
   static int per_cu[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   if (per_cu[dev] == 0) {
     int n = 0;
-    per_cu[dev] = (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, KERNEL, 256, 0) == hipSuccess && n > 0) ? n : 1;
+    per_cu[dev] = (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, KERNEL, THREADS, 0) == hipSuccess && n > 0) ? n : 1;
   }
   return (unsigned)std::max<int64_t>(1, std::min<int64_t>(rows, (int64_t)per_cu[dev] * device_cus()));
 }
@@ -615,40 +615,43 @@ __device__ __forceinline__ float image_amax(const float* __restrict__ parts, int
   return group_max<256>(m, red);
 }
 
-template <int DT>
-__global__ __launch_bounds__(256) void image_absmax_kernel(const void* __restrict__ x, int64_t per,
-                                                           float* __restrict__ parts) {
-  __shared__ float red[4];
+// Grid (parts, nb) of 1024-thread blocks (16 waves per CU at one block per CU), parts chosen by the launcher
+// so that the whole grid is one round of resident blocks (a second, partial round leaves most CUs idle:
+// 2048 blocks of 256 threads read 537 MB at 3.8 TB/s). Each lane keeps U 16-byte loads in flight per step
+// (a branch-free buffer resource over the image: past its end they read zeros; non-temporal under NT);
+// magnitude bits keep a NaN as torch.amax does.
+template <int DT, bool NT>
+__global__ __launch_bounds__(1024) void image_absmax_kernel(const void* __restrict__ x, int64_t per,
+                                                            float* __restrict__ parts) {
+  __shared__ float red[16];
   const int64_t b = blockIdx.y;
   constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
   const char* xb = reinterpret_cast<const char*>(x) + b * per * ESZ;
+  const int t = threadIdx.x;
   float m = 0.0f;
   const bool vec_ok = ((per * ESZ) % 16 == 0) && aligned(x, 16) && per * ESZ < (int64_t(1) << 31);
   if (vec_ok) {
-    // U 16-byte loads per lane in flight per step (a branch-free buffer resource over the image: past its
-    // end they read zeros); magnitude bits keep a NaN as torch.amax does
-    constexpr int U = 16;
+    constexpr int U = 8;
     using V = Vec16<DT>;
     const __amdgpu_buffer_rsrc_t r = make_rsrc(xb, (uint32_t)(per * ESZ));
-    const int64_t nvec = per * ESZ / 16;
+    // 32-bit: nvec < 2^27, so every offset below stays under 2^32
+    const uint32_t nvec = (uint32_t)(per * ESZ / 16);
+    const uint32_t step = gridDim.x * 1024u * U;
     AbsMaxBits<DT> am;
-    for (int64_t base = (int64_t)blockIdx.x * 256 * U + threadIdx.x; base < nvec; base += (int64_t)gridDim.x * 256 * U) {
+    for (uint32_t base = blockIdx.x * 1024u * U + t; base < nvec; base += step) {
       V u[U];
 #pragma unroll
-      for (int j = 0; j < U; ++j) {
-        const int64_t iv = base + j * 256;
-        u[j].raw = buf_load_u4(r, iv < nvec ? (uint32_t)(iv * 16) : OOB);
-      }
+      for (int j = 0; j < U; ++j) u[j].raw = buf_load_u4<NT>(r, (base + j * 1024u) * 16u);
 #pragma unroll
       for (int j = 0; j < U; ++j) am.add(u[j]);
     }
     m = bits_to_abs<DT>(am.lane_bits());
   } else {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < per; i += (int64_t)gridDim.x * 256)
+    for (int64_t i = (int64_t)blockIdx.x * 1024 + t; i < per; i += (int64_t)gridDim.x * 1024)
       m = fmaxf(m, fabsf(load_as_f32<DT>(xb, i)));
   }
-  m = group_max<256>(m, red);
-  if (threadIdx.x == 0) parts[b * AMAX_PARTS + blockIdx.x] = m;
+  m = group_max<1024>(m, red);
+  if (t == 0) parts[b * AMAX_PARTS + blockIdx.x] = m;
 }
 
 // Quantize + NCHW -> NHWC with 16-byte accesses on both sides: a block (256 threads) covers 256
@@ -658,7 +661,7 @@ __global__ __launch_bounds__(256) void image_absmax_kernel(const void* __restric
 // consecutive channels of PPL pixels, quantizes each pixel's 16 channels into one 16-byte LDS word of the
 // tile [TP][256] and the tile leaves as 16-byte stores, 256 contiguous channel bytes per pixel.
 // Channels past ch read as zeros (quantized 0); needs hw % PPL == 0 and an image below 2 GB.
-template <int DT>
+template <int DT, bool NT>
 __global__ __launch_bounds__(256) void conv_quant_nhwc_vec_kernel(const void* __restrict__ x, int64_t ch, int64_t hw,
                                                                   const float* __restrict__ parts, int nparts,
                                                                   int8_t* __restrict__ q, int64_t c_pad,
@@ -673,20 +676,22 @@ __global__ __launch_bounds__(256) void conv_quant_nhwc_vec_kernel(const void* __
   const int64_t b = blockIdx.z;
   const int64_t p0 = (int64_t)blockIdx.x * TP;
   const int64_t c0 = (int64_t)blockIdx.y * 256;
-  const float sc = scale_from_amax(image_amax(parts, b, nparts, red));
-  const float rc = 1.0f / sc;
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) sx[b] = sc;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int cl = 64 * wave + 16 * (lane >> 4);             // the lane's first channel within the tile
   const int pl = PPL * (lane & 15);                        // the lane's first pixel within the tile
   const __amdgpu_buffer_rsrc_t r = make_rsrc(reinterpret_cast<const char*>(x) + b * ch * hw * ESZ,
                                              (uint32_t)(ch * hw * ESZ));
+  // the tile's loads go out first: they do not depend on the image's scale, whose reduction (a load of
+  // the block maxima and a barrier) then overlaps them
   V v[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t c = c0 + cl + i;
-    v[i].raw = buf_load_u4(r, c < ch ? (uint32_t)((c * hw + p0 + pl) * ESZ) : OOB);
+    v[i].raw = buf_load_u4<NT>(r, c < ch ? (uint32_t)((c * hw + p0 + pl) * ESZ) : OOB);
   }
+  const float sc = scale_from_amax(image_amax(parts, b, nparts, red));
+  const float rc = 1.0f / sc;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) sx[b] = sc;
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
     float f[16];
@@ -1198,17 +1203,24 @@ int xdna_conv_quant_nhwc(const void* x, int x_dtype, int64_t nb, int64_t ch, int
   XDNA_REQUIRE(aligned(q, 16), "q must be 16-byte aligned");
   hipStream_t st = as_stream(stream);
   const int64_t hw = h * w, per = ch * hw;
-  const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(per, 256 * 16), AMAX_PARTS));
+  const int esz = x_dtype == XDNA_F32 ? 4 : 2;
+  // per-image max: at least 8 loads of 16 bytes per thread per block, and one round of resident blocks
+  const bool nt = nb * per * esz >= (int64_t(128) << 20);   // half the Infinity Cache
+  const int64_t resident = x_dtype == XDNA_F32 ? stream_blocks<image_absmax_kernel<XDNA_F32, false>, 1024>(INT64_MAX)
+                                               : stream_blocks<image_absmax_kernel<XDNA_BF16, false>, 1024>(INT64_MAX);
+  const int parts = (int)std::max<int64_t>(
+      1, std::min<int64_t>({cdiv(per * esz, 1024 * 8 * 16), (int64_t)AMAX_PARTS, std::max<int64_t>(1, resident / nb)}));
   dim3 g1((unsigned)parts, (unsigned)nb, 1);
   dim3 g2((unsigned)cdiv(hw, 64), (unsigned)cdiv(c_pad, 64), (unsigned)nb);
   XDNA_REQUIRE(cdiv(hw, 64) < (1ll << 31) && cdiv(c_pad, 64) < 65536, "image too large");
-  const int esz = x_dtype == XDNA_F32 ? 4 : 2;
   // the 16-byte path: pixel rows in whole 16-byte loads, an image's bytes addressable by one buffer resource
   const bool vec = hw % (16 / esz) == 0 && aligned(x, 16) && per * esz < (int64_t(1) << 31);
   const dim3 gv((unsigned)cdiv(hw, 16 * (16 / esz)), (unsigned)cdiv(c_pad, 256), (unsigned)nb);
 #define XDNA_CQ(DT)                                                                                        \
-  image_absmax_kernel<DT><<<g1, 256, 0, st>>>(x, per, amax_ws);                                             \
-  if (vec) conv_quant_nhwc_vec_kernel<DT><<<gv, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);     \
+  if (nt) image_absmax_kernel<DT, true><<<g1, 1024, 0, st>>>(x, per, amax_ws);                              \
+  else image_absmax_kernel<DT, false><<<g1, 1024, 0, st>>>(x, per, amax_ws);                                \
+  if (vec && nt) conv_quant_nhwc_vec_kernel<DT, true><<<gv, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx); \
+  else if (vec) conv_quant_nhwc_vec_kernel<DT, false><<<gv, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx); \
   else conv_quant_nhwc_kernel<DT><<<g2, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);
   switch (x_dtype) {
     case XDNA_F32: XDNA_CQ(XDNA_F32) break;
