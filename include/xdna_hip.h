@@ -84,6 +84,7 @@ extern "C" {
 #define XDNA_TILE_128x256W8 27
 #define XDNA_TILE_256x128W8 28
 #define XDNA_TILE_256x256PP 29  /* 256 x 256, 8 waves, ping-pong schedule (two groups of four waves) */
+#define XDNA_TILE_256x64 30     /* 256 x 64, 4 waves stacked along M (narrow outputs with many rows) */
 
 /* Library version (XDNA_ABI_VERSION). Replaces the import probe of kernels.available()
  * (torch_xdna/kernels.py:43-56): a loader checks it before trusting the other symbols. */

@@ -352,7 +352,7 @@ def tile_table():
 @pytest.mark.parametrize("tile", ["t256x256w8", "t256x256w4", "t256x128", "t128x256", "t128x128", "t64x64",
                                   "t192x256", "t256x192", "t64x32", "t32x64", "t32x32",
                                   "t64x64k2", "t64x64k4", "t32x64k4", "t32x32k4", "t128x128k2", "t128x256w8",
-                                  "t256x128w8", "t256x256pp"])
+                                  "t256x128w8", "t256x256pp", "t256x64"])
 def test_tiles_forced(gpu, tile, tile_table):
     """Each tile configuration of the engine, forced through the library's tile table: int32 and
     fused bf16 GEMMs with partial tiles and K both a multiple of 64 and not (for the K-group tiles:

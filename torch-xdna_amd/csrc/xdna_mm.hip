@@ -977,7 +977,7 @@ constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128
               T_192x256 = 12, T_256x192 = 13, T_64x32 = 14, T_32x64 = 15, T_32x32 = 16, T_GEMV4 = 17,
               T_GEMV2 = 18, T_GEMV8 = 19, T_SEG4R2 = 20, T_SEG4R4 = 21, T_64x64K2 = 22, T_64x64K4 = 23,
               T_32x64K4 = 24, T_32x32K4 = 25, T_128x128K2 = 26, T_128x256W8 = 27, T_256x128W8 = 28,
-              T_256x256PP = 29, T_COUNT = 30;
+              T_256x256PP = 29, T_256x64 = 30, T_COUNT = 31;
 
 static_assert(T_SMALL2 == T_SMALL1 + 1 && T_SMALL4 == T_SMALL1 + 2 && T_SMALL8 == T_SMALL1 + 3 &&
                   T_SMALL16 == T_SMALL1 + 4,
@@ -1008,6 +1008,7 @@ inline TileCfg tile_cfg(int t) {
     case T_128x256W8: return {128, 256, 8, 1};
     case T_256x128W8: return {256, 128, 8, 1};
     case T_256x256PP: return {256, 256, 8, 1};
+    case T_256x64: return {256, 64, 4, 1};
     default: return {64, 64, 4, 1};
   }
 }
@@ -1060,6 +1061,9 @@ int rule_tile(int64_t M, int64_t N, int64_t kbytes, bool small_ok) {
   if (small_ok && M <= 8 && kbytes >= 2048) return T_SEG4R2;
   if (small_ok && M <= 64) return (kbytes + 63) / 64 > 128 ? T_SMALL4 : T_SMALL2;
   const int64_t cus = device_cus();
+  // narrow outputs with rows for at least two rounds of 256 x 64 tiles (the VGG-16 224 x 224 convs): a
+  // quarter of the 64 x 64 tiles, each paying its fixed prologue / epilogue cost once for four times the work
+  if (N <= 64 && ((M + 255) / 256) * ((N + 63) / 64) >= 2 * cus) return T_256x64;
   if (M <= 64 || N <= 64) return T_64x64;
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
@@ -1141,6 +1145,8 @@ int launch_tiles_once(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw
     XDNA_TILE_W(128, 256, 2, 4, 4)
   } else if (t.waves == 8 && t.bn == 128) {
     XDNA_TILE_W(256, 128, 4, 2, 4)
+  } else if (t.bm == 256 && t.bn == 64) {
+    XDNA_TILE_W(256, 64, 4, 1, 4)
   } else if (t.bm == 256 && t.bn == 256 && t.waves == 8) {
     XDNA_TILE_W(256, 256, 2, 4, 3)
   } else if (t.bm == 256 && t.bn == 256) {

@@ -188,7 +188,7 @@ KINDS = {"i8": KIND_I8, "bf16": KIND_BF16, "conv": KIND_CONV}
 TILES = ("auto", "t256x256w8", "t256x256w4", "t256x128", "t128x256", "t128x128", "t64x64",
          "small_w1", "small_w2", "small_w4", "small_w8", "small_w16", "t192x256", "t256x192", "t64x32", "t32x64",
          "t32x32", "gemv_w4", "gemv_w2", "gemv_w8", "seg4_r2", "seg4_r4", "t64x64k2", "t64x64k4", "t32x64k4",
-         "t32x32k4", "t128x128k2", "t128x256w8", "t256x128w8", "t256x256pp")
+         "t32x32k4", "t128x128k2", "t128x256w8", "t256x128w8", "t256x256pp", "t256x64")
 TILE_ID = {name: i for i, name in enumerate(TILES)}
 
 
