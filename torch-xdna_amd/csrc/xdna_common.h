@@ -35,6 +35,7 @@ __host__ __device__ inline bool aligned(const void* p, int64_t a) { return (rein
 
 // ------------------------------------------------------------------------------ device types
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // float32 -> bfloat16 bits, round to nearest even (NaN stays a quiet NaN), the rounding torch's

@@ -785,7 +785,7 @@ __global__ __launch_bounds__(256) void conv_weight_pack_kernel(const void* __res
 // 64 w + 16 (l / 16) .. + 15 of pixels PPL (l % 16) .. + PPL (PPL 16-byte LDS reads) and writes, per
 // channel, PPL contiguous outputs as one 16-byte store: y = (float)q * (scale[o] * sx[b]) (+ bias[o]).
 // Needs hw % PPL == 0.
-template <int DT, bool RELU>
+template <int DT, bool RELU, bool NT>
 __global__ __launch_bounds__(256) void conv_dequant_vec_kernel(const void* __restrict__ qv, int64_t hw, int64_t co,
                                                                const float* __restrict__ scale,
                                                                const float* __restrict__ sx,
@@ -805,7 +805,7 @@ __global__ __launch_bounds__(256) void conv_dequant_vec_kernel(const void* __res
     const int64_t p = p0 + pix, c = c0 + part * 16;
     uint4 v = make_uint4(0, 0, 0, 0);
     if (co16) {
-      v = buf_load_u4(r, (p < hw && c < co) ? (uint32_t)(p * co + c) : OOB);
+      v = buf_load_u4<NT>(r, (p < hw && c < co) ? (uint32_t)(p * co + c) : OOB);
     } else if (p < hw) {        // rows not 16-byte aligned: bytes
       uint8_t by[16];
 #pragma unroll
@@ -840,15 +840,17 @@ __global__ __launch_bounds__(256) void conv_dequant_vec_kernel(const void* __res
     const int64_t p = p0 + pl;
     if (p >= hw) continue;
     char* out = reinterpret_cast<char*>(y) + ((b * co + o) * hw + p) * ESZ;
+    u32x4 word;
     if constexpr (DT == XDNA_F32) {
-      *reinterpret_cast<f32x4*>(out) = f32x4{v[0], v[1], v[2], v[3]};
+      word = __builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]});
     } else {
-      uint32_t h[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        h[e] = DT == XDNA_BF16 ? f32x2_to_bf16x2_bits(v[2 * e], v[2 * e + 1]) : f32x2_to_f16x2_bits(v[2 * e], v[2 * e + 1]);
-      *reinterpret_cast<uint4*>(out) = make_uint4(h[0], h[1], h[2], h[3]);
+        word[e] = DT == XDNA_BF16 ? f32x2_to_bf16x2_bits(v[2 * e], v[2 * e + 1]) : f32x2_to_f16x2_bits(v[2 * e], v[2 * e + 1]);
     }
+    // outputs above 128 MB (NT) do not fit the Infinity Cache: written past it
+    if constexpr (NT) __builtin_nontemporal_store(word, reinterpret_cast<u32x4*>(out));
+    else *reinterpret_cast<u32x4*>(out) = word;
   }
 }
 
@@ -1268,10 +1270,13 @@ int xdna_conv_dequant(const void* q, int relu, int64_t nb, int64_t h, int64_t w,
   const int esz = y_dtype == XDNA_F32 ? 4 : 2;
   // the 16-byte path: output rows in whole 16-byte stores, an image's int8 addressable by one resource
   const bool vec = hw % (16 / esz) == 0 && aligned(y, 16) && hw * co < (int64_t(1) << 31);
+  const bool nt = nb * hw * co * esz >= (int64_t(128) << 20);   // output above half the Infinity Cache
   const dim3 gv((unsigned)cdiv(hw, 16 * (16 / esz)), (unsigned)cdiv(co, 256), (unsigned)nb);
 #define XDNA_DQ(DT)                                                                                   \
-  if (vec && relu) conv_dequant_vec_kernel<DT, true><<<gv, 256, 0, st>>>(q, hw, co, scale, sx, bias, y); \
-  else if (vec) conv_dequant_vec_kernel<DT, false><<<gv, 256, 0, st>>>(q, hw, co, scale, sx, bias, y);   \
+  if (vec && relu && nt) conv_dequant_vec_kernel<DT, true, true><<<gv, 256, 0, st>>>(q, hw, co, scale, sx, bias, y); \
+  else if (vec && relu) conv_dequant_vec_kernel<DT, true, false><<<gv, 256, 0, st>>>(q, hw, co, scale, sx, bias, y); \
+  else if (vec && nt) conv_dequant_vec_kernel<DT, false, true><<<gv, 256, 0, st>>>(q, hw, co, scale, sx, bias, y); \
+  else if (vec) conv_dequant_vec_kernel<DT, false, false><<<gv, 256, 0, st>>>(q, hw, co, scale, sx, bias, y); \
   else if (relu) conv_dequant_kernel<DT, true><<<g, 256, 0, st>>>(q, hw, co, scale, sx, bias, y);       \
   else conv_dequant_kernel<DT, false><<<g, 256, 0, st>>>(q, hw, co, scale, sx, bias, y);
   switch (y_dtype) {
