@@ -70,6 +70,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="headline", choices=WORKLOADS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--operands", default="randn", choices=["randn", "zeros"],
+                    help="zeros: all-zero activations and weights on the GEMM workloads (a diagnostic of the power "
+                         "limit: the same work with the least switching; never the reported configuration)")
     ap.add_argument("--tile", default=None,
                     help="force this tile (a kernels.TILES name) on every GEMM shape of the c1/c2/c5/decode "
                          "workloads instead of the built-in rule and the tuned table (results do not depend on it)")
@@ -81,9 +84,10 @@ def gen(seed):
 
 
 # ------------------------------------------------------------------------------ GEMM workloads
-def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed=0):
+def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed=0, zeros=False):
     """Per set: for each (M, N, K): x [M, K] (0.1% outliers x20), quantized weight [N, K] + sw
-    (+ bias) on the GPU."""
+    (+ bias) on the GPU. zeros: x and the weight all zero (int8 operands all zero: the same work with
+    the least switching in the MFMA units, to separate the power limit from the schedule's own)."""
     g = gen(seed)
     per_set = sum(M * K * x_dtype.itemsize + N * K + M * N * 2 + M * K for M, N, K in shapes)
     nsets = max(nsets_min, -(-(MALL_BYTES + (64 << 20)) // per_set))
@@ -94,6 +98,9 @@ def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed
             x = torch.randn(M, K, generator=g)
             x = torch.where(torch.rand(M, K, generator=g) < 1e-3, x * 20, x).to(x_dtype).to(dev)
             w = (torch.randn(N, K, generator=g) * 0.02).to(dev)
+            if zeros:
+                x.zero_()
+                w.zero_()
             b = (torch.randn(N, generator=g) * 0.01).to(dev) if bias else None
             wq, sw = kernels.quant_rows(w)
             items.append((x, wq, sw, b, M, N, K))
@@ -224,7 +231,8 @@ def main():
     torch.cuda.set_device(dev)
     res = {"metric": METRIC, "unit": "TOPS", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
-           "data": "synthetic (seed 0, randn)"}
+           "data": "synthetic (seed 0, randn)" if a.operands == "randn" else
+                   "synthetic, all-zero GEMM operands (power-limit diagnostic, not the benchmark)"}
     bench = {"headline": bench_headline, "c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4,
              "c5": bench_c5, "decode": bench_decode, "quant": bench_quant, "bf16": bench_bf16, "vgg16": bench_vgg16,
              "stack": bench_stack, "copy": bench_copy, "libref": bench_libref}[a.workload]
@@ -376,7 +384,9 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
         for M, N, K in shapes:
             kernels.tile_set("i8", M, N, kernels.round_up(K, 16), a.tile)
         workload += f" (tile forced: {a.tile})"
-    sets = gemm_sets(shapes, dev, x_dtype=x_dtype, bias=bias)
+    if a.operands == "zeros":
+        workload += " (operands all zero: power-limit diagnostic)"
+    sets = gemm_sets(shapes, dev, x_dtype=x_dtype, bias=bias, zeros=a.operands == "zeros")
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(a.steps)]
     step = lambda i, t: run_gemm_step_split(sets[i % len(sets)], ev[i] if t else None)   # noqa: E731
     for i in range(a.warmup):
@@ -406,7 +416,8 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
            "config": {"workload": workload, "shapes_mnk": shapes, "x_dtype": str(x_dtype).replace("torch.", ""),
                       "bias": bias, "rotating_sets": len(sets)},
            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                        "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None if a.tile else traffic(label.lower()),
+                        "frac": round(achieved / PEAK_INT8_TOPS, 4),
+                        "traffic": None if a.tile or a.operands != "randn" else traffic(label.lower()),
                         "kernel": gemm_kernels(dev, shapes),
                         "launches": nshape * reps, "avg_launch_us": round(g_sec / (nshape * reps) * 1e6, 2),
                         "alg_bytes_per_launch": round(g_bytes / (nshape * reps)),
