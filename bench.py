@@ -626,25 +626,36 @@ def conv_op_record(a, dev, shape, sample_shape):
     layer = conv._layer(wt, h, w, True)
     if layer.device != "gpu" or layer.shift is None:
         raise SystemExit(f"conv {shape} did not run on the GPU: {layer.device}")
-    # the conv kernel alone, back to back on the op's own quantized inputs
+    # the op's conv launch alone (conv, requantize and dequantize to NCHW float32 in one kernel), back to
+    # back on the op's own quantized inputs
     wq, _ = layer.gpu_weights(dev)
-    xq_list = [kernels.conv_quant(x, layer.ci_pad)[0] for x in xs[:3]]
-    conv_us = back_to_back_us([lambda xq=xq: kernels.conv3x3(xq, wq, layer.shift, True) for xq in xq_list],
+    qs = [kernels.conv_quant(x, layer.ci_pad) for x in xs[:3]]
+    scale = layer.scale(dev)
+    conv_us = back_to_back_us([lambda xq=xq, sx=sx: kernels.conv3x3_dequant(xq, wq, layer.shift, True, scale, sx, None,
+                                                                            torch.float32) for xq, sx in qs],
+                              max(3, a.steps))
+    # and the conv with its requantize alone (NHWC int8 out), the engine's own figure
+    only_us = back_to_back_us([lambda xq=xq: kernels.conv3x3(xq, wq, layer.shift, True) for xq, _ in qs],
                               max(3, a.steps))
     ops_ = 2 * n * h * w * c * c * 9
     ach = ops_ / (conv_us / 1e6) / 1e12
-    conv_bytes = n * c * h * w * 2 + 9 * c * c + 4 * c
+    conv_bytes = n * c * h * w * (1 + 4) + 9 * c * c + 4 * c + 4 * n   # int8 in, float32 out, scales
     label = f"C4 conv3x3 {c}->{c} on {n}x{c}x{h}x{w}"
     rec = {"workload_key": f"C4 {n}x{c}x{h}x{w}", "value": round(ops_ / sec / 1e12, 2), "unit": "TOPS",
            "ms_per_step": round(sec * 1e3, 4), "host_ms_per_step": round(host * 1e3, 4),
            "config": {"workload": f"{label} + ReLU as the op xdna::conv3x3_fused: float32 NCHW in -> per-image "
                                   "quantize -> int8 implicit-GEMM conv (calibrated shift, round half up, uint8 "
-                                  "saturate) -> dequantize -> float32 NCHW out", "shift": layer.shift,
+                                  "saturate) -> dequantize -> float32 NCHW out (the last three in one launch)",
+                      "shift": layer.shift,
                       "plan": list(kernels.tile_plan(dev, "conv", n * h * w, c, 9 * layer.ci_pad)),
                       "rotating_inputs": nsets},
            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": traffic(f"c4_{n}x{c}x{h}x{w}"),
-                        "kernel": "mm_tile_kernel (conv, EPI_REQUANT)", "avg_launch_us": round(conv_us, 2),
+                        "kernel": "mm_tile_kernel (conv, EPI_REQUANT with the dequantize fused, NCHW float32 out)",
+                        "avg_launch_us": round(conv_us, 2),
+                        "conv_only": {"kernel": "mm_tile_kernel (conv, EPI_REQUANT, NHWC uint8 out)",
+                                      "avg_launch_us": round(only_us, 2),
+                                      "frac": round(ops_ / (only_us / 1e6) / 1e12 / PEAK_INT8_TOPS, 4)},
                         "alg_bytes_per_launch": conv_bytes,
                         "timing": "conv kernel launches back to back behind the gate and a pre-heat, events around them"}}
     if not a.no_cpu_baseline:

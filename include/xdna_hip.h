@@ -212,6 +212,15 @@ int xdna_conv_dequant(const void* q, int relu, int64_t nb, int64_t h, int64_t w,
                       const float* scale, const float* sx, const float* bias, void* y, int y_dtype,
                       void* stream);
 
+/* The conv, its requantize and the dequantize in one launch: what xdna_conv3x3_i8 followed by
+ * xdna_conv_dequant computes (the GPU form of conv3x3_int8's conv + dequant, torch_xdna/conv.py:47-51),
+ * bit for bit, without the NHWC integers in memory. x NHWC [nb, h, w, c_pad] int8, wq [co][9][c_pad],
+ * scale [co] (the weight scales), sx [nb] (the per-image input scales), bias [co] or NULL;
+ * y NCHW [nb, co, h, w] of y_dtype (XDNA_F32/BF16/F16), 16-byte aligned. 1 <= shift <= 31. */
+int xdna_conv3x3_dequant(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad, const int8_t* wq,
+                         int64_t co, int shift, int relu, const float* scale, const float* sx, const float* bias,
+                         void* y, int y_dtype, void* stream);
+
 /* Conv-to-conv chaining (the reference's "What is left", results/conv3x3_cascade.md:216-222): the
  * previous conv's NHWC output q [nb, h, w, co] (uint8 when relu) goes straight to the next conv's
  * NHWC int8 input xq_next [nb, h', w', c_pad_next] with its per-image scale sx_next [nb], computing

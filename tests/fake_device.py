@@ -100,6 +100,10 @@ def conv_dequant(q, relu, scale, sx, bias, out_dtype):
     return _to_torch(O.to_dtype(y, _NP_OF[out_dtype]), out_dtype)
 
 
+def conv3x3_dequant(xq, wq, shift, relu, scale, sx, bias, out_dtype):
+    return conv_dequant(conv3x3(xq, wq, shift, relu), relu, scale, sx, bias, out_dtype)
+
+
 def conv_requant_next(q, relu, pool, scale, sx, bias, x_dtype, c_pad_next, relu_y=False):
     y = O.to_dtype(O.conv_dequant(q.numpy().transpose(0, 3, 1, 2), scale.numpy(), sx.numpy(),
                                   None if bias is None else bias.float().numpy()), _NP_OF[x_dtype])
@@ -122,7 +126,7 @@ def nhwc_to_nchw(q):
 
 
 LAUNCHERS = ("quant_rows", "pad_k", "mm_i8", "mm_i8_dequant", "bf16_rows", "mm_bf16", "conv_weight_pack", "conv_quant", "conv3x3",
-             "conv3x3_calibrate", "conv_dequant", "conv_requant_next", "nchw_to_nhwc", "nhwc_to_nchw")
+             "conv3x3_calibrate", "conv_dequant", "conv3x3_dequant", "conv_requant_next", "nchw_to_nhwc", "nhwc_to_nchw")
 
 
 def install(monkeypatch):

@@ -183,6 +183,12 @@ def test_c4_large_conv(gpu, shape):
     assert torch.equal(got, want), f"{int((got != want).sum())} of {want.numel()} differ"
     wq_ref = ref.wq.numpy()
     _sampled_conv_check(xq_r, wq_ref, q.cpu().numpy(), shift, True, 500, seed=1)
+    # the op's fused conv + dequantize (one launch, the tail split included) against the two-launch form
+    scale = torch.from_numpy(O.conv_scale(sw.cpu().numpy(), shift)).to(gpu)
+    bias = (torch.randn(c, generator=_gen(23)) * 0.1).to(gpu)
+    y2 = kernels.conv_dequant(q, True, scale, sx, bias, torch.float32)
+    y1 = kernels.conv3x3_dequant(xq, wq, shift, True, scale, sx, bias, torch.float32)
+    assert torch.equal(y1, y2), f"{int((y1 != y2).sum())} of {y2.numel()} differ"
 
 
 # VGG16's thirteen 3x3 convs have these nine distinct (Ci, Co, H=W) shapes

@@ -257,6 +257,34 @@ def test_conv3x3(gpu, n, ci, co, h, w, relu):
     bias = _rand((co,), torch.float32, seed=5, scale=0.1)
     y = kernels.conv_dequant(q, relu, torch.from_numpy(scale).to(gpu), sx, bias.to(gpu), torch.float32)
     assert np.array_equal(_np(y), O.conv_dequant(want_q, scale, sx_r, bias.numpy()))
+    # the conv with the dequantize fused into its epilogue: the same floats without the integers in memory
+    y_fused = kernels.conv3x3_dequant(xq, wq, shift, relu, torch.from_numpy(scale).to(gpu), sx, bias.to(gpu),
+                                      torch.float32)
+    assert np.array_equal(_np(y_fused), O.conv_dequant(want_q, scale, sx_r, bias.numpy()))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("n,ci,co,h,w", [(2, 3, 48, 13, 37), (3, 40, 64, 9, 9), (2, 16, 20, 5, 7), (5, 16, 36, 1, 3),
+                                         (1, 64, 128, 16, 64), (1, 256, 256, 8, 64), (1, 32, 256, 64, 256)])
+def test_conv3x3_dequant_fused(gpu, dtype, n, ci, co, h, w):
+    """xdna_conv3x3_dequant against xdna_conv3x3_i8 + xdna_conv_dequant, bit for bit, in every output dtype,
+    with and without ReLU and bias: images whose pixel counts are not multiples of 4 (runs of four pixels
+    crossing images, one image of 3 pixels), channel counts off the tile widths, several images per launch."""
+    from torch_xdna import kernels
+
+    x, wt = _conv_case(n, ci, co, h, w, seed=n * 17 + ci + co + h * w)
+    c_pad = -(-ci // 16) * 16
+    xq, sx = kernels.conv_quant(x.to(gpu), c_pad)
+    wq, sw = kernels.conv_weight_pack(wt.to(gpu), c_pad)
+    for relu in (False, True):
+        shift = O.shift_from_top(float(kernels.conv3x3_calibrate(xq[:1], wq, relu)), relu)
+        scale = torch.from_numpy(O.conv_scale(sw.cpu().numpy(), shift)).to(gpu)
+        q = kernels.conv3x3(xq, wq, shift, relu)
+        for bias in (None, _rand((co,), torch.float32, seed=co, scale=0.1).to(gpu)):
+            want = kernels.conv_dequant(q, relu, scale, sx, bias, DT[dtype])
+            got = kernels.conv3x3_dequant(xq, wq, shift, relu, scale, sx, bias, DT[dtype])
+            assert got.shape == want.shape and got.dtype == want.dtype
+            assert torch.equal(got, want), f"{int((got != want).sum())} of {want.numel()} differ (relu {relu})"
 
 
 @pytest.mark.parametrize("relu", [False, True])
@@ -393,6 +421,11 @@ def test_tiles_forced(gpu, tile, tile_table):
         acc = c_oracle.conv3x3_acc(xq.numpy(), wq.numpy())
         q = kernels.conv3x3(x_nhwc, packed.to(gpu), 9, False)
         assert np.array_equal(_np(q).transpose(0, 3, 1, 2), O.requant(acc, 9, False)), (n, ci, co, h, w_)
+        scale = (torch.rand(co) + 0.5).to(gpu)
+        sx = (torch.rand(n) + 0.5).to(gpu)
+        want = kernels.conv_dequant(q, False, scale, sx, None, torch.float32)
+        assert torch.equal(kernels.conv3x3_dequant(x_nhwc, packed.to(gpu), 9, False, scale, sx, None, torch.float32),
+                           want), ("fused dequant", n, ci, co, h, w_)
         if n == 1:
             assert kernels.conv3x3_calibrate(x_nhwc, packed.to(gpu), False) == int(np.abs(acc).max())
 

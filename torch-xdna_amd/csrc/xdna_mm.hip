@@ -57,15 +57,19 @@ constexpr bool epi_dq(int e) { return e == EPI_DQ_F32 || e == EPI_DQ_BF16 || e =
 constexpr bool epi_bf(int e) { return e == EPI_BF_F32 || e == EPI_BF_BF16 || e == EPI_BF_F16; }
 
 struct EpiArgs {
-  void* out;            // int32 C, float y, or int8/uint8 q (NHWC)
+  void* out;            // int32 C, float y, or int8/uint8 q (NHWC); with dq_out float y (NCHW)
   int64_t ldo;          // elements between output rows
-  const float* sx;      // [M]
+  const float* sx;      // [M]; with dq_out per image [nb]
   const float* sw;      // [N]
   const float* bias;    // [N] or null
   int shift;            // EPI_REQUANT
   int relu;             // EPI_REQUANT / EPI_CALIB
   int32_t* acc_max;     // EPI_CALIB
   int vec_ok;           // output 16-byte aligned, row stride a multiple of 8 elements
+  int dq_out;           // EPI_REQUANT: 0 writes the integers (NHWC); XDNA_F32 / BF16 / F16 + 1: the
+                        // integers dequantized with sw = the conv's weight scales and sx = the per-image
+                        // scales (+ bias), written NCHW in that dtype (out, sx not shifted by launch rows)
+  int64_t px0;          // with dq_out: global pixel of the conv launch's first image
 };
 
 struct ConvGeom {
@@ -217,6 +221,68 @@ __device__ __forceinline__ void epilogue_w(const EpiArgs& e, int64_t m, int64_t 
           if (n + r < N) y[r] = (uint16_t)(h[r / 2] >> (16 * (r & 1)));
       }
     }
+  }
+}
+
+// Per element: an image boundary, an unaligned run, the end of the launch's rows.
+__device__ __forceinline__ void epilogue_rqdq_each(const EpiArgs& e, int64_t hw, int64_t b, int64_t p, int64_t m,
+                                                int64_t n, int64_t M, int64_t N, const float (&v)[4], float fo, float bo) {
+  const int dt = e.dq_out - 1;
+  const int esz = dt == XDNA_F32 ? 4 : 2;
+  for (int r = 0; r < 4; ++r) {
+    if (m + r >= M) return;
+    while (p >= hw) {                        // the next image (several when an image has fewer than 4 pixels)
+      p -= hw;
+      ++b;
+    }
+    float t = v[r] * (fo * e.sx[b]);
+    if (e.bias) t = t + bo;
+    char* o = reinterpret_cast<char*>(e.out) + ((b * N + n) * hw + p) * esz;
+    if (dt == XDNA_F32) *reinterpret_cast<float*>(o) = t;
+    else if (dt == XDNA_BF16) *reinterpret_cast<uint16_t*>(o) = f32_to_bf16_bits(t);
+    else *reinterpret_cast<uint16_t*>(o) = f32_to_f16_bits(t);
+    ++p;
+  }
+}
+
+// The conv's requantize fused with the op's dequantize: four consecutive output pixels m .. m+3 (launch
+// rows) of channel n, int32 sums in a[]. Each is requantized as EPI_REQUANT does, then dequantized as the
+// separate dequantize kernel does, y = (float)q * (scale[n] * sx[image]) (+ bias[n]), and stored NCHW in
+// dtype e.dq_out - 1: one 16-byte (float32) or 8-byte store when the four pixels lie in one image at an
+// aligned position, else per element.
+__device__ __forceinline__ void epilogue_rqdq(const EpiArgs& e, const ConvGeom& cg, int64_t m, int64_t n, int64_t M,
+                                              int64_t N, const int32_t (&a)[4], float fo, float bo) {
+  if (n >= N || m >= M) return;
+  const int64_t hw = cg.h * cg.w;
+  const int64_t gp = e.px0 + cg.m0 + m;  // global pixel of the first of the four
+  const int64_t b = gp / hw, p = gp - b * hw;
+  const int half = 1 << (e.shift - 1);
+  float v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    int q = (a[r] + half) >> e.shift;        // arithmetic shift: floor, i.e. round half up
+    q = e.relu ? min(max(q, 0), 255) : min(max(q, -128), 127);
+    v[r] = (float)q;
+  }
+  if (!(m + 3 < M && p + 3 < hw && (p % 4) == 0 && hw % 4 == 0)) {
+    epilogue_rqdq_each(e, hw, b, p, m, n, M, N, v, fo, bo);
+    return;
+  }
+  const int dt = e.dq_out - 1;
+  const float f = fo * e.sx[b];
+  float t[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    t[r] = v[r] * f;
+    if (e.bias) t[r] = t[r] + bo;
+  }
+  char* o = reinterpret_cast<char*>(e.out) + ((b * N + n) * hw + p) * (dt == XDNA_F32 ? 4 : 2);
+  if (dt == XDNA_F32) {
+    *reinterpret_cast<f32x4*>(o) = f32x4{t[0], t[1], t[2], t[3]};
+  } else if (dt == XDNA_BF16) {
+    *reinterpret_cast<uint2*>(o) = make_uint2(f32x2_to_bf16x2_bits(t[0], t[1]), f32x2_to_bf16x2_bits(t[2], t[3]));
+  } else {
+    *reinterpret_cast<uint2*>(o) = make_uint2(f32x2_to_f16x2_bits(t[0], t[1]), f32x2_to_f16x2_bits(t[2], t[3]));
   }
 }
 
@@ -672,6 +738,16 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
   const bool full = m0 + BM <= M && n0 + BN <= N && (EPI == EPI_CALIB || e.vec_ok);
   const int rsub = lane >> 3;            // read-back: row rr * 8 + rsub, columns CW * (lane & 7) ..
   const int cq = lane & 7;
+  // the conv's fused dequantize (EPI_REQUANT with e.dq_out, uniform): the staged block (32 pixels x COLS
+  // channels) is read back transposed, eight lanes per channel with four consecutive pixels each, so every
+  // store instruction writes whole 128-byte runs of eight channels of the NCHW output
+  constexpr int COLS = 32 * CB;          // staged columns per block
+  // not for three column blocks per wave (256 x 192): that epilogue would outgrow full unrolling, and the
+  // launcher runs such launches with another tile
+  constexpr bool RQDQ = EPI == EPI_REQUANT && FN != 3;
+  const bool rqdq = RQDQ && e.dq_out != 0;
+  const int dquad = lane & 7;            // the lane's four pixels: 4 * dquad .. + 3 of the block
+  const int dch = lane >> 3;             // the lane's channel within each group of eight
 #pragma unroll
   for (int jp = 0; jp < FN / CB; ++jp) {
     const int64_t n = n0 + wn * TN + jp * 32 * CB + cq * CW;
@@ -686,19 +762,38 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
               i32x4{c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
         }
       }
+      if (rqdq) {
+        if constexpr (RQDQ) {
+          // a rolled loop: it indexes only LDS and addresses, and unrolled (with every tile's blocks) the
+          // epilogue would outgrow full unrolling of the accumulator loops
+#pragma unroll 1
+          for (int g8 = 0; g8 < COLS / 8; ++g8) {
+            const int col = 8 * g8 + dch;
+            const int64_t nd = n0 + wn * TN + jp * COLS + col;
+            const int64_t nc = min(nd, N - 1);
+            const float fo = e.sw[nc];
+            const float bo = e.bias ? e.bias[nc] : 0.0f;
+            int32_t a4[4];
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int row = rr * 8 + rsub;
-        int32_t v[CW];
-#pragma unroll
-        for (int q = 0; q < CB; ++q) {
-          const i32x4 t = *reinterpret_cast<const i32x4*>(stg + row * PITCH + cq * CW * 4 + q * 16);
-          v[4 * q] = t[0], v[4 * q + 1] = t[1], v[4 * q + 2] = t[2], v[4 * q + 3] = t[3];
+            for (int r = 0; r < 4; ++r) a4[r] = *reinterpret_cast<const int32_t*>(stg + (4 * dquad + r) * PITCH + col * 4);
+            epilogue_rqdq(e, cg, m0 + wm * TM + i * 32 + 4 * dquad, nd, M, N, a4, fo, bo);
+          }
         }
-        const int64_t m = m0 + wm * TM + i * 32 + row;
-        const float sxm = sx_pre[DQ ? i * 4 + rr : 0];
-        if (full) epilogue_w<EPI, true, CW>(e, m, n, M, N, v, calib, cols_pre[jp], sxm);
-        else epilogue_w<EPI, false, CW>(e, m, n, M, N, v, calib, cols_pre[jp], sxm);
+      } else {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int row = rr * 8 + rsub;
+          int32_t v[CW];
+#pragma unroll
+          for (int q = 0; q < CB; ++q) {
+            const i32x4 t = *reinterpret_cast<const i32x4*>(stg + row * PITCH + cq * CW * 4 + q * 16);
+            v[4 * q] = t[0], v[4 * q + 1] = t[1], v[4 * q + 2] = t[2], v[4 * q + 3] = t[3];
+          }
+          const int64_t m = m0 + wm * TM + i * 32 + row;
+          const float sxm = sx_pre[DQ ? i * 4 + rr : 0];
+          if (full) epilogue_w<EPI, true, CW>(e, m, n, M, N, v, calib, cols_pre[jp], sxm);
+          else epilogue_w<EPI, false, CW>(e, m, n, M, N, v, calib, cols_pre[jp], sxm);
+        }
       }
     }
   }
@@ -1109,6 +1204,7 @@ constexpr int out_bytes() {
 template <int CONVM, int EPI>
 int launch_tiles_once(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                       ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
+  if (e.dq_out && tile == T_256x192) tile = T_256x256W8;   // no fused dequantize in that tile (same results)
   const TileCfg t = tile_cfg(tile);
   const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   if (tiles >= (1ll << 31)) {
@@ -1229,7 +1325,8 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
   const int8_t* at = a;
   if constexpr (CONVM != 0) ct.m0 += m1;
   else at += m1 * lda;
-  const EpiArgs et = shift_epi(e, out_bytes<EPI>(), m1, 0);
+  // the conv's NCHW dequantized output is addressed by the pixel offset in its geometry (ct.m0)
+  const EpiArgs et = (CONVM != 0 && e.dq_out) ? e : shift_epi(e, out_bytes<EPI>(), m1, 0);
   // the tail's tile may split K over groups: CONVM 1 needs c_pad to be a multiple of its groups' slices
   if constexpr (CONVM != 0) {
     if (cg.c_pad % (64 * tile_cfg(p.tail).kg) != 0)
@@ -1351,7 +1448,9 @@ int launch_conv(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad
   ConvGeom cg{h, w, c_pad};
   for (int64_t b0 = 0; b0 < nb; b0 += imgs) {
     const int64_t bc = std::min(imgs, nb - b0);
-    const EpiArgs eb = shift_epi(e, 1, b0 * h * w, 0);
+    EpiArgs eb = e;
+    if (e.dq_out) eb.px0 = e.px0 + b0 * h * w;   // NCHW output: addressed by global pixel, not by row
+    else eb = shift_epi(e, 1, b0 * h * w, 0);
     const int8_t* xb = x + b0 * per_img;
     // the running tap counters of CONVM 1 step by KG slices of 64 channels
     int rc = (c_pad % (64 * tile_cfg(tile).kg) == 0)
@@ -1452,6 +1551,31 @@ int xdna_conv3x3_i8(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c
   e.shift = shift;
   e.vec_ok = (co % 8 == 0) && aligned(y, 16);
   return launch_conv<EPI_REQUANT>(x, nb, h, w, c_pad, wq, co, e, st);
+}
+
+int xdna_conv3x3_dequant(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad, const int8_t* wq,
+                         int64_t co, int shift, int relu, const float* scale, const float* sx, const float* bias,
+                         void* y, int y_dtype, void* stream) {
+  XDNA_REQUIRE(nb >= 0 && h >= 1 && w >= 1 && co >= 1, "bad sizes");
+  XDNA_REQUIRE(c_pad >= 16 && c_pad % 16 == 0, "c_pad must be a positive multiple of 16");
+  XDNA_REQUIRE(y_dtype == XDNA_F32 || y_dtype == XDNA_BF16 || y_dtype == XDNA_F16,
+               "y_dtype must be XDNA_F32, XDNA_BF16 or XDNA_F16");
+  if (nb == 0) return XDNA_OK;
+  XDNA_REQUIRE(x && wq && aligned(x, 16) && aligned(wq, 16), "operands must be 16-byte aligned device pointers");
+  XDNA_REQUIRE(scale && sx && y, "null pointer");
+  XDNA_REQUIRE(shift >= 1 && shift <= 31, "shift must be in [1, 31]");
+  XDNA_REQUIRE(aligned(y, 16), "y must be 16-byte aligned");
+  EpiArgs e{};
+  e.out = y;
+  e.ldo = co;
+  e.shift = shift;
+  e.relu = relu ? 1 : 0;
+  e.sw = scale;
+  e.sx = sx;
+  e.bias = bias;
+  e.dq_out = y_dtype + 1;
+  e.px0 = 0;
+  return launch_conv<EPI_REQUANT>(x, nb, h, w, c_pad, wq, co, e, as_stream(stream));
 }
 
 int xdna_tile_set(int kind, int64_t m, int64_t n, int64_t k, int tile) {

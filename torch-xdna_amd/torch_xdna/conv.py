@@ -252,9 +252,14 @@ def conv3x3_fused(cfg, x, weight, bias, relu):
                 if layer.device is None:
                     _first_call(cfg, layer, lambda v: layer.gpu_nhwc(xq, verify=v), None, on_gpu)
                 if layer.device == "gpu":
-                    q = layer.gpu_nhwc(xq, verify=cfg.verify == "always")
                     b = None if bias is None else bias.to(x.device, torch.float32).contiguous()
-                    y = kernels.conv_dequant(q, relu, layer.scale(x.device), sx, b, x.dtype)
+                    if cfg.verify == "always":     # the integers are checked, so they go through memory
+                        q = layer.gpu_nhwc(xq, verify=True)
+                        y = kernels.conv_dequant(q, relu, layer.scale(x.device), sx, b, x.dtype)
+                    else:                          # conv, requantize and dequantize in one launch
+                        wq, _ = layer.gpu_weights(x.device)
+                        y = kernels.conv3x3_dequant(xq, wq, layer.shift, relu, layer.scale(x.device), sx, b, x.dtype)
+                        stats.launches += 1
                     device = "gpu"
             except Exception as e:
                 _failed(layer, e)
@@ -335,8 +340,14 @@ def _gpu_chain(cfg, x, layers, biases, relu_after, pools):
                 _first_call(cfg, L, lambda v, L=L, xq=xq: L.gpu_nhwc(xq, verify=v), None, True)
             if L.device != "gpu":
                 return None
-            q = L.gpu_nhwc(xq, verify=cfg.verify == "always")
             b = None if biases[i] is None else biases[i].to(dev, torch.float32).contiguous()
+            if i == last and cfg.verify != "always":   # the last conv with its dequantize in one launch
+                wq, _ = L.gpu_weights(dev)
+                y = kernels.conv3x3_dequant(xq, wq, L.shift, L.relu, L.scale(dev), sx, b, x.dtype)
+                stats.launches += 1
+                done += 1
+                continue
+            q = L.gpu_nhwc(xq, verify=cfg.verify == "always")
             if i < last:
                 xq, sx = kernels.conv_requant_next(q, L.relu, pools[i], L.scale(dev), sx, b, x.dtype,
                                                    layers[i + 1].ci_pad, relu_y=relu_after[i])

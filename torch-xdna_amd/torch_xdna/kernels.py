@@ -102,6 +102,7 @@ def _declare(L):
         "xdna_conv_weight_pack": ([p, i, i64, i64, p, i64, p, p], i),
         "xdna_conv3x3_i8": ([p, i64, i64, i64, i64, p, i64, i, i, p, p, p], i),
         "xdna_conv_dequant": ([p, i, i64, i64, i64, i64, p, p, p, p, i, p], i),
+        "xdna_conv3x3_dequant": ([p, i64, i64, i64, i64, p, i64, i, i, p, p, p, p, i, p], i),
         "xdna_conv_requant_next": ([p, i, i, i, i64, i64, i64, i64, p, p, p, i, p, i64, p, p, p], i),
         "xdna_nchw_to_nhwc_i8": ([p, i64, i64, i64, i64, p, i64, p], i),
         "xdna_nhwc_to_nchw_i8": ([p, i64, i64, i64, i64, p, p], i),
@@ -123,7 +124,8 @@ def _declare(L):
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
            "xdna_gemm_i8_dequant", "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc",
            "xdna_conv_quant_nhwc_noalloc", "xdna_conv_weight_pack",
-           "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8", "xdna_nhwc_to_nchw_i8",
+           "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv3x3_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8",
+           "xdna_nhwc_to_nchw_i8",
            "xdna_tile_set", "xdna_tile_get", "xdna_tile_plan", "xdna_tile_clear", "xdna_rmsnorm_bf16", "xdna_qk_norm_rope",
            "xdna_attention_bf16", "xdna_silu_mul_bf16", "xdna_add_f32")
 
@@ -453,6 +455,22 @@ def conv_dequant(q, relu, scale, sx, bias, out_dtype):
         with _on(dev):
             _check(lib().xdna_conv_dequant(_ptr(q), int(bool(relu)), n, h, w, co, _ptr(scale), _ptr(sx), _ptr(bias),
                                            _ptr(y), _DTYPE_CODE[out_dtype], _stream(dev)), "conv_dequant")
+    return y
+
+
+def conv3x3_dequant(xq, wq, shift, relu, scale, sx, bias, out_dtype):
+    """conv3x3 followed by conv_dequant in one launch, bit for bit: NHWC int8 xq [N, H, W, c_pad] (*) wq
+    [Co, 9, c_pad], requantized by `shift`, dequantized with scale [Co] and sx [N] (+ bias [Co]) ->
+    NCHW y [N, Co, H, W] as out_dtype."""
+    dev = _need_gpu(xq, wq, scale, sx, bias)
+    n, h, w, c_pad = xq.shape
+    co = wq.shape[0]
+    y = torch.empty((n, co, h, w), dtype=out_dtype, device=dev)
+    if n:
+        with _on(dev):
+            _check(lib().xdna_conv3x3_dequant(_ptr(xq), n, h, w, c_pad, _ptr(wq), co, int(shift), int(bool(relu)),
+                                              _ptr(scale), _ptr(sx), _ptr(bias), _ptr(y), _DTYPE_CODE[out_dtype],
+                                              _stream(dev)), "conv3x3_dequant")
     return y
 
 
