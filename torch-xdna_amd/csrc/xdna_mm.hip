@@ -856,6 +856,17 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
       if (u + 1 < U) mfma(wv[u + 1], av[u + 1], acc1);
     }
   };
+  // the epilogue's operands (wave 0 runs it) go out ahead of the K loop where the 9 registers they hold
+  // through it cost no occupancy (up to 4 waves; 8 and 16 waves load them after the loop)
+  constexpr bool PRE = WAVES <= 4;
+  const int64_t mrow = m0 + (lane & 15);
+  EpiCols<EPI> cols;
+  float sxm = 0.0f;
+  auto load_epi = [&]() {
+    cols = EpiCols<EPI>(e, n0 + 4 * (lane >> 4), N);
+    if constexpr (epi_dq(EPI)) sxm = e.sx[min(mrow, M - 1)];
+  };
+  if constexpr (PRE) load_epi();
   i32x4 w0[U], a0[U], w1[U], a1[U];
   load(kbeg, w0, a0);
   for (int64_t kb = kbeg; kb < kend; kb += 2 * U * 64) {
@@ -872,10 +883,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
 #pragma unroll
   for (int v = 1; v < WAVES; ++v) acc += red[v][lane];
   int calib = 0;
-  const EpiCols<EPI> cols(e, n0 + 4 * (lane >> 4), N);
-  const int64_t mrow = m0 + (lane & 15);
-  float sxm = 0.0f;
-  if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16) sxm = mrow < M ? e.sx[mrow] : 0.0f;
+  if constexpr (!PRE) load_epi();
   epilogue4<EPI>(e, mrow, n0 + 4 * (lane >> 4), M, N, __builtin_bit_cast(i32x4, acc), calib, cols, sxm);
   calib_flush<EPI>(e, calib);
 }
@@ -889,24 +897,43 @@ __global__ __launch_bounds__(WAVES * 64) void mm_small_kernel(const int8_t* __re
 // load is one contiguous KB of one row and every activation byte is loaded once per wave, where the
 // 16-row layout of mm_small_kernel spends a mostly-empty activation load per weight load. A wave owns
 // one output column; KS steps (KS KB of K) are loaded before their MFMAs, longer K in rounds.
+// The scale and bias operands of one output element (row m, column n), loaded by the kernel ahead of its
+// K loop so that their latency hides under the weight stream instead of following it. m and n must be
+// in range (callers clamp them).
+template <int EPI>
+struct Epi1Ops {
+  float sx = 0.0f, sw = 0.0f, b = 0.0f;
+  __device__ __forceinline__ Epi1Ops() {}
+  __device__ __forceinline__ Epi1Ops(const EpiArgs& e, int64_t m, int64_t n) {
+    if constexpr (epi_dq(EPI)) {
+      sx = e.sx[m];
+      sw = e.sw[n];
+    }
+    if constexpr (epi_dq(EPI) || epi_bf(EPI)) {
+      if (e.bias) b = e.bias[n];
+    }
+  }
+};
+
 // One output element (row m, column n) of a GEMM epilogue, with the arithmetic of epilogue_w.
 template <int EPI, typename T>
-__device__ __forceinline__ void epilogue1(const EpiArgs& e, int64_t m, int64_t n, T v) {
+__device__ __forceinline__ void epilogue1(const EpiArgs& e, int64_t m, int64_t n, T v, const Epi1Ops<EPI>& o) {
   static_assert(EPI != EPI_REQUANT && EPI != EPI_CALIB, "GEMM epilogues only");
   const int64_t off = m * e.ldo + n;
   if constexpr (EPI == EPI_I32) {
     reinterpret_cast<int32_t*>(e.out)[off] = v;
   } else {
-    // ((float)acc * sx) * sw (+ bias), or the float sum (+ bias)
+    // ((float)acc * sx) * sw (+ bias), or the float sum (+ bias); no bias adds nothing (not +0.0,
+    // which would turn a -0.0 into +0.0)
     float t;
     if constexpr (epi_bf(EPI)) {
       t = v;
     } else {
       t = (float)v;
-      t = t * e.sx[m];
-      t = t * e.sw[n];
+      t = t * o.sx;
+      t = t * o.sw;
     }
-    if (e.bias) t = t + e.bias[n];
+    if (e.bias) t = t + o.b;
     if constexpr (EPI == EPI_DQ_F32 || EPI == EPI_BF_F32) reinterpret_cast<float*>(e.out)[off] = t;
     else if constexpr (EPI == EPI_DQ_BF16 || EPI == EPI_BF_BF16) reinterpret_cast<uint16_t*>(e.out)[off] = f32_to_bf16_bits(t);
     else reinterpret_cast<uint16_t*>(e.out)[off] = f32_to_f16_bits(t);
@@ -929,6 +956,7 @@ __global__ __launch_bounds__(W * 64) void mm_gemv_kernel(const int8_t* __restric
     if constexpr (BFE) c = mfma16x16x32bf(w_, a_, c);
     else c = mfma16x16x64(w_, a_, c);
   };
+  const Epi1Ops<EPI> ops(e, 0, n);
   Acc4 acc0 = {}, acc1 = {};
   for (int64_t kc = 0; kc < K; kc += KS * 1024) {
     i32x4 wv[KS], xv[KS];
@@ -958,7 +986,7 @@ __global__ __launch_bounds__(W * 64) void mm_gemv_kernel(const int8_t* __restric
   T v = (i >> 2) == (lane >> 4) ? d : T(0);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  if (lane == 0) epilogue1<EPI>(e, 0, n, v);
+  if (lane == 0) epilogue1<EPI>(e, 0, n, v, ops);
 }
 
 // ------------------------------------------------------------------------------ a few rows (M <= 16)
@@ -1005,6 +1033,17 @@ __global__ __launch_bounds__(W * 64) void mm_seg4_kernel(const int8_t* __restric
     if constexpr (BFE) c = mfma16x16x32bf(w_, a_, c);
     else c = mfma16x16x64(w_, a_, c);
   };
+  // the epilogue's operands for this lane's outputs (row 4 q + rsub, column n0 + 4 r + lane / 16) go out
+  // ahead of the K loop where the 3 R XG registers they hold through it cost no occupancy
+  constexpr bool PRE = R * XG <= 2;
+  Epi1Ops<EPI> ops[PRE ? R : 1][PRE ? XG : 1];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < XG; ++q)
+        ops[r][q] = Epi1Ops<EPI>(e, min<int64_t>(4 * q + rsub, M - 1), min<int64_t>(n0 + 4 * r + (lane >> 4), N - 1));
+  }
   Acc4 acc[R][XG];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -1057,7 +1096,10 @@ __global__ __launch_bounds__(W * 64) void mm_seg4_kernel(const int8_t* __restric
       for (int u = 1; u < W; ++u) v += red[u][r][q][lane];
       const int64_t m = 4 * q + rsub;
       const int64_t n = n0 + 4 * r + (lane >> 4);
-      if (m < M && n < N) epilogue1<EPI>(e, m, n, v);
+      if (m < M && n < N) {
+        if constexpr (PRE) epilogue1<EPI>(e, m, n, v, ops[r][q]);
+        else epilogue1<EPI>(e, m, n, v, Epi1Ops<EPI>(e, m, n));
+      }
     }
 }
 
