@@ -145,6 +145,26 @@ int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const in
                          const float* sw, const float* bias, void* y, int y_dtype, int64_t ldy,
                          int64_t m, int64_t n, int64_t k, void* stream);
 
+/* xdna_gemm_i8_i32 and xdna_gemm_i8_dequant with a workspace, for shapes whose tiles (up to 64 x 64)
+ * would leave most of the GPU idle (decode-sized M against N of a few thousand, short-M GEMMs): the
+ * workgroups of a tile split its K, each stores its int32 partial sums in ws, and the last to finish
+ * adds the others' and runs the epilogue. Results are identical to the calls without a workspace
+ * (integer sums are exact in any order); the replaced reference interfaces are theirs
+ * (torch_xdna/kernels.py:172-192 and torch_xdna/runtime.py:350-353 / :429-432 / :370-374).
+ * ws: 256-byte aligned device memory whose first XDNA_GEMM_WS_COUNTER_BYTES are zero before its first
+ * use (every call leaves them zero); the rest is overwritten. A launch splits only where ws_bytes
+ * holds its split, so any size (or NULL) is valid; xdna_gemm_ws_bytes(m, n, k) gives the size that
+ * allows every split a call of that shape makes (0: it makes none). Calls that share a workspace must
+ * be ordered (one stream): concurrent calls on one workspace race. */
+#define XDNA_GEMM_WS_COUNTER_BYTES 65536
+int64_t xdna_gemm_ws_bytes(int64_t m, int64_t n, int64_t k);
+int xdna_gemm_i8_i32_ws(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int32_t* c,
+                        int64_t ldc, int64_t m, int64_t n, int64_t k, void* ws, int64_t ws_bytes,
+                        void* stream);
+int xdna_gemm_i8_dequant_ws(const int8_t* a, int64_t lda, const float* sx, const int8_t* w, int64_t ldw,
+                            const float* sw, const float* bias, void* y, int y_dtype, int64_t ldy,
+                            int64_t m, int64_t n, int64_t k, void* ws, int64_t ws_bytes, void* stream);
+
 /* The bf16 GEMM of precision "bf16": y[m, n] = sum_k a[m, k] * w[n, k] with bf16 operands and float32
  * accumulation (+ bias[n] in float32), converted to y_dtype (XDNA_F32/BF16/F16, round to nearest
  * even). Replaces kernels.mm_bf16 (torch_xdna/kernels.py:167-169) behind runtime._npu_bf16 /

@@ -13,7 +13,7 @@ HEADER = os.path.join(ROOT, "include", "xdna_hip.h")
 
 def declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(xdna_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(xdna_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -56,6 +56,15 @@ def test_argument_validation(lib):
     assert "multiple of 16" in lib.xdna_last_error().decode()
     assert lib.xdna_gemm_i8_dequant(p, 16, p, p, 16, p, None, p, 7, 16, 4, 4, 16, None) == -1
     assert "y_dtype" in lib.xdna_last_error().decode()
+    # the workspace forms: the same checks, and a workspace that is not 256-byte aligned
+    assert lib.xdna_gemm_i8_i32_ws(p, 16, p, 16, p, 16, 4, 4, 15, None, 0, None) == -1
+    assert "multiple of 16" in lib.xdna_last_error().decode()
+    assert lib.xdna_gemm_i8_i32_ws(p, 16, p, 16, p, 16, 4, 4, 16, ctypes.c_void_p(272), 4096, None) == -1
+    assert "256-byte" in lib.xdna_last_error().decode()
+    assert lib.xdna_gemm_i8_dequant_ws(p, 16, p, p, 16, p, None, p, 7, 16, 4, 4, 16, None, 0, None) == -1
+    assert lib.xdna_gemm_i8_dequant_ws(p, 16, p, p, 16, p, None, p, 0, 16, 4, 4, 16, p, -1, None) == -1
+    assert lib.xdna_gemm_ws_bytes(4, 4, 15) == -1
+    assert "bad sizes" in lib.xdna_last_error().decode()
     assert lib.xdna_quant_rows(p, 9, 4, 16, 16, p, 16, 16, p, None) == -1
     assert lib.xdna_quant_rows(p, 0, 4, 16, 8, p, 16, 16, p, None) == -1          # ld_x < k
     assert lib.xdna_conv3x3_i8(p, 1, 4, 4, 15, p, 8, 3, 0, p, None, None) == -1    # c_pad % 16

@@ -430,6 +430,76 @@ def test_tiles_forced(gpu, tile, tile_table):
             assert kernels.conv3x3_calibrate(x_nhwc, packed.to(gpu), False) == int(np.abs(acc).max())
 
 
+def _ksplit(cus, bm, bn, kg, tiles, k):
+    """Workgroups per tile along K that the library gives a launch: 1 above 64 x 64 or when the tiles fill
+    more than half of the CUs, else up to CUs / tiles, at most 16, with at least 16 slices of 64 per K
+    group (used here only to check that the test's shapes reach the split)."""
+    if bm * bn > 64 * 64 or 2 * tiles > cus:
+        return 1
+    nk = -(-k // 64)
+    ks = min(cus // tiles, nk // (16 * kg), 16)
+    if ks < 2:
+        return 1
+    per = -(-nk // ks)
+    return -(-nk // per)
+
+
+KSPLIT_TILES = {"t32x32": (32, 32, 1), "t32x64": (32, 64, 1), "t64x32": (64, 32, 1), "t64x64": (64, 64, 1),
+                "t64x64k2": (64, 64, 2), "t64x64k4": (64, 64, 4), "t32x64k4": (32, 64, 4), "t32x32k4": (32, 32, 4)}
+
+
+@pytest.mark.parametrize("tile", sorted(KSPLIT_TILES))
+def test_gemm_ksplit(gpu, tile, tile_table):
+    """The K split across workgroups (xdna_gemm_i8_i32_ws / xdna_gemm_i8_dequant_ws): shapes whose tiles
+    leave most of the CUs idle, K in whole and partial 64-byte slices and splits of unequal length, ragged
+    M and N. The int32 sums against the oracle; the workspace calls equal the calls without a workspace for
+    the int32 sums and the fused dequant to every dtype with and without bias; a workspace that holds only
+    the counters (no split) gives the same; calls follow each other on one workspace, whose counters are
+    zero again after them."""
+    from torch_xdna import kernels
+
+    L = kernels.lib()
+    cus = kernels.num_cus(gpu)
+    bm, bn, kg = KSPLIT_TILES[tile]
+    st = kernels._stream(gpu)
+    split_seen = False
+    for m, n, k in [(16, 1000, 4160), (3, 200, 14336), (40, 130, 4112), (5, 260, 14352), (64, 64, 1040),
+                    (100, 520, 3072)]:
+        kernels.tile_set("i8", m, n, k, tile)
+        assert kernels.tile_get(gpu, "i8", m, n, k) == tile
+        assert L.xdna_gemm_ws_bytes(m, n, k) > 0
+        split_seen |= _ksplit(cus, bm, bn, kg, -(-m // bm) * -(-n // bn), k) > 1
+        a, w = _i8((m, k), seed=m + k), _i8((n, k), seed=n + 2 * k)
+        ag, wg = a.to(gpu), w.to(gpu)
+        acc = c_oracle.gemm_i32(a.numpy(), w.numpy())
+        c = kernels.mm_i8(ag, wg)
+        assert np.array_equal(_np(c), acc), (tile, m, n, k)
+        c0 = torch.empty_like(c)
+        assert L.xdna_gemm_i8_i32(kernels._ptr(ag), k, kernels._ptr(wg), k, kernels._ptr(c0), n, m, n, k, st) == 0
+        assert torch.equal(c0, c), (tile, m, n, k)
+        ws = torch.zeros(65536, dtype=torch.uint8, device=gpu)           # the counters only: no split
+        c1 = torch.empty_like(c)
+        assert L.xdna_gemm_i8_i32_ws(kernels._ptr(ag), k, kernels._ptr(wg), k, kernels._ptr(c1), n, m, n, k,
+                                     kernels._ptr(ws), ws.numel(), st) == 0
+        assert torch.equal(c1, c), (tile, m, n, k)
+        sx, sw = (torch.rand(m) + 0.01).to(gpu), (torch.rand(n) + 0.01).to(gpu)
+        b = torch.randn(n).to(gpu)
+        for out in ("f32", "bf16", "f16"):
+            for bias in (b, None):
+                y = kernels.mm_i8_dequant(ag, sx, wg, sw, bias, DT[out])
+                y0 = torch.empty_like(y)
+                assert L.xdna_gemm_i8_dequant(kernels._ptr(ag), k, kernels._ptr(sx), kernels._ptr(wg), k,
+                                              kernels._ptr(sw), kernels._ptr(bias), kernels._ptr(y0),
+                                              kernels._DTYPE_CODE[DT[out]], n, m, n, k, st) == 0
+                assert torch.equal(y, y0), (tile, m, n, k, out, bias is None)
+        want = O.to_bf16(O.dequant(acc, sx.cpu().numpy(), sw.cpu().numpy(), b.cpu().numpy()))
+        assert np.array_equal(_f32(kernels.mm_i8_dequant(ag, sx, wg, sw, b, torch.bfloat16)), want), (tile, m, n, k)
+    assert split_seen, f"no shape of the test splits K with {tile}"
+    torch.cuda.synchronize()
+    for buf in kernels._ws_buf.values():
+        assert int(buf[:65536].view(torch.int32).abs().sum()) == 0, "arrival counters not back to zero"
+
+
 @pytest.mark.parametrize("tile", ["t256x256w8", "t256x128w8", "t128x256", "t256x256pp"])
 def test_tiles_tail_split(gpu, tile, tile_table):
     """A one-workgroup-per-CU tile whose last round of tiles would fill at most half of the CUs runs the

@@ -70,6 +70,13 @@ struct EpiArgs {
                         // integers dequantized with sw = the conv's weight scales and sx = the per-image
                         // scales (+ bias), written NCHW in that dtype (out, sx not shifted by launch rows)
   int64_t px0;          // with dq_out: global pixel of the conv launch's first image
+  // K split across workgroups (int8 GEMM tiles of at most 64 x 64): grid.y workgroups share a tile, each
+  // summing a contiguous range of its K slices; ksplit <= 1 or part == null: no split
+  int ksplit;
+  uint32_t* cnt;        // [tiles * waves] arrival counters, zero before the launch (reset by the last arrival)
+  int32_t* part;        // [tiles * waves][ksplit][the wave's int32 accumulators in register order]
+  void* ws;             // host side: the caller's workspace (counters, then partial sums), or null
+  int64_t ws_bytes;
 };
 
 struct ConvGeom {
@@ -498,7 +505,18 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
     ow[j] = n < N ? (uint32_t)(n * ldw + cw[j] * 16) : OOB;
   }
 
-  const int64_t nk = (K + BK - 1) / BK;
+  // The cross-workgroup K split (int8 GEMM tiles of at most 64 x 64): workgroup blockIdx.y of the tile
+  // sums slices [kbase, kbase + nk) of its nk_all
+  constexpr bool CAN_SPLIT = CONVM == 0 && !PP && (EPI == EPI_I32 || epi_dq(EPI)) && BM * BN <= 64 * 64;
+  const int64_t nk_all = (K + BK - 1) / BK;
+  int64_t kbase = 0, nk = nk_all;
+  if constexpr (CAN_SPLIT) {
+    if (e.ksplit > 1) {
+      const int64_t per = (nk_all + e.ksplit - 1) / e.ksplit;
+      kbase = (int64_t)blockIdx.y * per;
+      nk = max<int64_t>(0, min(nk_all, kbase + per) - kbase);
+    }
+  }
   // CONVM 1: a group's slices are issued in order, KG slices apart, so the tap and channel offset of
   // its next slice are kept as running counters instead of being divided out of k (the launcher takes
   // CONVM 1 with KG > 1 only when c_pad is a multiple of KG * 64, so each step wraps at most once).
@@ -510,7 +528,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
   (void)dtap;
   (void)dc0;
   auto dma_slice = [&](int64_t kt, int8_t* stage) {
-    const int64_t k0 = kt * BK;
+    const int64_t k0 = (kbase + kt) * BK;
     const bool live = kt < nk;           // uniform; dead slices read zeros without memory traffic
     int8_t* sa = stage;
     int8_t* sw = stage + BM * BK;
@@ -550,7 +568,8 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
       } else {
 #pragma unroll
         for (int j = 0; j < IA; ++j) {
-          const bool ok = oa[j] != OOB && k0 + ca[j] * 16 < K;
+          // live: with a K split, a slice past this workgroup's range still lies inside K
+          const bool ok = live && oa[j] != OOB && k0 + ca[j] * 16 < K;
           dma16(ra_rsrc, ok ? oa[j] + (uint32_t)k0 : OOB, sa + ((wave * IA + j) << 10));
         }
       }
@@ -562,7 +581,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
     } else {
 #pragma unroll
       for (int j = 0; j < IW; ++j) {
-        const bool ok = ow[j] != OOB && k0 + cw[j] * 16 < K;
+        const bool ok = live && ow[j] != OOB && k0 + cw[j] * 16 < K;
         dma16(rw_rsrc, ok ? ow[j] + (uint32_t)k0 : OOB, sw + ((wave * IW + j) << 10));
       }
     }
@@ -730,6 +749,52 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
 #pragma unroll
             for (int q = 0; q < 4; ++q) acc[j][i][4 * g + q] += t[q];
           }
+    }
+  }
+  if constexpr (CAN_SPLIT) {
+    if (e.ksplit > 1) {
+      // Every wave (of group 0) stores its partial sums; the wave that arrives last for its (tile, wave)
+      // slot adds the others' and runs the epilogue. The workgroups of a tile may run on different XCDs,
+      // whose L2 caches are not coherent with each other: the partials go out as agent-scope atomic
+      // stores and come back as agent-scope atomic loads, which are coherent across XCDs by themselves,
+      // and the arrival count is an agent-scope atomic issued after every partial store has completed
+      // (vmcnt 0). Fences would write back and invalidate the whole L2 of the XCD instead, for every
+      // wave. Integer sums are exact in any order: the result does not depend on which wave is last.
+      constexpr int WORDS = FN * FM * 16;                   // int32 accumulators per lane
+      const int64_t slot = (int64_t)blockIdx.x * NW + wave;
+      const int ks = (int)blockIdx.y;
+      int32_t* const base = e.part + slot * e.ksplit * WORDS * 64;
+      {
+        int32_t* mine = base + ks * WORDS * 64;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            const i32x16 c = __builtin_bit_cast(i32x16, acc[j][i]);
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              __hip_atomic_store(mine + ((j * FM + i) * 16 + r) * 64 + lane, c[r], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+          }
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      uint32_t prev = 0;
+      if (lane == 0) prev = __hip_atomic_fetch_add(e.cnt + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      prev = (uint32_t)__builtin_amdgcn_readfirstlane((int)prev);
+      if (prev + 1 < (uint32_t)e.ksplit) return;          // wave-uniform; no barrier follows
+      for (int u = 0; u < e.ksplit; ++u) {
+        if (u == ks) continue;
+        const int32_t* p = base + u * WORDS * 64;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              acc[j][i][r] += __hip_atomic_load(p + ((j * FM + i) * 16 + r) * 64 + lane, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (lane == 0) __hip_atomic_store(e.cnt + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
     }
   }
   int8_t* stg = lds + wave * 32 * PITCH;     // group 0: lds == lds_all
@@ -1243,10 +1308,33 @@ constexpr int out_bytes() {
                                                                                                : 1;
 }
 
+// The cross-workgroup K split of the int8 GEMM tiles up to 64 x 64 (the kernel's CAN_SPLIT). A launch
+// whose tiles would leave more than half of the CUs idle gives each tile up to CUs / tiles workgroups
+// along K (at most 16, each with at least 16 slices of 64 per K group: measured, shorter splits cost
+// more in partial sums than they gain, e.g. 128 x 1024 x 3072 in 32 x 32 tiles with 4 K groups takes
+// 5.7 us unsplit and 6.3 us in two splits of 6 slices per group); 1: no split. Its workspace is
+// WS_CNT_BYTES of arrival counters (a launch uses tiles x waves of them) and then the partial sums,
+// tiles x bm x bn int32 per split.
+constexpr int64_t WS_CNT_BYTES = XDNA_GEMM_WS_COUNTER_BYTES;
+
+int ksplit_for(const TileCfg& t, int64_t tiles, int64_t K) {
+  const int64_t cus = device_cus();
+  if (t.bm * t.bn > 64 * 64 || 2 * tiles > cus || tiles * t.waves * 4 > WS_CNT_BYTES) return 1;
+  const int64_t nk = (K + 63) / 64;
+  const int64_t ks = std::min<int64_t>({cus / tiles, nk / (16 * t.kg), 16});
+  if (ks < 2) return 1;
+  const int64_t per = (nk + ks - 1) / ks;
+  return (int)((nk + per - 1) / per);     // no split without slices
+}
+
+int64_t split_ws_bytes(const TileCfg& t, int64_t tiles, int ks) {
+  return ks > 1 ? WS_CNT_BYTES + tiles * t.bm * t.bn * 4 * ks : 0;
+}
+
 template <int CONVM, int EPI>
 int launch_tiles_once(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
-                      ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
-  if (e.dq_out && tile == T_256x192) tile = T_256x256W8;   // no fused dequantize in that tile (same results)
+                      ConvGeom cg, const EpiArgs& e_in, int tile, hipStream_t st) {
+  if (e_in.dq_out && tile == T_256x192) tile = T_256x256W8;   // no fused dequantize in that tile (same results)
   const TileCfg t = tile_cfg(tile);
   const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   if (tiles >= (1ll << 31)) {
@@ -1254,6 +1342,18 @@ int launch_tiles_once(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw
     return XDNA_EINVAL;
   }
   dim3 grid((unsigned)tiles, 1, 1);
+  EpiArgs e = e_in;
+  e.ksplit = 1;
+  if constexpr (CONVM == 0 && (EPI == EPI_I32 || epi_dq(EPI))) {
+    // split only where the caller's workspace holds it (else the same sums in one workgroup per tile)
+    const int ks = e.ws ? ksplit_for(t, tiles, K) : 1;
+    if (ks > 1 && split_ws_bytes(t, tiles, ks) <= e.ws_bytes) {
+      e.ksplit = ks;
+      e.cnt = static_cast<uint32_t*>(e.ws);
+      e.part = reinterpret_cast<int32_t*>(static_cast<char*>(e.ws) + WS_CNT_BYTES);
+      grid.y = (unsigned)ks;
+    }
+  }
   const bool kfull = K % 64 == 0;
   // LDS stages per tile shape, from a measured sweep of 3 / 4 / 5 (and 4 / 8 / 12 for 64 x 64): 3 for
   // the large tiles (96 KB at 256 x 256; 48 KB at 128 x 128, three workgroups per CU), 4 for 64 x 64
@@ -1511,30 +1611,39 @@ using namespace xdna;
 
 extern "C" {
 
-int xdna_gemm_i8_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int32_t* c, int64_t ldc, int64_t m,
-                     int64_t n, int64_t k, void* stream) {
+int xdna_gemm_i8_i32_ws(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int32_t* c, int64_t ldc,
+                        int64_t m, int64_t n, int64_t k, void* ws, int64_t ws_bytes, void* stream) {
   XDNA_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative size");
   if (m == 0 || n == 0) return XDNA_OK;
   XDNA_REQUIRE(k % 16 == 0 && k >= 16, "k must be a positive multiple of 16 (pad with xdna_pad_rows_i8)");
   XDNA_REQUIRE(lda >= k && ldw >= k && lda % 16 == 0 && ldw % 16 == 0 && ldc >= n, "bad leading dimensions");
   XDNA_REQUIRE(a && w && c && aligned(a, 16) && aligned(w, 16), "operands must be 16-byte aligned device pointers");
+  XDNA_REQUIRE(ws_bytes >= 0 && (ws == nullptr || aligned(ws, 256)), "workspace must be 256-byte aligned");
   EpiArgs e{};
   e.out = c;
   e.ldo = ldc;
   e.vec_ok = (ldc % 8 == 0) && aligned(c, 16);
+  e.ws = ws;
+  e.ws_bytes = ws ? ws_bytes : 0;
   const int tile = choose_tile(XDNA_KIND_I8, m, n, k, k);
   return launch_gemm<EPI_I32>(a, lda, w, ldw, m, n, k, e, tile, as_stream(stream));
 }
 
-int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const int8_t* w, int64_t ldw, const float* sw,
-                         const float* bias, void* y, int y_dtype, int64_t ldy, int64_t m, int64_t n, int64_t k,
-                         void* stream) {
+int xdna_gemm_i8_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int32_t* c, int64_t ldc, int64_t m,
+                     int64_t n, int64_t k, void* stream) {
+  return xdna_gemm_i8_i32_ws(a, lda, w, ldw, c, ldc, m, n, k, nullptr, 0, stream);
+}
+
+int xdna_gemm_i8_dequant_ws(const int8_t* a, int64_t lda, const float* sx, const int8_t* w, int64_t ldw,
+                            const float* sw, const float* bias, void* y, int y_dtype, int64_t ldy, int64_t m,
+                            int64_t n, int64_t k, void* ws, int64_t ws_bytes, void* stream) {
   XDNA_REQUIRE(y_dtype == XDNA_F32 || y_dtype == XDNA_BF16 || y_dtype == XDNA_F16, "y_dtype must be F32/BF16/F16");
   XDNA_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative size");
   if (m == 0 || n == 0) return XDNA_OK;
   XDNA_REQUIRE(k % 16 == 0 && k >= 16, "k must be a positive multiple of 16 (pad with xdna_pad_rows_i8)");
   XDNA_REQUIRE(lda >= k && ldw >= k && lda % 16 == 0 && ldw % 16 == 0 && ldy >= n, "bad leading dimensions");
   XDNA_REQUIRE(a && w && y && sx && sw && aligned(a, 16) && aligned(w, 16), "bad pointers");
+  XDNA_REQUIRE(ws_bytes >= 0 && (ws == nullptr || aligned(ws, 256)), "workspace must be 256-byte aligned");
   EpiArgs e{};
   e.out = y;
   e.ldo = ldy;
@@ -1542,11 +1651,19 @@ int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const in
   e.sw = sw;
   e.bias = bias;
   e.vec_ok = (ldy % 8 == 0) && aligned(y, 16);
+  e.ws = ws;
+  e.ws_bytes = ws ? ws_bytes : 0;
   hipStream_t st = as_stream(stream);
   const int tile = choose_tile(XDNA_KIND_I8, m, n, k, k);
   if (y_dtype == XDNA_F32) return launch_gemm<EPI_DQ_F32>(a, lda, w, ldw, m, n, k, e, tile, st);
   if (y_dtype == XDNA_BF16) return launch_gemm<EPI_DQ_BF16>(a, lda, w, ldw, m, n, k, e, tile, st);
   return launch_gemm<EPI_DQ_F16>(a, lda, w, ldw, m, n, k, e, tile, st);
+}
+
+int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const int8_t* w, int64_t ldw, const float* sw,
+                         const float* bias, void* y, int y_dtype, int64_t ldy, int64_t m, int64_t n, int64_t k,
+                         void* stream) {
+  return xdna_gemm_i8_dequant_ws(a, lda, sx, w, ldw, sw, bias, y, y_dtype, ldy, m, n, k, nullptr, 0, stream);
 }
 
 int xdna_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const float* bias, void* y, int y_dtype,
@@ -1663,6 +1780,22 @@ int xdna_tile_plan(int kind, int64_t m, int64_t n, int64_t k, int* head, int64_t
   *m1 = p.m1;
   *tail = p.tail;
   return XDNA_OK;
+}
+
+int64_t xdna_gemm_ws_bytes(int64_t m, int64_t n, int64_t k) {
+  XDNA_REQUIRE(m >= 1 && n >= 1 && k >= 16 && k % 16 == 0, "bad sizes");
+  int head = 0, tail = 0;
+  int64_t m1 = 0;
+  if (xdna_tile_plan(XDNA_KIND_I8, m, n, k, &head, &m1, &tail) != XDNA_OK) return -1;
+  if (is_small(head) || is_gemv(head) || is_seg4(head)) return 0;
+  auto can_split = [](int tile) {
+    const TileCfg t = tile_cfg(tile);
+    return t.bm * t.bn <= 64 * 64;
+  };
+  if (!can_split(head) && !(m1 > 0 && can_split(tail))) return 0;
+  // a split launch has at most as many workgroups as CUs (tiles x splits <= CUs), each holding at most a
+  // 64 x 64 int32 tile of partial sums: one bound for every launch of the call
+  return WS_CNT_BYTES + device_cus() * 64 * 64 * 4;
 }
 
 int xdna_tile_clear(void) {

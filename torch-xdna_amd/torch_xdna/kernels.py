@@ -95,6 +95,9 @@ def _declare(L):
         "xdna_quant_rows": ([p, i, i64, i64, i64, p, i64, i64, p, p], i),
         "xdna_gemm_i8_i32": ([p, i64, p, i64, p, i64, i64, i64, i64, p], i),
         "xdna_gemm_i8_dequant": ([p, i64, p, p, i64, p, p, p, i, i64, i64, i64, i64, p], i),
+        "xdna_gemm_ws_bytes": ([i64, i64, i64], i64),
+        "xdna_gemm_i8_i32_ws": ([p, i64, p, i64, p, i64, i64, i64, i64, p, i64, p], i),
+        "xdna_gemm_i8_dequant_ws": ([p, i64, p, p, i64, p, p, p, i, i64, i64, i64, i64, p, i64, p], i),
         "xdna_gemm_bf16": ([p, i64, p, i64, p, p, i, i64, i64, i64, i64, p], i),
         "xdna_pad_rows_i8": ([p, i64, i64, i64, p, i64, i64, p], i),
         "xdna_conv_quant_nhwc": ([p, i, i64, i64, i64, i64, p, i64, p, p, p], i),
@@ -122,7 +125,8 @@ def _declare(L):
 
 
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
-           "xdna_gemm_i8_dequant", "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc",
+           "xdna_gemm_i8_dequant", "xdna_gemm_ws_bytes", "xdna_gemm_i8_i32_ws", "xdna_gemm_i8_dequant_ws",
+           "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc",
            "xdna_conv_quant_nhwc_noalloc", "xdna_conv_weight_pack",
            "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv3x3_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8",
            "xdna_nhwc_to_nchw_i8",
@@ -198,6 +202,7 @@ def tile_set(kind, M, N, K, tile):
     """Make every later launch of exactly (kind, M, N, K) use `tile` (a TILES name; "auto" removes the
     entry). For convs M = n*h*w, N = Co, K = 9*Ci_pad. Results do not depend on the tile."""
     _check(lib().xdna_tile_set(KINDS.get(kind, kind), M, N, K, TILE_ID[tile]), "tile_set")
+    _ws_need.clear()
 
 
 def tile_get(dev, kind, M, N, K) -> str:
@@ -212,6 +217,7 @@ def tile_get(dev, kind, M, N, K) -> str:
 
 def tile_clear():
     _check(lib().xdna_tile_clear(), "tile_clear")
+    _ws_need.clear()
 
 
 def tile_plan(dev, kind, M, N, K):
@@ -324,6 +330,36 @@ def pad_k(xq, k_pad):
     return out
 
 
+# The int8 GEMMs' K-split workspace (xdna_gemm_*_ws): the bytes a shape's plan can use, per device (they
+# follow the tile table, so tile_set / tile_clear forget them), and one buffer per device and stream whose
+# counter bytes are zero from its allocation on (each call leaves them zero). Under graph capture the
+# GEMMs run without a workspace (no split; the same results), so no captured graph holds one.
+_ws_need = {}
+_ws_buf = {}
+
+
+def _gemm_ws(dev, M, N, K):
+    """(pointer, bytes) of the workspace for an int8 GEMM of M x N x K on dev's current stream, or
+    (None, 0) when its plan splits nothing."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, M, N, K)
+    need = _ws_need.get(key)
+    if need is None:
+        with _on(dev):
+            need = lib().xdna_gemm_ws_bytes(M, N, K)
+        if need < 0:
+            _check(need, "gemm_ws_bytes")
+        _ws_need[key] = need
+    if need == 0 or torch.cuda.is_current_stream_capturing():
+        return None, 0
+    skey = (idx, torch._C._cuda_getCurrentRawStream(idx))
+    buf = _ws_buf.get(skey)
+    if buf is None or buf.numel() < need:
+        buf = torch.zeros(need, dtype=torch.uint8, device=torch.device("cuda", idx))
+        _ws_buf[skey] = buf
+    return _ptr(buf), buf.numel()
+
+
 def mm_i8(a, w, out=None):
     """c [M, N] int32 = a [M, Kp] @ w [N, Kp]^T, int8 operands with 16-byte aligned rows, Kp % 16 == 0
     (the role of the reference's kernels.mm_i8, without its padding rules)."""
@@ -335,8 +371,9 @@ def mm_i8(a, w, out=None):
     c = torch.empty((M, N), dtype=torch.int32, device=dev) if out is None else out
     if M and N:
         with _on(dev):
-            _check(lib().xdna_gemm_i8_i32(_ptr(a), a.stride(0), _ptr(w), w.stride(0), _ptr(c), c.stride(0), M, N, K,
-                                          _stream(dev)), "gemm_i8_i32")
+            ws, wsb = _gemm_ws(dev, M, N, K)
+            _check(lib().xdna_gemm_i8_i32_ws(_ptr(a), a.stride(0), _ptr(w), w.stride(0), _ptr(c), c.stride(0), M, N,
+                                             K, ws, wsb, _stream(dev)), "gemm_i8_i32")
     return c
 
 
@@ -350,9 +387,10 @@ def mm_i8_dequant(a, sx, w, sw, bias, out_dtype):
     y = torch.empty((M, N), dtype=out_dtype, device=dev)
     if M and N:
         with _on(dev):
-            _check(lib().xdna_gemm_i8_dequant(_ptr(a), a.stride(0), _ptr(sx), _ptr(w), w.stride(0), _ptr(sw),
-                                              _ptr(bias), _ptr(y), _DTYPE_CODE[out_dtype], y.stride(0), M, N, K,
-                                              _stream(dev)), "gemm_i8_dequant")
+            ws, wsb = _gemm_ws(dev, M, N, K)
+            _check(lib().xdna_gemm_i8_dequant_ws(_ptr(a), a.stride(0), _ptr(sx), _ptr(w), w.stride(0), _ptr(sw),
+                                                 _ptr(bias), _ptr(y), _DTYPE_CODE[out_dtype], y.stride(0), M, N, K,
+                                                 ws, wsb, _stream(dev)), "gemm_i8_dequant")
     return y
 
 
