@@ -158,6 +158,10 @@ int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const in
  * be ordered (one stream): concurrent calls on one workspace race. */
 #define XDNA_GEMM_WS_COUNTER_BYTES 65536
 int64_t xdna_gemm_ws_bytes(int64_t m, int64_t n, int64_t k);
+/* The K split of a call's launches with a workspace of xdna_gemm_ws_bytes (for the first row chunk:
+ * *head_ks for rows [0, m1) of xdna_tile_plan, *tail_ks for the tail; 1: no split). Part of the launch
+ * plan a per-kernel-variant verify cache keys on (the reference's `_verified` key, runtime.py:207). */
+int xdna_gemm_ksplit(int64_t m, int64_t n, int64_t k, int* head_ks, int* tail_ks);
 int xdna_gemm_i8_i32_ws(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int32_t* c,
                         int64_t ldc, int64_t m, int64_t n, int64_t k, void* ws, int64_t ws_bytes,
                         void* stream);

@@ -468,7 +468,10 @@ def test_gemm_ksplit(gpu, tile, tile_table):
         kernels.tile_set("i8", m, n, k, tile)
         assert kernels.tile_get(gpu, "i8", m, n, k) == tile
         assert L.xdna_gemm_ws_bytes(m, n, k) > 0
-        split_seen |= _ksplit(cus, bm, bn, kg, -(-m // bm) * -(-n // bn), k) > 1
+        ks = _ksplit(cus, bm, bn, kg, -(-m // bm) * -(-n // bn), k)
+        split_seen |= ks > 1
+        # the launch plan (the verify cache's key) names the split
+        assert kernels.gemm_variant(gpu, m, n, k) == (tile if ks == 1 else f"{tile}/k{ks}"), (tile, m, n, k)
         a, w = _i8((m, k), seed=m + k), _i8((n, k), seed=n + 2 * k)
         ag, wg = a.to(gpu), w.to(gpu)
         acc = c_oracle.gemm_i32(a.numpy(), w.numpy())

@@ -1798,6 +1798,26 @@ int64_t xdna_gemm_ws_bytes(int64_t m, int64_t n, int64_t k) {
   return WS_CNT_BYTES + device_cus() * 64 * 64 * 4;
 }
 
+int xdna_gemm_ksplit(int64_t m, int64_t n, int64_t k, int* head_ks, int* tail_ks) {
+  XDNA_REQUIRE(head_ks && tail_ks, "null output pointer");
+  *head_ks = *tail_ks = 1;
+  int head = 0, tail = 0;
+  int64_t m1 = 0;
+  const int rc = xdna_tile_plan(XDNA_KIND_I8, m, n, k, &head, &m1, &tail);
+  if (rc != XDNA_OK) return rc;
+  if (is_small(head) || is_gemv(head) || is_seg4(head)) return XDNA_OK;
+  // the first row and column chunk's launches, as launch_gemm / launch_tiles make them (dense rows)
+  const int64_t mc = std::min(m, std::max<int64_t>(256, (MAX_BUF / k) / 256 * 256));
+  const int64_t nc = std::min(n, std::max<int64_t>(256, (MAX_BUF / k) / 256 * 256));
+  auto ks_of = [&](int tile, int64_t rows) {
+    const TileCfg t = tile_cfg(tile);
+    return ksplit_for(t, ((rows + t.bm - 1) / t.bm) * ((nc + t.bn - 1) / t.bn), k);
+  };
+  *head_ks = ks_of(head, m1 ? m1 : mc);
+  if (m1) *tail_ks = ks_of(tail, mc - m1);
+  return XDNA_OK;
+}
+
 int xdna_tile_clear(void) {
   std::lock_guard<std::mutex> lock(g_tile_mu);
   g_tiles.clear();

@@ -96,6 +96,7 @@ def _declare(L):
         "xdna_gemm_i8_i32": ([p, i64, p, i64, p, i64, i64, i64, i64, p], i),
         "xdna_gemm_i8_dequant": ([p, i64, p, p, i64, p, p, p, i, i64, i64, i64, i64, p], i),
         "xdna_gemm_ws_bytes": ([i64, i64, i64], i64),
+        "xdna_gemm_ksplit": ([i64, i64, i64, p, p], i),
         "xdna_gemm_i8_i32_ws": ([p, i64, p, i64, p, i64, i64, i64, i64, p, i64, p], i),
         "xdna_gemm_i8_dequant_ws": ([p, i64, p, p, i64, p, p, p, i, i64, i64, i64, i64, p, i64, p], i),
         "xdna_gemm_bf16": ([p, i64, p, i64, p, p, i, i64, i64, i64, i64, p], i),
@@ -125,7 +126,7 @@ def _declare(L):
 
 
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
-           "xdna_gemm_i8_dequant", "xdna_gemm_ws_bytes", "xdna_gemm_i8_i32_ws", "xdna_gemm_i8_dequant_ws",
+           "xdna_gemm_i8_dequant", "xdna_gemm_ws_bytes", "xdna_gemm_ksplit", "xdna_gemm_i8_i32_ws", "xdna_gemm_i8_dequant_ws",
            "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc",
            "xdna_conv_quant_nhwc_noalloc", "xdna_conv_weight_pack",
            "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv3x3_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8",
@@ -231,10 +232,19 @@ def tile_plan(dev, kind, M, N, K):
 
 
 def gemm_variant(dev, M, N, K, kind=KIND_I8) -> str:
-    """The kernels a GEMM of M x N x K runs (the library's plan): the head tile, and after a tail split
-    "+<tail tile>@<first tail row>". One NPU-program key of the reference (runtime.py:207)
-    corresponds to one (variant, N, K) here."""
+    """The kernels a GEMM of M x N x K runs (the library's plan): the head tile, after a tail split
+    "+<tail tile>@<first tail row>", and for an int8 launch that splits K across workgroups "/k<splits>"
+    after its tile. One NPU-program key of the reference (runtime.py:207) corresponds to one
+    (variant, N, K) here."""
     head, m1, tail = tile_plan(dev, kind, M, N, K)
+    hk = tk = 1
+    if kind == KIND_I8 and K % 16 == 0 and K >= 16:
+        a, b = ctypes.c_int(), ctypes.c_int()
+        with _on(dev):
+            _check(lib().xdna_gemm_ksplit(M, N, K, ctypes.byref(a), ctypes.byref(b)), "gemm_ksplit")
+        hk, tk = a.value, b.value
+    head = head if hk == 1 else f"{head}/k{hk}"
+    tail = tail if tk == 1 else f"{tail}/k{tk}"
     return head if m1 == 0 else f"{head}+{tail}@{m1}"
 
 
