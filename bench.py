@@ -386,7 +386,8 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
         workload += f" (tile forced: {a.tile})"
     if a.operands == "zeros":
         workload += " (operands all zero: power-limit diagnostic)"
-    sets = gemm_sets(shapes, dev, x_dtype=x_dtype, bias=bias, zeros=a.operands == "zeros")
+    # at least three distinct sets, together beyond the Infinity Cache (the measurement protocol)
+    sets = gemm_sets(shapes, dev, 3, x_dtype=x_dtype, bias=bias, zeros=a.operands == "zeros")
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(a.steps)]
     step = lambda i, t: run_gemm_step_split(sets[i % len(sets)], ev[i] if t else None)   # noqa: E731
     for i in range(a.warmup):
@@ -616,7 +617,7 @@ def conv_op_record(a, dev, shape, sample_shape):
     n, c, h, w = shape
     cid = ops.config_id(Config(policy="gpu", verify="off"))
     xs = []
-    nsets = max(2, -(-(MALL_BYTES + (64 << 20)) // (n * c * h * w * 9)))   # float in + int8 + float out
+    nsets = max(3, -(-(MALL_BYTES + (64 << 20)) // (n * c * h * w * 9)))   # float in + int8 + float out
     g = gen(0)
     for _ in range(nsets):
         xs.append(torch.randn(n, c, h, w, generator=g).to(dev))
