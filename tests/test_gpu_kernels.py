@@ -497,6 +497,12 @@ def test_gemm_ksplit(gpu, tile, tile_table):
                 assert torch.equal(y, y0), (tile, m, n, k, out, bias is None)
         want = O.to_bf16(O.dequant(acc, sx.cpu().numpy(), sw.cpu().numpy(), b.cpu().numpy()))
         assert np.array_equal(_f32(kernels.mm_i8_dequant(ag, sx, wg, sw, b, torch.bfloat16)), want), (tile, m, n, k)
+        if ks > 1:
+            # back-to-back launches on one workspace: which workgroup of a tile arrives last (and so reads
+            # the others' partials from other XCDs) varies between launches; every launch gives the sums
+            outs = [kernels.mm_i8(ag, wg) for _ in range(24)]
+            for o in outs:
+                assert torch.equal(o, c), (tile, m, n, k, "repeated launch")
     assert split_seen, f"no shape of the test splits K with {tile}"
     torch.cuda.synchronize()
     for buf in kernels._ws_buf.values():
