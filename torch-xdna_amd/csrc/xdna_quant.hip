@@ -326,80 +326,63 @@ __global__ __launch_bounds__(256) void quant_rows_pipe_kernel(const void* __rest
   }
 }
 
-// Rows of more than 4096 (up to 16 * 256 * G) elements with k % 16 == 0: persistent blocks of 256 threads
-// walk rows with a grid stride; thread t owns groups t, t + 256, ... of 16 consecutive elements, read as raw
-// buffer loads (past the row's end they read zeros; non-temporal under NT) and written as one 16-byte store
-// each. The loads of the block's next row are issued before this row's max, quantize and stores, and the
-// four waves' maxima meet in a double-buffered LDS slot: one barrier per row. (A wave per row holds such a
-// row in up to 224 registers, too many for a second row in flight.)
+// Rows of more than 2048 (up to 16 * 256 * G) elements with k % 16 == 0: one block of 256 threads per row;
+// thread t owns groups t, t + 256, ... of 16 consecutive elements, read as raw buffer loads (past the row's
+// end they read zeros; non-temporal under NT) and written as one 16-byte store each; the four waves' maxima
+// meet in LDS (one barrier). Many small blocks in flight keep HBM busier than persistent blocks that
+// prefetch their next row: with one row per block the registers of a second row are not needed, so more
+// blocks are resident (bf16, G 4: 8192 x 14336 64.2 us against 67.2 us persistent, 8192 x 4096 20.0-21.1
+// against 21.4, 3000 x 3072 8.5 against 8.8; float32 2000 x 8192 16.2 against 16.9, all before the second
+// buffer was dropped). (A wave per row holds such a row in up to 224 registers.)
 template <int DT, int G, bool NT>
-__global__ __launch_bounds__(256) void quant_rows_block_kernel(const void* __restrict__ x, int64_t rows, int64_t k,
-                                                               int64_t ld_x, int8_t* __restrict__ q, int64_t ld_q,
-                                                               int64_t k_pad, float* __restrict__ s) {
+__global__ __launch_bounds__(256) void quant_rows_block_kernel(const void* __restrict__ x, int64_t k, int64_t ld_x,
+                                                               int8_t* __restrict__ q, int64_t ld_q, int64_t k_pad,
+                                                               float* __restrict__ s) {
   using V = Vec16<DT>;
   constexpr int VEC = V::N;
   constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
   constexpr int LPG = 16 / VEC;
-  __shared__ int red[2][4];
+  __shared__ int red[4];
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  const int64_t stride = gridDim.x;
+  const int64_t row = blockIdx.x;
   const int ng = (int)(k / 16);          // at most 256 * G (checked by the launcher)
-  const uint32_t row_bytes = (uint32_t)(k * ESZ);
-  auto load = [&](int64_t row, V (&v)[G][LPG]) {
-    const __amdgpu_buffer_rsrc_t rr =
-        make_rsrc(reinterpret_cast<const char*>(x) + (row < rows ? row : 0) * ld_x * ESZ, row < rows ? row_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t rr = make_rsrc(reinterpret_cast<const char*>(x) + row * ld_x * ESZ, (uint32_t)(k * ESZ));
+  V v[G][LPG];
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-      const uint32_t off = (uint32_t)(t + j * 256) * (16 * ESZ);
+  for (int j = 0; j < G; ++j) {
+    const uint32_t off = (uint32_t)(t + j * 256) * (16 * ESZ);
 #pragma unroll
-      for (int l = 0; l < LPG; ++l) v[j][l].raw = buf_load_u4<NT>(rr, off + l * 16);
-    }
-  };
-  auto process = [&](int64_t row, const V (&v)[G][LPG], int buf) {
-    AbsMaxBits<DT> am;
-#pragma unroll
-    for (int j = 0; j < G; ++j)
-#pragma unroll
-      for (int l = 0; l < LPG; ++l) am.add(v[j][l]);
-    const int wm = wave_max_i(am.lane_bits());
-    if (lane == 0) red[buf][wave] = wm;
-    __syncthreads();
-    const float amax = bits_to_abs<DT>(max(max(red[buf][0], red[buf][1]), max(red[buf][2], red[buf][3])));
-    const float sc = scale_from_amax(amax);
-    const float rc = 1.0f / sc;
-    if (t == 0) s[row] = sc;
-    int8_t* qr = q + row * ld_q;
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-      const int gi = t + j * 256;
-      if (gi < ng) {
-        float f[16];
-#pragma unroll
-        for (int l = 0; l < LPG; ++l)
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) f[l * VEC + e] = v[j][l].get(e);
-        uint32_t w[4];
-        quant_pack<16>(f, sc, rc, w);
-        *reinterpret_cast<uint4*>(qr + (int64_t)gi * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-    }
-    for (int64_t c = k + t; c < k_pad; c += 256) qr[c] = 0;
-  };
-  // red[buf] of row i is read right after the barrier of row i and written again for row i + 2 only
-  // after the barrier of row i + 1, which every wave reaches after its read
-  V va[G][LPG], vb[G][LPG];
-  int64_t row = blockIdx.x;              // block-uniform: every barrier is reached by the whole block
-  load(row, va);
-  while (row < rows) {
-    load(row + stride, vb);
-    process(row, va, 0);
-    row += stride;
-    if (row >= rows) break;
-    load(row + stride, va);
-    process(row, vb, 1);
-    row += stride;
+    for (int l = 0; l < LPG; ++l) v[j][l].raw = buf_load_u4<NT>(rr, off + l * 16);
   }
+  AbsMaxBits<DT> am;
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int l = 0; l < LPG; ++l) am.add(v[j][l]);
+  const int wm = wave_max_i(am.lane_bits());
+  if (lane == 0) red[wave] = wm;
+  __syncthreads();
+  const float amax = bits_to_abs<DT>(max(max(red[0], red[1]), max(red[2], red[3])));
+  const float sc = scale_from_amax(amax);
+  const float rc = 1.0f / sc;
+  if (t == 0) s[row] = sc;
+  int8_t* qr = q + row * ld_q;
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    const int gi = t + j * 256;
+    if (gi < ng) {
+      float f[16];
+#pragma unroll
+      for (int l = 0; l < LPG; ++l)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) f[l * VEC + e] = v[j][l].get(e);
+      uint32_t w[4];
+      quant_pack<16>(f, sc, rc, w);
+      *reinterpret_cast<uint4*>(qr + (int64_t)gi * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  for (int64_t c = k + t; c < k_pad; c += 256) qr[c] = 0;
 }
 
 // Long rows (more than 512 vectors): persistent blocks of 256 threads walk rows with a grid stride;
@@ -513,8 +496,9 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
   }
   const int64_t nvec = k / VEC;
   constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
-  // One wavefront per row with 16-element groups for rows of up to 2048 elements; longer rows take
-  // 256-thread blocks per row, persistent, with the next row's loads in flight (quant_rows_block_kernel).
+  // One wavefront per row with 16-element groups for rows of up to 2048 elements; longer rows take one
+  // 256-thread block per row (quant_rows_block_kernel; the figures below were measured with its earlier
+  // persistent form, which one block per row beats).
   // Measured on MI355X, bf16, against a wave per row: 8192 x 14336 67.4 us against 74.9, 8192 x 4096 21.6
   // against 24.6, 3000 x 3072 8.8 against 10.7, 1024 x 3072 4.8 against 6.3, the decode rows (1 and 16 of
   // 4096 and 14336) 4.0 against 4.3 and 11.2 us; at 2048 elements the wave per row wins (14.0 against 15.9
@@ -522,14 +506,13 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
   const int64_t gpl = cdiv(k / 16, 64);  // groups per lane of a wave
   const int64_t ngr = k / 16;            // groups of the row
   const bool few = rows < 512;
-  if (k % 16 == 0 && gpl > 2 && ngr <= 256 * (DT == XDNA_F32 ? 4 : 8)) {
+  if (k % 16 == 0 && gpl > 2 && ngr <= 256 * (DT == XDNA_F32 ? 4 : 8) && rows < (int64_t(1) << 31)) {
     const bool nt = rows * k * ESZ >= (int64_t(128) << 20);   // half the Infinity Cache
+    const dim3 bg((unsigned)rows);                              // one block per row
 #define XDNA_QB(G_)                                                                                           \
   {                                                                                                           \
-    const dim3 bg(nt ? stream_blocks<quant_rows_block_kernel<DT, G_, true>>(rows)                             \
-                     : stream_blocks<quant_rows_block_kernel<DT, G_, false>>(rows));                          \
-    if (nt) quant_rows_block_kernel<DT, G_, true><<<bg, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);   \
-    else quant_rows_block_kernel<DT, G_, false><<<bg, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);     \
+    if (nt) quant_rows_block_kernel<DT, G_, true><<<bg, 256, 0, st>>>(x, k, ld_x, q, ld_q, k_pad, s);         \
+    else quant_rows_block_kernel<DT, G_, false><<<bg, 256, 0, st>>>(x, k, ld_x, q, ld_q, k_pad, s);           \
   }
     if (ngr <= 256) {
       XDNA_QB(1)
