@@ -301,6 +301,13 @@ int xdna_silu_mul_bf16(const float* gu, int64_t T, int64_t inter, void* y, void*
 /* x += y over n float32 values (residual adds). */
 int xdna_add_f32(float* x, const float* y, int64_t n, void* stream);
 
+/* The residual add and the RMSNorm that follows it in a Qwen3 layer (Qwen3DecoderLayer's
+ * `hidden_states = residual + hidden_states` then the next Qwen3RMSNorm) in one launch: x += a (float32,
+ * x and a [rows, d]), then y as xdna_rmsnorm_bf16 of the updated x. The same values as
+ * xdna_add_f32 followed by xdna_rmsnorm_bf16. */
+int xdna_add_rmsnorm_bf16(float* x, const float* a, int64_t rows, int64_t d, const void* w, int w_dtype, float eps,
+                          void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

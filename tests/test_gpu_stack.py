@@ -37,6 +37,27 @@ def test_rmsnorm_bf16(gpu):
         _close_bf16(y, Q.rms_norm(x.double(), wt.double(), 1e-6))
 
 
+def test_add_rmsnorm_bf16(gpu):
+    """The residual add fused into the norm: x after the launch equals x + a in float32 (torch's CPU sum),
+    and the normalized output equals the separate add then norm launches bit for bit (and the float64
+    norm of x + a within the bf16 tolerance), for d of 1024 and 4096 and both weight dtypes."""
+    from torch_xdna import kernels
+
+    g = torch.Generator().manual_seed(11)
+    for d in (1024, 4096):
+        x = torch.randn(41, d, generator=g) * 3
+        a = torch.randn(41, d, generator=g)
+        w = 1 + 0.1 * torch.randn(d, generator=g)
+        for wt in (w, w.to(torch.bfloat16)):
+            xf = x.to(gpu)
+            y = kernels.add_rmsnorm_bf16(xf, a.to(gpu), wt.to(gpu), 1e-6)
+            assert torch.equal(xf.cpu(), x + a)
+            xs = x.to(gpu)
+            kernels.add_(xs, a.to(gpu))
+            assert torch.equal(y, kernels.rmsnorm_bf16(xs, wt.to(gpu), 1e-6)), (d, wt.dtype)
+            _close_bf16(y, Q.rms_norm((x + a).double(), wt.double(), 1e-6))
+
+
 def test_qk_norm_rope(gpu):
     """q / k heads RMSNorm'd and rotated at each token's own position; v lands transposed at its column."""
     from torch_xdna import kernels

@@ -39,14 +39,16 @@ __device__ __forceinline__ float ld(const void* p, int64_t i) {
 }
 
 // ------------------------------------------------------------------------------ RMSNorm -> bf16
-// One 256-thread block per row; d % 4 == 0 and d <= 4096 (the host checks).
-template <int WDT>
-__global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const float* __restrict__ x, int64_t d,
-                                                           const void* __restrict__ w, float eps,
+// One 256-thread block per row; d % 256 == 0 and d <= 4096 (the host checks). ADD: the residual add
+// that precedes the norm in the layer, x += a, in the same launch (the float32 sums are written back
+// and normalized as the separate add and norm would: the same values, one launch fewer).
+template <int WDT, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(float* __restrict__ x, const float* __restrict__ a,
+                                                           int64_t d, const void* __restrict__ w, float eps,
                                                            uint16_t* __restrict__ y) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
-  const float* xr = x + row * d;
+  float* xr = x + row * d;
   float v[16];
   float ss = 0.0f;
   const int nper = (int)(d / 256);       // d is a multiple of 256 here, at most 16 per thread
@@ -55,6 +57,10 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const float* __restri
     v[j] = 0.0f;
     if (j < nper) {
       v[j] = xr[j * 256 + threadIdx.x];
+      if constexpr (ADD) {
+        v[j] = v[j] + a[row * d + j * 256 + threadIdx.x];
+        xr[j * 256 + threadIdx.x] = v[j];
+      }
       ss += v[j] * v[j];
     }
   }
@@ -243,10 +249,25 @@ int xdna_rmsnorm_bf16(const float* x, int64_t rows, int64_t d, const void* w, in
   XDNA_REQUIRE(x && w && y && rows < (1ll << 31), "bad arguments");
   hipStream_t st = as_stream(stream);
   uint16_t* yb = static_cast<uint16_t*>(y);
-  if (w_dtype == XDNA_F32) rmsnorm_bf16_kernel<XDNA_F32><<<(unsigned)rows, 256, 0, st>>>(x, d, w, eps, yb);
-  else if (w_dtype == XDNA_BF16) rmsnorm_bf16_kernel<XDNA_BF16><<<(unsigned)rows, 256, 0, st>>>(x, d, w, eps, yb);
-  else rmsnorm_bf16_kernel<XDNA_F16><<<(unsigned)rows, 256, 0, st>>>(x, d, w, eps, yb);
+  float* xm = const_cast<float*>(x);     // read only without ADD
+  if (w_dtype == XDNA_F32) rmsnorm_bf16_kernel<XDNA_F32, false><<<(unsigned)rows, 256, 0, st>>>(xm, nullptr, d, w, eps, yb);
+  else if (w_dtype == XDNA_BF16) rmsnorm_bf16_kernel<XDNA_BF16, false><<<(unsigned)rows, 256, 0, st>>>(xm, nullptr, d, w, eps, yb);
+  else rmsnorm_bf16_kernel<XDNA_F16, false><<<(unsigned)rows, 256, 0, st>>>(xm, nullptr, d, w, eps, yb);
   return launch_status("rmsnorm_bf16");
+}
+
+int xdna_add_rmsnorm_bf16(float* x, const float* a, int64_t rows, int64_t d, const void* w, int w_dtype, float eps,
+                          void* y, void* stream) {
+  XDNA_REQUIRE(w_dtype == XDNA_F32 || w_dtype == XDNA_BF16 || w_dtype == XDNA_F16, "w_dtype must be F32/BF16/F16");
+  XDNA_REQUIRE(rows >= 0 && d >= 256 && d % 256 == 0 && d <= 4096, "d must be a multiple of 256, at most 4096");
+  if (rows == 0) return XDNA_OK;
+  XDNA_REQUIRE(x && a && w && y && rows < (1ll << 31), "bad arguments");
+  hipStream_t st = as_stream(stream);
+  uint16_t* yb = static_cast<uint16_t*>(y);
+  if (w_dtype == XDNA_F32) rmsnorm_bf16_kernel<XDNA_F32, true><<<(unsigned)rows, 256, 0, st>>>(x, a, d, w, eps, yb);
+  else if (w_dtype == XDNA_BF16) rmsnorm_bf16_kernel<XDNA_BF16, true><<<(unsigned)rows, 256, 0, st>>>(x, a, d, w, eps, yb);
+  else rmsnorm_bf16_kernel<XDNA_F16, true><<<(unsigned)rows, 256, 0, st>>>(x, a, d, w, eps, yb);
+  return launch_status("add_rmsnorm_bf16");
 }
 
 int xdna_qk_norm_rope(const float* qkv, int64_t T, int nh, int nkv, const void* q_w, const void* k_w, int w_dtype,

@@ -115,6 +115,7 @@ def _declare(L):
         "xdna_tile_plan": ([i, i64, i64, i64, p, p, p], i),
         "xdna_tile_clear": ([], i),
         "xdna_rmsnorm_bf16": ([p, i64, i64, p, i, ctypes.c_float, p, p], i),
+        "xdna_add_rmsnorm_bf16": ([p, p, i64, i64, p, i, ctypes.c_float, p, p], i),
         "xdna_qk_norm_rope": ([p, i64, i, i, p, p, i, p, p, p, ctypes.c_float, p, p, p, i64, p], i),
         "xdna_attention_bf16": ([p, p, p, i64, p, p, p, i64, i64, i, i, ctypes.c_float, p, p], i),
         "xdna_silu_mul_bf16": ([p, i64, i64, p, p], i),
@@ -131,7 +132,8 @@ EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quan
            "xdna_conv_quant_nhwc_noalloc", "xdna_conv_weight_pack",
            "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv3x3_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8",
            "xdna_nhwc_to_nchw_i8",
-           "xdna_tile_set", "xdna_tile_get", "xdna_tile_plan", "xdna_tile_clear", "xdna_rmsnorm_bf16", "xdna_qk_norm_rope",
+           "xdna_tile_set", "xdna_tile_get", "xdna_tile_plan", "xdna_tile_clear", "xdna_rmsnorm_bf16",
+           "xdna_add_rmsnorm_bf16", "xdna_qk_norm_rope",
            "xdna_attention_bf16", "xdna_silu_mul_bf16", "xdna_add_f32")
 
 
@@ -578,6 +580,21 @@ def rmsnorm_bf16(x, w, eps):
         with _on(dev):
             _check(lib().xdna_rmsnorm_bf16(_ptr(x), R, D, _ptr(w), _wcode(w), float(eps), _ptr(y), _stream(dev)),
                    "rmsnorm_bf16")
+    return y
+
+
+def add_rmsnorm_bf16(x, a, w, eps):
+    """x += a, then rmsnorm_bf16(x, w, eps), in one launch (x, a float32 [R, D], contiguous; D a multiple
+    of 256): the same values as add_ followed by rmsnorm_bf16."""
+    dev = _need_gpu(x, a, w)
+    R, D = x.shape
+    if a.shape != x.shape or not (x.is_contiguous() and a.is_contiguous()):
+        raise ValueError("add_rmsnorm_bf16: x and a must be contiguous tensors of one shape")
+    y = torch.empty((R, D), dtype=torch.bfloat16, device=dev)
+    if R:
+        with _on(dev):
+            _check(lib().xdna_add_rmsnorm_bf16(_ptr(x), _ptr(a), R, D, _ptr(w), _wcode(w), float(eps), _ptr(y),
+                                               _stream(dev)), "add_rmsnorm_bf16")
     return y
 
 

@@ -511,18 +511,23 @@ def _forward(pk, shape, x2d):
     T = x2d.shape[0]
     X = x2d.contiguous()
     max_len = max(shape.lens)
+
+    def norm(w, pending):
+        # a residual add is always followed by a norm: the two run as one launch
+        return kernels.rmsnorm_bf16(X, w, EPS) if pending is None else kernels.add_rmsnorm_bf16(X, pending, w, EPS)
+
+    down = None                           # the MLP output still to be added to X
     for L in pk["layers"]:
-        h = kernels.rmsnorm_bf16(X, L["input_norm"], EPS)
+        h = norm(L["input_norm"], down)
         qkv = kernels.mm_bf16(h, L["qkv"], None, torch.float32)
         q, k = kernels.qk_norm_rope(qkv, NH, NKV, L["q_norm"], L["k_norm"], pk["inv_freq"], shape.pos, shape.vt_col,
                                     EPS, shape.vt)
         att = kernels.attention_bf16(q, k, shape.vt, shape.seq_start, shape.seq_len, shape.seq_vt, max_len,
                                      DH ** -0.5)
-        kernels.add_(X, kernels.mm_bf16(att.view(T, NH * DH), L["o"], None, torch.float32))
-        h = kernels.rmsnorm_bf16(X, L["post_norm"], EPS)
+        h = norm(L["post_norm"], kernels.mm_bf16(att.view(T, NH * DH), L["o"], None, torch.float32))
         act = kernels.silu_mul_bf16(kernels.mm_bf16(h, L["gu"], None, torch.float32))
-        kernels.add_(X, kernels.mm_bf16(act, L["down"], None, torch.float32))
-    h = kernels.rmsnorm_bf16(X, pk["norm"], EPS)
+        down = kernels.mm_bf16(act, L["down"], None, torch.float32)
+    h = norm(pk["norm"], down)
     return kernels.mm_bf16(h, pk["head"], pk["bias"], torch.float32)
 
 
