@@ -258,74 +258,6 @@ __global__ __launch_bounds__(256) void quant_rows_wave_kernel(const void* __rest
   for (int64_t c = k + t; c < k_pad; c += 64) qr[c] = 0;
 }
 
-// The same quantize with persistent waves: wave i of the grid walks rows i, i + W, i + 2W, ... (W waves in
-// the grid), and the 16-byte loads of its next row are issued before the current row's max, quantize and
-// stores, so loads, arithmetic and stores of different rows overlap (with one row per wave they run in
-// three bursts). Two register sets alternate between the rows.
-template <int DT, int G, bool NT>
-__global__ __launch_bounds__(256) void quant_rows_pipe_kernel(const void* __restrict__ x, int64_t rows, int64_t k,
-                                                              int64_t ld_x, int8_t* __restrict__ q, int64_t ld_q,
-                                                              int64_t k_pad, float* __restrict__ s) {
-  using V = Vec16<DT>;
-  constexpr int VEC = V::N;
-  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
-  constexpr int LPG = 16 / VEC;
-  const int t = threadIdx.x & 63;
-  const int64_t stride = (int64_t)gridDim.x * 4;
-  const int ng = (int)(k / 16);
-  const uint32_t row_bytes = (uint32_t)(k * ESZ);
-  auto load = [&](int64_t row, V (&v)[G][LPG]) {
-    // rows past the end read zeros (out-of-range resource); the row as its own buffer resource
-    const __amdgpu_buffer_rsrc_t rr =
-        make_rsrc(reinterpret_cast<const char*>(x) + (row < rows ? row : 0) * ld_x * ESZ, row < rows ? row_bytes : 0u);
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-      const uint32_t off = (uint32_t)(t + j * 64) * (16 * ESZ);
-#pragma unroll
-      for (int l = 0; l < LPG; ++l) v[j][l].raw = buf_load_u4<NT>(rr, off + l * 16);
-    }
-  };
-  auto process = [&](int64_t row, const V (&v)[G][LPG]) {
-    AbsMaxBits<DT> am;
-#pragma unroll
-    for (int j = 0; j < G; ++j)
-#pragma unroll
-      for (int l = 0; l < LPG; ++l) am.add(v[j][l]);
-    const float amax = bits_to_abs<DT>(wave_max_i(am.lane_bits()));
-    const float sc = scale_from_amax(amax);
-    const float rc = 1.0f / sc;
-    if (t == 0) s[row] = sc;
-    int8_t* qr = q + row * ld_q;
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-      const int gi = t + j * 64;
-      if (gi < ng) {
-        float f[16];
-#pragma unroll
-        for (int l = 0; l < LPG; ++l)
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) f[l * VEC + e] = v[j][l].get(e);
-        uint32_t w[4];
-        quant_pack<16>(f, sc, rc, w);
-        *reinterpret_cast<uint4*>(qr + (int64_t)gi * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-    }
-    for (int64_t c = k + t; c < k_pad; c += 64) qr[c] = 0;
-  };
-  V va[G][LPG], vb[G][LPG];
-  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  load(row, va);
-  while (row < rows) {                   // wave-uniform: no barrier in the loop
-    load(row + stride, vb);
-    process(row, va);
-    row += stride;
-    if (row >= rows) break;
-    load(row + stride, va);
-    process(row, vb);
-    row += stride;
-  }
-}
-
 // Rows of more than 2048 (up to 16 * 256 * G) elements with k % 16 == 0: one block of 256 threads per row;
 // thread t owns groups t, t + 256, ... of 16 consecutive elements, read as raw buffer loads (past the row's
 // end they read zeros; non-temporal under NT) and written as one 16-byte store each; the four waves' maxima
@@ -528,26 +460,11 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
   }
   if (k % 16 == 0 && k < (int64_t(1) << 31) && gpl <= 2) {
     const bool nt = rows * k * (DT == XDNA_F32 ? 4 : 2) >= (int64_t(128) << 20);   // half the Infinity Cache
+    // one wave per row at any row count: a grid of many more waves than are resident keeps more loads in
+    // flight than persistent waves that prefetch their next row (measured against such a kernel, bf16:
+    // 3000 x 1024 4.9 against 5.1 us, 8192 x 2048 12.6 against 13.8 us, 8192 x 1024 8.2 against 8.5 us;
+    // float32 4096 x 2048 10.9 against 11.7 us)
     const dim3 grid((unsigned)cdiv(rows, 4));
-    // at least 8 rows per CU: one round of resident workgroups whose waves take the rows beyond it, so the
-    // loads of a wave's next row overlap this row's arithmetic (a sweep of 1, 2, 4, 8 and 16 rows per wave
-    // on MI355X: 4.5 TB/s at one or two on 8192 x 4096 bf16, against 2.7 TB/s for two rounds of one-row
-    // waves; more rows per wave leave too few waves in flight)
-    if (rows >= 8 * (int64_t)device_cus()) {
-      const int64_t want = cdiv(rows, 4);
-      const dim3 pg(gpl <= 1 ? stream_blocks<quant_rows_pipe_kernel<DT, 1, false>>(want)
-                             : stream_blocks<quant_rows_pipe_kernel<DT, 2, false>>(want));
-#define XDNA_QP(G_)                                                                                        \
-  if (nt) quant_rows_pipe_kernel<DT, G_, true><<<pg, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s); \
-  else quant_rows_pipe_kernel<DT, G_, false><<<pg, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
-      if (gpl <= 1) {
-        XDNA_QP(1)
-      } else {
-        XDNA_QP(2)
-      }
-#undef XDNA_QP
-      return launch_status("quant_rows");
-    }
 #define XDNA_QW(G_)                                                                                     \
   if (nt) quant_rows_wave_kernel<DT, G_, true><<<grid, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s); \
   else quant_rows_wave_kernel<DT, G_, false><<<grid, 256, 0, st>>>(x, rows, k, ld_x, q, ld_q, k_pad, s);
