@@ -298,6 +298,15 @@ int xdna_attention_bf16(const void* q, const void* k, const void* vt, int64_t ld
 /* y = bf16(silu(gu[:, :inter]) * gu[:, inter:]), gu float32 [T, 2 inter] (gate, then up). */
 int xdna_silu_mul_bf16(const float* gu, int64_t T, int64_t inter, void* y, void* stream);
 
+/* The gate|up projection of Qwen3MLP with `act_fn(gate_proj(x)) * up_proj(x)` fused into the GEMM:
+ * y[m, c] = bf16(silu(g) * u), g and u the float32 sums of a[m, :] with gate row c and up row c
+ * (silu(g) = g / (1 + exp(-g))), the values of xdna_gemm_bf16 (float32 out) then xdna_silu_mul_bf16
+ * in one launch. w is [n2, k] bf16 with the gate and up rows interleaved in pairs: rows 4j, 4j + 1 are
+ * gate rows 2j, 2j + 1 and rows 4j + 2, 4j + 3 up rows 2j, 2j + 1 (n2 = 2 inter, a multiple of 4); y is
+ * bf16 [m, n2 / 2] with row stride ldy (even, 4-byte aligned). Operand rules of xdna_gemm_bf16. */
+int xdna_gemm_bf16_silu(const void* a, int64_t lda, const void* w, int64_t ldw, void* y, int64_t ldy, int64_t m,
+                        int64_t n2, int64_t k, void* stream);
+
 /* x += y over n float32 values (residual adds). */
 int xdna_add_f32(float* x, const float* y, int64_t n, void* stream);
 

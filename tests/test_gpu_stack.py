@@ -58,6 +58,39 @@ def test_add_rmsnorm_bf16(gpu):
             _close_bf16(y, Q.rms_norm((x + a).double(), wt.double(), 1e-6))
 
 
+@pytest.mark.parametrize("tile", ["t64x64", "t32x64k4", "t128x128", "t256x256w8", "small_w2", "gemv_w4", "seg4_r2"])
+def test_gemm_bf16_silu(gpu, tile):
+    """The gate|up GEMM with SiLU(gate) * up in its epilogue, on the interleaved weight, against the float32
+    GEMM of the concatenated weight then the separate SiLU kernel, with the same tile forced on both (their
+    float sums then match), bit for bit; rows from 1 to 486, ragged rows and K, and the one-row and few-row
+    tiles, which the fused form replaces by the small-M kernel (there only the float64 bound is checked)."""
+    from torch_xdna import kernels
+
+    kernels.use_tuned(False)
+    kernels.tile_clear()
+    try:
+        g = torch.Generator().manual_seed(5)
+        for m, inter, k in [(1, 3072, 1024), (5, 256, 1024), (16, 260, 40), (70, 3072, 1024), (486, 3072, 1024)]:
+            x = (torch.randn(m, k, generator=g)).to(torch.bfloat16)
+            gate = (torch.randn(inter, k, generator=g) * 0.05).to(torch.bfloat16)
+            up = (torch.randn(inter, k, generator=g) * 0.05).to(torch.bfloat16)
+            kernels.tile_set("bf16", m, 2 * inter, k, tile)
+            xg = x.to(gpu)
+            y = kernels.mm_bf16_silu(xg, kernels.gate_up_interleaved(gate, up).to(gpu))
+            assert y.shape == (m, inter) and y.dtype == torch.bfloat16
+            ref = kernels.silu_mul_bf16(kernels.mm_bf16(xg, torch.cat([gate, up]).to(gpu), None, torch.float32))
+            if not tile.startswith(("gemv", "seg4")):
+                assert torch.equal(y, ref), (tile, m, inter, k)
+            gd, ud = x.double() @ gate.double().t(), x.double() @ up.double().t()
+            want = torch.nn.functional.silu(gd) * ud
+            err = (y.double().cpu() - want).abs().max() / want.abs().max()
+            assert err < 2e-2, (tile, m, inter, k, float(err))
+            kernels.tile_set("bf16", m, 2 * inter, k, "auto")
+    finally:
+        kernels.tile_clear()
+        kernels._tuned_applied = None
+
+
 def test_qk_norm_rope(gpu):
     """q / k heads RMSNorm'd and rotated at each token's own position; v lands transposed at its column."""
     from torch_xdna import kernels

@@ -122,3 +122,20 @@ def test_backend_keeps_host_stacks_plain():
         y = torch.compile(net, backend="xdna", options={"fallback": "eager"})(x, mask)
     assert not runtime.stats.as_dict()["stacks"]
     assert rel_err(y, ref) < 0.05
+
+
+def test_gate_up_interleaved():
+    """The fused SiLU GEMM's weight: gate and up rows in pairs, rows 4j, 4j + 1 gate rows 2j, 2j + 1 and rows
+    4j + 2, 4j + 3 up rows 2j, 2j + 1; an odd row count is refused."""
+    from torch_xdna import kernels
+
+    gate = torch.arange(6 * 3).view(6, 3).float()
+    up = -gate - 1
+    w = kernels.gate_up_interleaved(gate, up)
+    assert w.shape == (12, 3)
+    order = [("g", 0), ("g", 1), ("u", 0), ("u", 1), ("g", 2), ("g", 3), ("u", 2), ("u", 3), ("g", 4), ("g", 5),
+             ("u", 4), ("u", 5)]
+    for r, (which, i) in enumerate(order):
+        assert torch.equal(w[r], (gate if which == "g" else up)[i]), r
+    with pytest.raises(ValueError):
+        kernels.gate_up_interleaved(gate[:5], up[:5])

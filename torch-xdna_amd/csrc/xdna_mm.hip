@@ -51,10 +51,13 @@ namespace xdna {
 // EPI_BF_*: the bf16 GEMM (precision "bf16"): float accumulators, + bias, cast to the output dtype.
 enum Epi {
   EPI_I32 = 0, EPI_REQUANT = 2, EPI_CALIB = 3, EPI_DQ_F32 = 4, EPI_DQ_BF16 = 5, EPI_DQ_F16 = 6,
-  EPI_BF_F32 = 7, EPI_BF_BF16 = 8, EPI_BF_F16 = 9
+  EPI_BF_F32 = 7, EPI_BF_BF16 = 8, EPI_BF_F16 = 9, EPI_BF_SILU = 10
 };
 constexpr bool epi_dq(int e) { return e == EPI_DQ_F32 || e == EPI_DQ_BF16 || e == EPI_DQ_F16; }
-constexpr bool epi_bf(int e) { return e == EPI_BF_F32 || e == EPI_BF_BF16 || e == EPI_BF_F16; }
+// EPI_BF_SILU: the bf16 GEMM of a gated MLP's gate|up projection, its weight rows interleaved in pairs
+// (gate 2j, gate 2j + 1, up 2j, up 2j + 1): each group of four sums gives two bf16 outputs silu(g) * u,
+// column n of the GEMM writing output column n / 2.
+constexpr bool epi_bf(int e) { return e == EPI_BF_F32 || e == EPI_BF_BF16 || e == EPI_BF_F16 || e == EPI_BF_SILU; }
 
 struct EpiArgs {
   void* out;            // int32 C, float y, or int8/uint8 q (NHWC); with dq_out float y (NCHW)
@@ -182,6 +185,30 @@ __device__ __forceinline__ void epilogue_w(const EpiArgs& e, int64_t m, int64_t 
 #pragma unroll
       for (int r = 0; r < CW; ++r)
         if (n + r < N) o[r] = (uint8_t)(qv[r] & 0xff);
+    }
+  } else if constexpr (EPI == EPI_BF_SILU) {
+    // n is a multiple of 4 and N of 4 (the launcher checks): a group of four columns is wholly in or out;
+    // silu(g) * u as the separate kernel computes it, g / (1 + exp(-g)) * u
+    uint32_t h[CW / 4];
+#pragma unroll
+    for (int q = 0; q < CW / 4; ++q) {
+      float y2[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const float g = __builtin_bit_cast(float, acc[4 * q + r]);
+        const float u = __builtin_bit_cast(float, acc[4 * q + 2 + r]);
+        y2[r] = g / (1.0f + __expf(-g)) * u;
+      }
+      h[q] = f32x2_to_bf16x2_bits(y2[0], y2[1]);
+    }
+    uint16_t* y = reinterpret_cast<uint16_t*>(e.out) + m * e.ldo + n / 2;
+    if (vec) {
+      if constexpr (CW == 8) *reinterpret_cast<uint2*>(y) = make_uint2(h[0], h[1]);
+      else *reinterpret_cast<uint32_t*>(y) = h[0];
+    } else {
+#pragma unroll
+      for (int q = 0; q < CW / 4; ++q)
+        if (n + 4 * q < N) *reinterpret_cast<uint32_t*>(y + 2 * q) = h[q];
     }
   } else {
     // EPI_DQ_*: ((float)acc * sx[m]) * sw[n] (+ bias[n]), each step rounded once;
@@ -1304,7 +1331,8 @@ inline EpiArgs shift_epi(const EpiArgs& e, int out_bytes, int64_t m0, int64_t n0
 template <int EPI>
 constexpr int out_bytes() {
   return (EPI == EPI_I32 || EPI == EPI_DQ_F32 || EPI == EPI_BF_F32) ? 4
-         : (EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16 || EPI == EPI_BF_BF16 || EPI == EPI_BF_F16) ? 2
+         : (EPI == EPI_DQ_BF16 || EPI == EPI_DQ_F16 || EPI == EPI_BF_BF16 || EPI == EPI_BF_F16 ||
+            EPI == EPI_BF_SILU) ? 2     // EPI_BF_SILU: per output row; its calls make no column chunks
                                                                                                : 1;
 }
 
@@ -1484,6 +1512,10 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
   // resource, 16 rows per grid row
   if (is_gemv(tile) && M != 1) tile = rule_tile(M, N, K, M > 1);
   if (is_seg4(tile) && M > 16) tile = rule_tile(M, N, K, true);
+  // the one-row and few-row kernels write one column per lane: the fused SiLU needs a column's partner
+  if (EPI == EPI_BF_SILU && (is_gemv(tile) || is_seg4(tile))) tile = T_SMALL2;
+  if (is_small(tile) && (M * lda > MAX_BUF || (M + 15) / 16 >= 65536)) tile = rule_tile(M, N, K, false);
+  if constexpr (EPI != EPI_BF_SILU) {
   if (is_seg4(tile)) {
     // four rows per segment group; the workgroup's 4 waves split K into multiples of 256 bytes
     constexpr int W = 4;
@@ -1512,7 +1544,6 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
     }
     return XDNA_OK;
   }
-  if (is_small(tile) && (M * lda > MAX_BUF || (M + 15) / 16 >= 65536)) tile = rule_tile(M, N, K, false);
   if (is_gemv(tile)) {
     // one wave per output column, the weight in row chunks one buffer resource can address; K in
     // rounds of 4 KB (K <= 4 KB) or 16 KB
@@ -1538,6 +1569,7 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
       if (rc) return rc;
     }
     return XDNA_OK;
+  }
   }
   if (is_small(tile)) {
     // weight streaming: the waves of a workgroup split K into multiples of 64 bytes; the weight is
@@ -1687,6 +1719,26 @@ int xdna_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const
   if (y_dtype == XDNA_F32) return launch_gemm<EPI_BF_F32>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, tile, st);
   if (y_dtype == XDNA_BF16) return launch_gemm<EPI_BF_BF16>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, tile, st);
   return launch_gemm<EPI_BF_F16>(ab, 2 * lda, wb, 2 * ldw, m, n, 2 * k, e, tile, st);
+}
+
+int xdna_gemm_bf16_silu(const void* a, int64_t lda, const void* w, int64_t ldw, void* y, int64_t ldy, int64_t m,
+                        int64_t n2, int64_t k, void* stream) {
+  XDNA_REQUIRE(m >= 0 && n2 >= 0 && k >= 0, "negative size");
+  if (m == 0 || n2 == 0) return XDNA_OK;
+  XDNA_REQUIRE(n2 % 4 == 0, "n2 (gate and up rows together) must be a multiple of 4");
+  XDNA_REQUIRE(k % 8 == 0 && k >= 8, "k must be a positive multiple of 8 (16-byte bf16 rows; pad with zeros)");
+  XDNA_REQUIRE(lda >= k && ldw >= k && lda % 8 == 0 && ldw % 8 == 0 && ldy >= n2 / 2 && ldy % 2 == 0,
+               "bad leading dimensions");
+  XDNA_REQUIRE(a && w && y && aligned(a, 16) && aligned(w, 16) && aligned(y, 4), "misaligned operands");
+  XDNA_REQUIRE(n2 * ldw * 2 <= MAX_BUF, "the gate|up weight must be at most 1 GB");   // no column chunks
+  EpiArgs e{};
+  e.out = y;
+  e.ldo = ldy;
+  e.vec_ok = (ldy % 4 == 0) && aligned(y, 8);
+  const int8_t* ab = static_cast<const int8_t*>(a);
+  const int8_t* wb = static_cast<const int8_t*>(w);
+  const int tile = choose_tile(XDNA_KIND_BF16, m, n2, k, 2 * k);
+  return launch_gemm<EPI_BF_SILU>(ab, 2 * lda, wb, 2 * ldw, m, n2, 2 * k, e, tile, as_stream(stream));
 }
 
 int xdna_conv3x3_i8(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad, const int8_t* wq, int64_t co,

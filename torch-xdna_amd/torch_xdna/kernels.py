@@ -100,6 +100,7 @@ def _declare(L):
         "xdna_gemm_i8_i32_ws": ([p, i64, p, i64, p, i64, i64, i64, i64, p, i64, p], i),
         "xdna_gemm_i8_dequant_ws": ([p, i64, p, p, i64, p, p, p, i, i64, i64, i64, i64, p, i64, p], i),
         "xdna_gemm_bf16": ([p, i64, p, i64, p, p, i, i64, i64, i64, i64, p], i),
+        "xdna_gemm_bf16_silu": ([p, i64, p, i64, p, i64, i64, i64, i64, p], i),
         "xdna_pad_rows_i8": ([p, i64, i64, i64, p, i64, i64, p], i),
         "xdna_conv_quant_nhwc": ([p, i, i64, i64, i64, i64, p, i64, p, p, p], i),
         "xdna_conv_quant_nhwc_noalloc": ([p, i, i64, i64, i64, i64, p, i64, p, p], i),
@@ -128,7 +129,7 @@ def _declare(L):
 
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
            "xdna_gemm_i8_dequant", "xdna_gemm_ws_bytes", "xdna_gemm_ksplit", "xdna_gemm_i8_i32_ws", "xdna_gemm_i8_dequant_ws",
-           "xdna_gemm_bf16", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc",
+           "xdna_gemm_bf16", "xdna_gemm_bf16_silu", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc",
            "xdna_conv_quant_nhwc_noalloc", "xdna_conv_weight_pack",
            "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv3x3_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8",
            "xdna_nhwc_to_nchw_i8",
@@ -434,6 +435,32 @@ def mm_bf16(a, w, bias, out_dtype):
         with _on(dev):
             _check(lib().xdna_gemm_bf16(_ptr(a), a.stride(0), _ptr(w), w.stride(0), _ptr(bias), _ptr(y),
                                         _DTYPE_CODE[out_dtype], y.stride(0), M, N, K, _stream(dev)), "gemm_bf16")
+    return y
+
+
+def gate_up_interleaved(gate, up):
+    """The [2 I, K] weight xdna_gemm_bf16_silu takes: gate and up rows interleaved in pairs (rows 4j, 4j + 1
+    gate rows 2j, 2j + 1; rows 4j + 2, 4j + 3 up rows 2j, 2j + 1). I must be even."""
+    I, K = gate.shape
+    if up.shape != (I, K) or I % 2:
+        raise ValueError(f"gate_up_interleaved: two [I, K] weights with I even, got {tuple(gate.shape)} {tuple(up.shape)}")
+    return torch.stack([gate.reshape(I // 2, 2, K), up.reshape(I // 2, 2, K)], dim=1).reshape(2 * I, K)
+
+
+def mm_bf16_silu(a, w_gu):
+    """bf16 [M, I] = silu(a @ gate^T) * (a @ up^T) in one kernel, with w_gu the bf16 [2 I, Kp] weight of
+    gate_up_interleaved: the values of mm_bf16 (float32 out, gate|up concatenated) then silu_mul_bf16."""
+    dev = _need_gpu(a, w_gu)
+    M, K = a.shape
+    N2 = w_gu.shape[0]
+    if w_gu.shape[1] != K or a.dtype != torch.bfloat16 or w_gu.dtype != torch.bfloat16 or N2 % 4:
+        raise ValueError(f"mm_bf16_silu: bf16 [M, K] x [2I, K] operands (2I a multiple of 4), got {a.dtype} "
+                         f"{tuple(a.shape)}, {w_gu.dtype} {tuple(w_gu.shape)}")
+    y = torch.empty((M, N2 // 2), dtype=torch.bfloat16, device=dev)
+    if M and N2:
+        with _on(dev):
+            _check(lib().xdna_gemm_bf16_silu(_ptr(a), a.stride(0), _ptr(w_gu), w_gu.stride(0), _ptr(y), y.stride(0),
+                                             M, N2, K, _stream(dev)), "gemm_bf16_silu")
     return y
 
 

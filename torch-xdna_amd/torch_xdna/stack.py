@@ -357,8 +357,9 @@ class _Stack:
         return st
 
     def packed(self, dev):
-        """The GEMM weights as bf16 [N, K] on dev (q|k|v and gate|up concatenated), the norms and
-        RoPE frequencies as given; built again when a weight changed (its _version)."""
+        """The GEMM weights as bf16 [N, K] on dev (q|k|v concatenated, gate and up interleaved in row pairs
+        for the GEMM with the SiLU fused), the norms and RoPE frequencies as given; built again when a
+        weight changed (its _version)."""
         ts = [r() for r in self.refs]
         if any(t is None for t in ts):
             raise RuntimeError("the stack's weights are gone")
@@ -378,7 +379,8 @@ class _Stack:
         layers = []
         for i in range(self.layers):
             Lw = dict(zip(LAYER_KEYS, ts[i * n:(i + 1) * n]))
-            layers.append(dict(qkv=bf(Lw["q"], Lw["k"], Lw["v"]), o=bf(Lw["o"]), gu=bf(Lw["gate"], Lw["up"]),
+            gu = kernels.gate_up_interleaved(Lw["gate"].detach().to(dev), Lw["up"].detach().to(dev))
+            layers.append(dict(qkv=bf(Lw["q"], Lw["k"], Lw["v"]), o=bf(Lw["o"]), gu=bf(gu),
                                down=bf(Lw["down"]), input_norm=vec(Lw["input_norm"]), post_norm=vec(Lw["post_norm"]),
                                q_norm=vec(Lw["q_norm"]), k_norm=vec(Lw["k_norm"])))
         norm, head, inv_freq = ts[self.layers * n:]
@@ -525,7 +527,7 @@ def _forward(pk, shape, x2d):
         att = kernels.attention_bf16(q, k, shape.vt, shape.seq_start, shape.seq_len, shape.seq_vt, max_len,
                                      DH ** -0.5)
         h = norm(L["post_norm"], kernels.mm_bf16(att.view(T, NH * DH), L["o"], None, torch.float32))
-        act = kernels.silu_mul_bf16(kernels.mm_bf16(h, L["gu"], None, torch.float32))
+        act = kernels.mm_bf16_silu(h, L["gu"])
         down = kernels.mm_bf16(act, L["down"], None, torch.float32)
     h = norm(pk["norm"], down)
     return kernels.mm_bf16(h, pk["head"], pk["bias"], torch.float32)
