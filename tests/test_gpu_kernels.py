@@ -509,6 +509,38 @@ def test_gemm_ksplit(gpu, tile, tile_table):
         assert int(buf[:65536].view(torch.int32).abs().sum()) == 0, "arrival counters not back to zero"
 
 
+@pytest.mark.parametrize("tile", ["t256x256w8", "t128x256w8"])
+def test_conv_halo(gpu, tile, tile_table):
+    """The conv from a haloed input tile (the 8-wave 256 x 256 and 128 x 256 tiles when a tile is whole image
+    rows, or a segment of one row, of one image): the input pixels of a tile and their one-pixel border are
+    loaded once per 64-channel slice and read at each tap's offset. Image rows of 32 to 512 pixels (several
+    rows per tile, one, half a row), 1, 2 and 4 channel slices, ragged and several column tiles, batches
+    of one and two: the requantized integers against the oracle, the fused dequantize against the
+    separate one and the calibration max."""
+    from torch_xdna import kernels
+
+    for n, ci, co, h, w_ in [(2, 64, 256, 8, 64), (1, 128, 200, 16, 32), (1, 256, 512, 4, 128),
+                             (2, 64, 256, 3, 256), (1, 128, 256, 2, 512)]:
+        c_pad = ci
+        kernels.tile_set("conv", n * h * w_, co, 9 * c_pad, tile)
+        assert kernels.tile_get(gpu, "conv", n * h * w_, co, 9 * c_pad) == tile
+        xq = _i8((n, ci, h, w_), seed=ci + h + w_)
+        wq = _i8((co, ci, 3, 3), seed=co + w_)
+        packed = wq.permute(0, 2, 3, 1).reshape(co, 9, ci).contiguous()
+        x_nhwc = kernels.nchw_to_nhwc(xq.to(gpu), c_pad)
+        acc = c_oracle.conv3x3_acc(xq.numpy(), wq.numpy())
+        for relu in (False, True):
+            q = kernels.conv3x3(x_nhwc, packed.to(gpu), 12, relu)
+            assert np.array_equal(_np(q).transpose(0, 3, 1, 2), O.requant(acc, 12, relu)), (tile, n, ci, co, h, w_, relu)
+        scale = (torch.rand(co) + 0.5).to(gpu)
+        sx = (torch.rand(n) + 0.5).to(gpu)
+        want = kernels.conv_dequant(q, True, scale, sx, None, torch.float32)
+        assert torch.equal(kernels.conv3x3_dequant(x_nhwc, packed.to(gpu), 12, True, scale, sx, None, torch.float32),
+                           want), ("fused dequant", tile, n, ci, co, h, w_)
+        top = kernels.conv3x3_calibrate(x_nhwc[:1], packed.to(gpu), False)
+        assert top == int(np.abs(acc[:1]).max()), (tile, n, ci, co, h, w_)
+
+
 @pytest.mark.parametrize("tile", ["t256x256w8", "t256x128w8", "t128x256", "t256x256pp"])
 def test_tiles_tail_split(gpu, tile, tile_table):
     """A one-workgroup-per-CU tile whose last round of tiles would fill at most half of the CUs runs the

@@ -368,6 +368,16 @@ __device__ __forceinline__ void tile_coords(uint32_t pid, uint32_t tiles_m, uint
 // the conflict-free minimum. f depends only on r & 15, so fragments 32 rows apart differ by a
 // constant offset.
 __device__ __forceinline__ int swz_f(int row) { return (row >> 2) & 3; }
+
+// CONVM 3: haloed pixels (a multiple of 16) one halo buffer of a tile with BN columns, S weight stages and
+// NW waves holds: what the LDS leaves after the weight stages and the sink, and what the loads can carry
+// in the (10 - S) slices of a channel slice that may load the next one (one 16-pixel instruction per wave
+// per slice).
+__host__ __device__ constexpr int conv_halo_max(int bn, int s, int nw) {
+  const int by_lds = ((160 * 1024 - s * bn * 64 - 1024) / (2 * 64)) / 16 * 16;
+  const int by_loads = (10 - s) * nw * 16;
+  return by_lds < by_loads ? by_lds : by_loads;
+}
 __device__ __forceinline__ int swz(int row, int chunk) { return (row << 6) + ((chunk ^ swz_f(row)) << 4); }
 
 
@@ -439,11 +449,22 @@ struct PinTwo {
 // barriers; at the end groups 1 .. KG-1 leave their accumulators in LDS and group 0 adds them before
 // the epilogue. It multiplies the loads in flight and the MFMA streams of a tile for shapes with few
 // tiles and deep K (integer sums are exact in any order).
+// f(std::integral_constant<int, I>{}) for I = I0 .. N - 1, unrolled at compile time
+template <int I0, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I0 < N) {
+    f(std::integral_constant<int, I0>{});
+    static_for<I0 + 1, N>(f);
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int S, int CONVM, int EPI, bool KFULL, int KG = 1, bool PP = false>
 __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t* __restrict__ a, int64_t lda,
                                                                const int8_t* __restrict__ w, int64_t ldw, int64_t M,
                                                                int64_t N, int64_t K, ConvGeom cg, EpiArgs e) {
-  constexpr bool CONV = CONVM != 0;      // CONVM: 0 GEMM, 1 conv with C_pad % 64 == 0, 2 any C_pad
+  // CONVM: 0 GEMM, 1 conv with C_pad % 64 == 0, 2 any C_pad, 3 conv from a haloed input tile (below)
+  constexpr bool CONV = CONVM != 0;
+  constexpr bool HALO = CONVM == 3;
   constexpr int BK = 64;
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
@@ -452,12 +473,20 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
   constexpr int IW = BN / 16 / NW;
   static_assert(FM >= 1 && FN >= 1, "wave tile below 32 x 32");
   static_assert(IA >= 1 && IW >= 1 && BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "tile / wave mismatch");
-  constexpr int STAGE = (BM + BN) * BK;
-  static_assert(S >= 2 && KG >= 1 && KG * S * STAGE <= 160 * 1024, "LDS stages");
-  constexpr int NDMA = IA + IW;
+  // CONVM 3: the K slices are (64-channel slice, tap) pairs, taps inner. The stages hold only the weight
+  // slices; the tile's input pixels plus a one-pixel border ("halo"), one channel slice at a time, sit in
+  // two halo buffers after them (the slice being read, the next one being loaded), then a 1 KB sink for
+  // the halo loads that carry nothing. Each input byte is loaded once per channel slice instead of once
+  // per tap.
+  static_assert(!HALO || (KG == 1 && !PP), "the haloed conv runs one K group, no ping-pong");
+  constexpr int STAGE = HALO ? BN * BK : (BM + BN) * BK;
+  constexpr int HMAX = HALO ? conv_halo_max(BN, S, NW) : 0;   // haloed pixels a buffer holds
+  constexpr int LDS_BYTES = HALO ? S * STAGE + 2 * HMAX * BK + 1024 : KG * S * STAGE;
+  static_assert(S >= 2 && KG >= 1 && LDS_BYTES <= 160 * 1024, "LDS stages");
+  constexpr int NDMA = HALO ? IW + 1 : IA + IW;   // CONVM 3: the weight slice and one halo instruction
   static_assert((S - 1) * NDMA <= 63, "vmcnt range");
 
-  __shared__ __attribute__((aligned(1024))) int8_t lds_all[KG * S * STAGE];
+  __shared__ __attribute__((aligned(1024))) int8_t lds_all[LDS_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -506,8 +535,10 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
   int py[IA], px[IA];
   (void)py;
   (void)px;
+  (void)oa;
+  (void)ca;
 #pragma unroll
-  for (int j = 0; j < IA; ++j) {
+  for (int j = 0; j < (HALO ? 0 : IA); ++j) {
     const int row = (wave * IA + j) * 16 + lrow;
     ca[j] = pch ^ swz_f(row);
     const int64_t m = m0 + row;
@@ -530,6 +561,65 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
     cw[j] = pch ^ swz_f(row);
     const int64_t n = n0 + row;
     ow[j] = n < N ? (uint32_t)(n * ldw + cw[j] * 16) : OOB;
+  }
+
+  // CONVM 3: the tile is rt whole image rows of wt pixels (or, for rows wider than the tile, a wt-pixel
+  // segment of one row) inside one image (the launcher checks); its halo is (rt + 2) x (wt + 2) pixels,
+  // haloed pixel hp = (row + 1) * hw_halo + col + 1 for tile pixel (row, col). hp0[i]: the haloed pixel of
+  // this lane's fragment row in MFMA row block i, before the tap's offset dy * hw_halo + dx.
+  // All of it in 32-bit arithmetic (the launch's bytes stay below 2^31); the slice bookkeeping runs on the
+  // scalar unit every slice, where 64-bit divisions would cost more issue slots than the MFMAs leave.
+  int h_y0 = 0, h_x0 = 0, hw_halo = 0, hp_n = 0, h_nq = 0;
+  uint32_t h_px0 = 0, h_ncs = 0;           // first pixel of the tile's image; channel slices
+  int hp0[HALO ? FM : 1];
+  (void)h_y0;
+  (void)h_x0;
+  (void)hw_halo;
+  (void)hp_n;
+  (void)h_nq;
+  (void)h_px0;
+  (void)h_ncs;
+  (void)hp0;
+  if constexpr (HALO) {
+    const uint32_t ipx = (uint32_t)(cg.h * cg.w);
+    const uint32_t gp0 = (uint32_t)(cg.m0 + m0);
+    const uint32_t img = gp0 / ipx;
+    h_px0 = img * ipx;
+    const uint32_t p0 = gp0 - h_px0;
+    h_y0 = (int)(p0 / (uint32_t)cg.w);
+    h_x0 = (int)(p0 - (uint32_t)h_y0 * (uint32_t)cg.w);
+    const int wt = (int)min<int64_t>(cg.w, BM);
+    hw_halo = wt + 2;
+    hp_n = (BM / wt + 2) * hw_halo;
+    h_nq = (hp_n + 15) / 16;
+    h_ncs = (uint32_t)(cg.c_pad / BK);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int p = wm * TM + i * 32 + (lane & 31);
+      const int prow = p / wt;
+      hp0[i] = (prow + 1) * hw_halo + (p - prow * wt) + 1;
+    }
+  }
+  int8_t* const halo = lds_all + S * STAGE;          // CONVM 3: buffer b at halo + b * HMAX * BK
+  int8_t* const halo_sink = halo + 2 * HMAX * BK;
+  (void)halo;
+  (void)halo_sink;
+  // CONVM 3: halo slot jj of this wave is load instruction q = jj * NW + wave of a channel slice's halo: lane l
+  // fills physical chunk l % 4 of haloed pixel 16 q + l / 4 with its logical chunk (l % 4) ^ f(pixel).
+  // hsrc[jj]: that lane's source byte offset less the channel slice's, OOB for pixels outside the image (the
+  // conv's zero padding) or past the halo (an offset past OOB is still past the buffer's end).
+  uint32_t hsrc[HALO ? 10 - S : 1];
+  (void)hsrc;
+  if constexpr (HALO) {
+#pragma unroll
+    for (int jj = 0; jj < 10 - S; ++jj) {
+      const int hp = 16 * (jj * NW + wave) + lrow;
+      const int hy = hp / hw_halo;
+      const int y = h_y0 - 1 + hy, x = h_x0 - 1 + (hp - hy * hw_halo);
+      const bool ok = hp < hp_n && (uint32_t)y < (uint32_t)cg.h && (uint32_t)x < (uint32_t)cg.w;
+      hsrc[jj] = ok ? (h_px0 + (uint32_t)(y * (int)cg.w + x)) * (uint32_t)cg.c_pad + (uint32_t)((pch ^ swz_f(hp)) * 16)
+                    : OOB;
+    }
   }
 
   // The cross-workgroup K split (int8 GEMM tiles of at most 64 x 64): workgroup blockIdx.y of the tile
@@ -628,6 +718,23 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
     for (int j = 0; j < FN; ++j)
       fw[set][j] = *reinterpret_cast<const i32x4*>(stage + BM * BK + swz(wn * TN + j * 32 + frow, ks * 2 + fk));
   };
+  // CONVM 3: the input fragment of a slice comes from its channel slice's halo buffer hb, each row at its
+  // haloed pixel moved by the tap (dy, dx): toff = dy * hw_halo + dx
+  auto read_halo = [&](const int8_t* stage, const int8_t* hb, int ks, int set, int toff) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      fa[set][i] = *reinterpret_cast<const i32x4*>(hb + swz(hp0[i] + toff, ks * 2 + fk));
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      fw[set][j] = *reinterpret_cast<const i32x4*>(stage + swz(wn * TN + j * 32 + frow, ks * 2 + fk));
+  };
+  // CONVM 3: the weight slice of (channel slice cs, tap) into a stage (zeros past the last channel slice)
+  auto dma_w_tap = [&](int8_t* stage, uint32_t cs, int tap) {
+    const bool live = cs < h_ncs;
+    const uint32_t k0 = live ? (uint32_t)tap * (uint32_t)cg.c_pad + cs * BK : 0u;
+#pragma unroll
+    for (int j = 0; j < IW; ++j) dma16(rw_rsrc, live ? ow[j] : OOB, stage + ((wave * IW + j) << 10), k0);
+  };
 
   constexpr bool BFE = epi_bf(EPI);       // bf16 operands, float accumulators
   using AccT = std::conditional_t<BFE, f32x16, i32x16>;
@@ -692,6 +799,72 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
       cur_s = cur_s + 1 == S ? 0 : cur_s + 1;
     }
     if (grp == 0) __builtin_amdgcn_s_barrier();
+  } else if constexpr (HALO) {
+    // The schedule of the loop below, one channel slice c per iteration with its nine taps unrolled, so the
+    // tap's offsets and the halo slot each tap carries are compile-time constants. In tap t of channel slice
+    // c (slice 9 c + t) the DMA issues slice 9 c + t + S's weights and, for t <= 9 - S, halo slot t of
+    // channel slice c + 1 into buffer (c + 1) & 1 (last read by channel slice c - 1, whose reads every wave
+    // finished before the first barrier of channel slice c); other taps issue one load into the sink, so
+    // every slice issues NDMA loads. The last slot rides on slice 9 c + 9's DMA, so the wait before that
+    // slice's first read covers the whole halo.
+    constexpr int NMF = FM * FN, NRD = FM + FN;
+    const int8_t* const hb0 = halo;
+    const int8_t* const hb1 = halo + HMAX * BK;
+    // prologue: the halo of channel slice 0, then taps 0 .. S-1 into stages 0 .. S-1; wait for tap 0
+#pragma unroll
+    for (int jj = 0; jj < 10 - S; ++jj) {
+      const int q = jj * NW + wave;
+      if (q < h_nq) dma16(ra_rsrc, hsrc[jj], halo + (q << 10));
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      dma_w_tap(lds + s * STAGE, 0u, s);
+      dma16(ra_rsrc, OOB, halo_sink);
+    }
+    wait_vmcnt<(S - 1) * NDMA>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read_halo(lds, hb0, 0, 0, -hw_halo - 1);
+    int cur_s = 0;
+    for (uint32_t c = 0; c < h_ncs; ++c) {
+      const int8_t* const hb = (c & 1u) ? hb1 : hb0;
+      const int8_t* const hbn = (c & 1u) ? hb0 : hb1;
+      // 256-row tiles: hw_halo through an empty asm each iteration, so the nine taps' fragment addresses are
+      // computed where they are read instead of being kept live across the loop (9 x FM registers more than
+      // such a tile has left); smaller tiles keep them
+      int hw = hw_halo;
+      if constexpr (FM * FN >= 8) asm volatile("" : "+s"(hw));
+      static_for<0, 9>([&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        constexpr int tn = (t + S) % 9, cn = (t + S) / 9;   // the slice this tap's DMA issues
+        constexpr int t1 = (t + 1) % 9;                      // the next slice's tap
+        int8_t* cur = lds + cur_s * STAGE;
+        const int nxt_s = cur_s + 1 == S ? 0 : cur_s + 1;
+        const int8_t* nxt = lds + nxt_s * STAGE;
+        // step 0
+        read_halo(cur, hb, 1, 1, (t / 3 - 1) * hw + (t % 3 - 1));
+        mfmas(0);
+        PinGroups<SG_DS_READ, NRD, NMF, 0>::emit();
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt_lgkm0<(S - 2) * NDMA>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // step 1
+        dma_w_tap(cur, c + cn, tn);
+        if constexpr (t <= 9 - S) {
+          const int q = t * NW + wave;
+          const bool on = c + 1u < h_ncs && q < h_nq;
+          dma16(ra_rsrc, on ? hsrc[t] + (c + 1u) * BK : OOB, on ? (int8_t*)hbn + (q << 10) : halo_sink);
+        } else {
+          dma16(ra_rsrc, OOB, halo_sink);
+        }
+        read_halo(nxt, t == 8 ? hbn : hb, 0, 0, (t1 / 3 - 1) * hw + (t1 % 3 - 1));
+        mfmas(1);
+        PinTwo<SG_VMEM_READ, NDMA, SG_DS_READ, NRD, NMF>::emit();
+        __builtin_amdgcn_sched_barrier(0);
+        cur_s = nxt_s;
+      });
+    }
   } else {
   // prologue: the group's slices 0 .. S-1 into stages 0 .. S-1, then wait for slice 0
 #pragma unroll
@@ -737,7 +910,7 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
   // reads), read back CW consecutive columns per lane, eight lanes per row: each store instruction
   // writes whole 8-row pieces of 32 * CB contiguous columns (full 128-byte lines for bf16 with CB 2).
   constexpr int PITCH = 32 * CB * 4 + 16;
-  static_assert(NW * 32 * PITCH <= S * STAGE, "staging does not fit in LDS");
+  static_assert(NW * 32 * PITCH <= (HALO ? LDS_BYTES : S * STAGE), "staging does not fit in LDS");
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();                       // every wave is done with the K-loop's LDS stages
   if constexpr (KG > 1) {
@@ -1390,7 +1563,14 @@ int launch_tiles_once(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw
   else mm_tile_kernel<BM_, BN_, WM_, WN_, S_, CONVM, EPI, false, KG_><<<grid, WM_ * WN_ * KG_ * 64, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
 #define XDNA_TILE_W(BM_, BN_, WM_, WN_, S_) XDNA_TILE_WK(BM_, BN_, WM_, WN_, S_, 1)
 #define XDNA_TILE(BM_, BN_, S_) XDNA_TILE_W(BM_, BN_, 2, 2, S_)
-  if (tile == T_256x256PP) {
+  if constexpr (CONVM == 3) {
+    // the haloed conv: the 8-wave 256 x 256 tile (3 stages) and, for tails, the 8-wave 128 x 256 (4 stages)
+    if (tile == T_256x256W8) {
+      XDNA_TILE_W(256, 256, 2, 4, 3)
+    } else {
+      XDNA_TILE_W(128, 256, 2, 4, 4)
+    }
+  } else if (tile == T_256x256PP) {
     // the ping-pong schedule: 4 stages (S - 2 = 2 slices between a DMA and its use)
     if (kfull) mm_tile_kernel<256, 256, 2, 4, 4, CONVM, EPI, true, 1, true><<<grid, 512, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
     else mm_tile_kernel<256, 256, 2, 4, 4, CONVM, EPI, false, 1, true><<<grid, 512, 0, st>>>(a, lda, w, ldw, M, N, K, cg, e);
@@ -1482,6 +1662,19 @@ TilePlan plan_tiles(int kind, int64_t M, int64_t N, int64_t kbytes, int64_t ktab
   return TilePlan{tile, m1, tail};
 }
 
+// The conv's loader for a tile: 3 (haloed input tile) for the 8-wave 256 x 256 and 128 x 256 tiles when a
+// tile is whole image rows (or a segment of one row) inside one image and its halo fits a buffer; else 1
+// (one tap per K slice: C_pad a multiple of the tile's K groups' 64-channel slices), else 2.
+int conv_mode(int tile, int64_t h, int64_t w, int64_t c_pad) {
+  const TileCfg t = tile_cfg(tile);
+  const int s = tile == T_256x256W8 ? 3 : tile == T_128x256W8 ? 4 : 0;
+  if (s != 0 && c_pad % 64 == 0 && (w <= t.bm ? (t.bm % w == 0 && h % (t.bm / w) == 0) : (w % t.bm == 0))) {
+    const int64_t wt = std::min<int64_t>(w, t.bm);
+    if ((t.bm / wt + 2) * (wt + 2) <= conv_halo_max(t.bn, s, t.waves)) return 3;
+  }
+  return c_pad % (64 * t.kg) == 0 ? 1 : 2;
+}
+
 template <int CONVM, int EPI>
 int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                  ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
@@ -1497,10 +1690,13 @@ int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
   else at += m1 * lda;
   // the conv's NCHW dequantized output is addressed by the pixel offset in its geometry (ct.m0)
   const EpiArgs et = (CONVM != 0 && e.dq_out) ? e : shift_epi(e, out_bytes<EPI>(), m1, 0);
-  // the tail's tile may split K over groups: CONVM 1 needs c_pad to be a multiple of its groups' slices
+  // the tail's tile has its own conv loader (it may split K over groups, or not take the halo)
   if constexpr (CONVM != 0) {
-    if (cg.c_pad % (64 * tile_cfg(p.tail).kg) != 0)
-      return launch_tiles_once<2, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, p.tail, st);
+    switch (conv_mode(p.tail, cg.h, cg.w, cg.c_pad)) {
+      case 3: return launch_tiles_once<3, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, p.tail, st);
+      case 1: return launch_tiles_once<1, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, p.tail, st);
+      default: return launch_tiles_once<2, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, p.tail, st);
+    }
   }
   return launch_tiles_once<CONVM, EPI>(at, lda, w, ldw, M - m1, N, K, ct, et, p.tail, st);
 }
@@ -1626,10 +1822,12 @@ int launch_conv(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad
     if (e.dq_out) eb.px0 = e.px0 + b0 * h * w;   // NCHW output: addressed by global pixel, not by row
     else eb = shift_epi(e, 1, b0 * h * w, 0);
     const int8_t* xb = x + b0 * per_img;
-    // the running tap counters of CONVM 1 step by KG slices of 64 channels
-    int rc = (c_pad % (64 * tile_cfg(tile).kg) == 0)
-                 ? launch_tiles<1, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st)
-                 : launch_tiles<2, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st);
+    // the haloed input tile where the tile allows it; the running tap counters of CONVM 1 step by KG
+    // slices of 64 channels
+    const int mode = conv_mode(tile, h, w, c_pad);
+    int rc = mode == 3   ? launch_tiles<3, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st)
+             : mode == 1 ? launch_tiles<1, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st)
+                         : launch_tiles<2, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st);
     if (rc) return rc;
   }
   return XDNA_OK;
