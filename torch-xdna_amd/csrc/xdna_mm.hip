@@ -279,17 +279,47 @@ __device__ __forceinline__ void epilogue_rqdq_each(const EpiArgs& e, int64_t hw,
   }
 }
 
-// The conv's requantize fused with the op's dequantize: four consecutive output pixels m .. m+3 (launch
-// rows) of channel n, int32 sums in a[]. Each is requantized as EPI_REQUANT does, then dequantized as the
-// separate dequantize kernel does, y = (float)q * (scale[n] * sx[image]) (+ bias[n]), and stored NCHW in
-// dtype e.dq_out - 1: one 16-byte (float32) or 8-byte store when the four pixels lie in one image at an
-// aligned position, else per element.
-__device__ __forceinline__ void epilogue_rqdq(const EpiArgs& e, const ConvGeom& cg, int64_t m, int64_t n, int64_t M,
-                                              int64_t N, const int32_t (&a)[4], float fo, float bo) {
-  if (n >= N || m >= M) return;
+// Where four consecutive output pixels m .. m+3 (launch rows) of the fused dequantize go: image b and pixel p
+// within it, and whether the four lie in one image at an aligned position (then one vector store per channel,
+// with the image's scale sx). The same for every channel, so the caller finds it once per four pixels. b_c /
+// sx_c: an image index and its scale the caller loaded ahead (the image of the wave's first pixel), used
+// instead of a load of e.sx[b] when the pixels lie in that image. Rows past M: fast = false, nothing loaded.
+struct RqPix {
+  int64_t b, p;
+  float sx;
+  bool fast;
+};
+
+__device__ __forceinline__ RqPix rq_pixel(const EpiArgs& e, const ConvGeom& cg, int64_t m, int64_t M, int64_t b_c,
+                                          float sx_c) {
+  RqPix r{0, 0, 0.0f, false};
+  if (m >= M) return r;
   const int64_t hw = cg.h * cg.w;
   const int64_t gp = e.px0 + cg.m0 + m;  // global pixel of the first of the four
-  const int64_t b = gp / hw, p = gp - b * hw;
+  // a 32-bit division where the pixel index allows (a 64-bit one costs several times the instructions)
+  if (gp <= 0xffffffffll && hw <= 0xffffffffll) {
+    const uint32_t bb = (uint32_t)gp / (uint32_t)hw;
+    r.b = bb;
+    r.p = gp - (int64_t)bb * hw;
+  } else {
+    r.b = gp / hw;
+    r.p = gp - r.b * hw;
+  }
+  r.fast = m + 3 < M && r.p + 3 < hw && (r.p % 4) == 0 && hw % 4 == 0;
+  if (r.fast) r.sx = r.b == b_c ? sx_c : e.sx[r.b];
+  return r;
+}
+
+// The conv's requantize fused with the op's dequantize: four consecutive output pixels m .. m+3 (launch
+// rows, placed by rq_pixel) of channel n, int32 sums in a[]. Each is requantized as EPI_REQUANT does, then
+// dequantized as the separate dequantize kernel does, y = (float)q * (scale[n] * sx[image]) (+ bias[n]),
+// and stored NCHW in dtype e.dq_out - 1: one 16-byte (float32) or 8-byte store when the four pixels lie in
+// one image at an aligned position, else per element.
+__device__ __forceinline__ void epilogue_rqdq(const EpiArgs& e, const ConvGeom& cg, const RqPix& px, int64_t m,
+                                              int64_t n, int64_t M, int64_t N, const int32_t (&a)[4], float fo,
+                                              float bo) {
+  if (n >= N || m >= M) return;
+  const int64_t hw = cg.h * cg.w;
   const int half = 1 << (e.shift - 1);
   float v[4];
 #pragma unroll
@@ -298,12 +328,13 @@ __device__ __forceinline__ void epilogue_rqdq(const EpiArgs& e, const ConvGeom& 
     q = e.relu ? min(max(q, 0), 255) : min(max(q, -128), 127);
     v[r] = (float)q;
   }
-  if (!(m + 3 < M && p + 3 < hw && (p % 4) == 0 && hw % 4 == 0)) {
-    epilogue_rqdq_each(e, hw, b, p, m, n, M, N, v, fo, bo);
+  if (!px.fast) {
+    epilogue_rqdq_each(e, hw, px.b, px.p, m, n, M, N, v, fo, bo);
     return;
   }
+  const int64_t b = px.b, p = px.p;
   const int dt = e.dq_out - 1;
-  const float f = fo * e.sx[b];
+  const float f = fo * px.sx;
   float t[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -1013,9 +1044,34 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
   const bool rqdq = RQDQ && e.dq_out != 0;
   const int dquad = lane & 7;            // the lane's four pixels: 4 * dquad .. + 3 of the block
   const int dch = lane >> 3;             // the lane's channel within each group of eight
+  // the fused dequantize's per-image scale of the wave's first pixel (its last rows may lie past M: the
+  // first pixel is clamped into the launch), loaded once instead of once per four outputs
+  int64_t rq_b = 0;
+  float rq_sx = 0.0f;
+  if constexpr (RQDQ) {
+    if (rqdq) {
+      const int64_t hw = cg.h * cg.w;
+      rq_b = (e.px0 + cg.m0 + min(m0 + wm * TM, M - 1)) / hw;
+      rq_sx = e.sx[rq_b];
+    }
+  }
+  (void)rq_b;
+  (void)rq_sx;
 #pragma unroll
   for (int jp = 0; jp < FN / CB; ++jp) {
     const int64_t n = n0 + wn * TN + jp * 32 * CB + cq * CW;
+    // the fused dequantize's weight scale and bias of column block jp: lane l holds those of channel l % COLS
+    // (all loaded at once); the rolled loop below takes its channel's from the holding lane
+    float rq_fo = 0.0f, rq_bo = 0.0f;
+    if constexpr (RQDQ) {
+      if (rqdq) {
+        const int64_t nl = min<int64_t>(n0 + wn * TN + jp * COLS + (lane % COLS), N - 1);
+        rq_fo = e.sw[nl];
+        rq_bo = e.bias ? e.bias[nl] : 0.0f;
+      }
+    }
+    (void)rq_fo;
+    (void)rq_bo;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -1031,17 +1087,18 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
         if constexpr (RQDQ) {
           // a rolled loop: it indexes only LDS and addresses, and unrolled (with every tile's blocks) the
           // epilogue would outgrow full unrolling of the accumulator loops
+          const int64_t mq = m0 + wm * TM + i * 32 + 4 * dquad;   // the lane's four pixels
+          const RqPix px = rq_pixel(e, cg, mq, M, rq_b, rq_sx);
 #pragma unroll 1
           for (int g8 = 0; g8 < COLS / 8; ++g8) {
             const int col = 8 * g8 + dch;
             const int64_t nd = n0 + wn * TN + jp * COLS + col;
-            const int64_t nc = min(nd, N - 1);
-            const float fo = e.sw[nc];
-            const float bo = e.bias ? e.bias[nc] : 0.0f;
+            const float fo = __shfl(rq_fo, col, 64);    // e.sw[min(nd, N - 1)]
+            const float bo = __shfl(rq_bo, col, 64);
             int32_t a4[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) a4[r] = *reinterpret_cast<const int32_t*>(stg + (4 * dquad + r) * PITCH + col * 4);
-            epilogue_rqdq(e, cg, m0 + wm * TM + i * 32 + 4 * dquad, nd, M, N, a4, fo, bo);
+            epilogue_rqdq(e, cg, px, mq, nd, M, N, a4, fo, bo);
           }
         }
       } else {
