@@ -1085,11 +1085,12 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
       }
       if (rqdq) {
         if constexpr (RQDQ) {
-          // a rolled loop: it indexes only LDS and addresses, and unrolled (with every tile's blocks) the
-          // epilogue would outgrow full unrolling of the accumulator loops
+          // unrolled by four, not fully: four channels' LDS reads and shuffles go out together (a rolled loop
+          // waited on them once per channel), and fully unrolled (with every tile's blocks) the epilogue would
+          // outgrow full unrolling of the accumulator loops
           const int64_t mq = m0 + wm * TM + i * 32 + 4 * dquad;   // the lane's four pixels
           const RqPix px = rq_pixel(e, cg, mq, M, rq_b, rq_sx);
-#pragma unroll 1
+#pragma unroll 4
           for (int g8 = 0; g8 < COLS / 8; ++g8) {
             const int col = 8 * g8 + dch;
             const int64_t nd = n0 + wn * TN + jp * COLS + col;
