@@ -73,6 +73,9 @@ def parse():
     ap.add_argument("--operands", default="randn", choices=["randn", "zeros"],
                     help="zeros: all-zero activations and weights on the GEMM workloads (a diagnostic of the power "
                          "limit: the same work with the least switching; never the reported configuration)")
+    ap.add_argument("--fq", default="off", choices=["on", "off"],
+                    help="on: the quantize inside the GEMM launch (xdna_linear_fq) where it applies (rows up to "
+                         "1024); measured slower than the two launches, so off by default")
     ap.add_argument("--tile", default=None,
                     help="force this tile (a kernels.TILES name) on every GEMM shape of the c1/c2/c5/decode "
                          "workloads instead of the built-in rule and the tuned table (results do not depend on it)")
@@ -109,17 +112,34 @@ def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed
     return sets
 
 
+FQ = {"on": False}     # the fused-quantize launch where it applies (--fq on)
+_fq_shapes = {}       # (M, N, K, dtype) -> whether xdna_linear_fq takes the shape
+
+
+def fq_taken(M, N, K, dtype):
+    return bool(FQ["on"] and _fq_shapes.get((M, N, K, dtype)))
+
+
 def run_gemm_step_split(items, ev=None):
     """One step ordered as all activation quantizes, then all fused GEMMs (the same work as
     quantize -> GEMM per shape); ev = three events recorded at the start, between the two groups and
-    at the end, so ev[1] -> ev[2] brackets exactly the step's GEMM launches, back to back."""
+    at the end, so ev[1] -> ev[2] brackets exactly the step's GEMM launches, back to back. Shapes the
+    fused-quantize launch takes (rows up to 1024) run as that one launch in the GEMM group and have no
+    quantize in the first (a shape's first step finds out which, in the warm-up)."""
     if ev:
         ev[0].record()
-    qs = [kernels.quant_rows(x) for x, *_ in items]
+    qs = [None if (FQ["on"] and _fq_shapes.get((M, N, K, x.dtype), True)) else kernels.quant_rows(x)
+          for x, wq, sw, b, M, N, K in items]
     if ev:
         ev[1].record()
-    for (x, wq, sw, b, M, N, K), (xq, sx) in zip(items, qs):
-        kernels.mm_i8_dequant(xq, sx, wq, sw, b, x.dtype)
+    for (x, wq, sw, b, M, N, K), q in zip(items, qs):
+        if q is None:
+            y = kernels.linear_fq(x, wq, sw, b)
+            _fq_shapes[(M, N, K, x.dtype)] = y is not None
+            if y is not None:
+                continue
+            q = kernels.quant_rows(x)
+        kernels.mm_i8_dequant(q[0], q[1], wq, sw, b, x.dtype)
     if ev:
         ev[2].record()
 
@@ -218,6 +238,7 @@ def cpu_baseline_conv(n, c, h, w, layers, sample, relu=True, budget_s=20.0):
 # ------------------------------------------------------------------------------ main
 def main():
     a = parse()
+    FQ["on"] = a.fq == "on"
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}); "
               "run with --gpus 1", file=sys.stderr)
@@ -335,6 +356,14 @@ def per_shape_us(sets, launches=10):
         ncopies = max(len(sets), min(64, -(-(MALL_BYTES + (64 << 20)) // wbytes)))
         launches = max(launches, ncopies)
         weights = [sets[i][j][1] if i < len(sets) else sets[0][j][1].clone() for i in range(ncopies)]
+        x0, _, _, _, M0, N0, K0 = sets[0][j]
+        if fq_taken(M0, N0, K0, x0.dtype):     # the one fused-quantize launch (it reads the float rows)
+            calls = []
+            for i in range(launches):
+                x, wq, sw, b, M, N, K = sets[i % len(sets)][j]
+                calls.append(lambda x=x, w=weights[i % ncopies], sw=sw, b=b: kernels.linear_fq(x, w, sw, b))
+            out.append(back_to_back_us(calls, launches))
+            continue
         for i in range(launches):
             x, wq, sw, b, M, N, K = sets[i % len(sets)][j]
             ops.append((kernels.quant_rows(x), weights[i % ncopies], sw, b, x.dtype))
@@ -403,11 +432,16 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
     xb = x_dtype.itemsize
     nshape = len(shapes)
     g_sec = sum(g_ms) / 1e3                            # GEMM launches of the timed steps
-    g_bytes = sum(gemm_bytes(M, N, K, xb, yb, bias) for M, N, K in shapes) * reps
-    q_bytes = sum(quant_bytes(M, K, xb) for M, N, K in shapes) * reps
+    fq = [fq_taken(M, N, K, x_dtype) for M, N, K in shapes]
+    # a fused-quantize launch also reads the float rows and writes their int8 copy and scales
+    launch_bytes = [gemm_bytes(M, N, K, xb, yb, bias) + (quant_bytes(M, K, xb) if f else 0)
+                    for (M, N, K), f in zip(shapes, fq)]
+    g_bytes = sum(launch_bytes) * reps
+    nq = sum(1 for f in fq if not f)
+    q_bytes = sum(quant_bytes(M, K, xb) for (M, N, K), f in zip(shapes, fq) if not f) * reps
     q_sec = sum(q_ms) / 1e3
     achieved = ops_step * reps / g_sec / 1e12
-    bound_us = sum(roofline_us(2 * M * N * K, gemm_bytes(M, N, K, xb, yb, bias)) for M, N, K in shapes)
+    bound_us = sum(roofline_us(2 * M * N * K, nb) for (M, N, K), nb in zip(shapes, launch_bytes))
     out = {"value": round(ops_step / sec / 1e12, 2), "ms_per_step": round(sec * 1e3, 4),
            "host_ms_per_step": round(host * 1e3, 4),
            "timing": "GPU time of K eager steps enqueued behind a gate and about 50 ms of untimed pre-heat "
@@ -415,7 +449,9 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
                      "step's quantizes then its GEMMs with events between; host_ms_per_step: the same "
                      "steps launched without a gate, wall clock",
            "config": {"workload": workload, "shapes_mnk": shapes, "x_dtype": str(x_dtype).replace("torch.", ""),
-                      "bias": bias, "rotating_sets": len(sets)},
+                      "bias": bias, "rotating_sets": len(sets),
+                      "quantize": "in the GEMM launch for the shapes listed in fused_quantize_shapes, else a launch of "
+                                  "its own (--fq on)" if FQ["on"] else "a launch of its own"},
            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(achieved / PEAK_INT8_TOPS, 4),
                         "traffic": None if a.tile or a.operands != "randn" else traffic(label.lower()),
@@ -424,8 +460,10 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
                         "alg_bytes_per_launch": round(g_bytes / (nshape * reps)),
                         "hbm_GBs_equiv": round(g_bytes / g_sec / 1e9, 1),
                         "frac_of_attainable": round(bound_us * reps / (g_sec * 1e6), 4)},
-           "quantize": {"achieved_GBs": round(q_bytes / q_sec / 1e9, 1), "peak": PEAK_HBM_GBS,
-                        "avg_launch_us": round(q_sec / (nshape * reps) * 1e6, 2)},
+           "quantize": None if nq == 0 else {"achieved_GBs": round(q_bytes / q_sec / 1e9, 1), "peak": PEAK_HBM_GBS,
+                                             "avg_launch_us": round(q_sec / (nq * reps) * 1e6, 2),
+                                             "launches": nq * reps},
+           "fused_quantize_shapes": [list(sh) for sh, f in zip(shapes, fq) if f],
            "per_shape": []}
     if bound == "hbm":
         gbs = g_bytes / g_sec / 1e9
@@ -434,7 +472,10 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
     for j, (M, N, K) in enumerate(shapes):
         t = per_shape[j] / 1e6
         b = gemm_bytes(M, N, K, xb, yb, bias)
-        out["per_shape"].append({"mnk": [M, N, K], "tile": kernels.gemm_variant(dev, M, N, kernels.round_up(K, 16)),
+        if fq[j]:
+            b += quant_bytes(M, K, xb)
+        tile = kernels.gemm_variant(dev, M, N, kernels.round_up(K, 16)) + ("+fq" if fq[j] else "")
+        out["per_shape"].append({"mnk": [M, N, K], "tile": tile,
                                  "us": round(t * 1e6, 2), "TOPS": round(2 * M * N * K / t / 1e12, 1),
                                  "GBs": round(b / t / 1e9, 1),
                                  "roofline_us": round(roofline_us(2 * M * N * K, b), 2)})

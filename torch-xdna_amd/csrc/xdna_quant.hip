@@ -46,23 +46,6 @@ int launch_status(const char* where) {
 }
 
 // ------------------------------------------------------------------------------ quant_rows
-// 16-byte vector of input elements: 8 x 16-bit or 4 x float32.
-template <int DT>
-struct Vec16 {
-  static constexpr int N = (DT == XDNA_F32) ? 4 : 8;
-  uint4 raw;
-  __device__ __forceinline__ float get(int i) const {
-    if constexpr (DT == XDNA_F32) {
-      const float* f = reinterpret_cast<const float*>(&raw);
-      return f[i];
-    } else {
-      const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
-      if constexpr (DT == XDNA_BF16) return bf16_bits_to_f32(h[i]);
-      else return f16_bits_to_f32(h[i]);
-    }
-  }
-};
-
 template <int TPR>
 __device__ __forceinline__ float group_max(float v, float* red) {
   v = wave_max(v);
@@ -79,40 +62,6 @@ __device__ __forceinline__ float group_max(float v, float* red) {
     for (int i = 1; i < W; ++i) m = fmaxf(m, red[i]);
     return m;
   }
-}
-
-// Row max |x| kept as magnitude bits: a float's magnitude orders like its bit pattern with the sign bit
-// cleared, NaN patterns above +inf, so an unsigned max finds max |x| and lets a NaN through (torch's
-// amax propagates NaN; a float max would drop it). bf16 / fp16 words hold two elements, which one
-// packed 16-bit max (v_pk_max_u16) compares at once; the float is formed once per row.
-template <int DT>
-struct AbsMaxBits {
-  uint32_t m = 0;                       // 16-bit types: two packed 16-bit maxima; float32: one
-  __device__ __forceinline__ void add(const Vec16<DT>& v) {
-    const uint32_t w[4] = {v.raw.x, v.raw.y, v.raw.z, v.raw.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (DT == XDNA_F32) {
-        m = max(m, w[i] & 0x7fffffffu);
-      } else {
-        typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-        m = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, m),
-                                                                   __builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu)));
-      }
-    }
-  }
-  // this lane's magnitude bits (below 2^31: usable as int)
-  __device__ __forceinline__ int lane_bits() const {
-    if constexpr (DT == XDNA_F32) return (int)m;
-    else return (int)max(m & 0xffffu, m >> 16);
-  }
-};
-
-template <int DT>
-__device__ __forceinline__ float bits_to_abs(int b) {
-  if constexpr (DT == XDNA_F32) return __uint_as_float((uint32_t)b);
-  else if constexpr (DT == XDNA_BF16) return bf16_bits_to_f32((uint16_t)b);
-  else return f16_bits_to_f32((uint16_t)b);
 }
 
 // max |x| over the row's TPR threads (one wave, or the whole block through LDS), as a float.
