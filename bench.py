@@ -155,7 +155,7 @@ def quant_bytes(M, K, xbytes):
 
 # ------------------------------------------------------------------------------ CPU baseline
 def cpu_model():
-    """The host CPU's model string (BASELINE.md asks for it beside every CPU number)."""
+    """The host CPU's model string, reported beside every CPU number."""
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
