@@ -169,25 +169,6 @@ int xdna_gemm_i8_dequant_ws(const int8_t* a, int64_t lda, const float* sx, const
                             const float* sw, const float* bias, void* y, int y_dtype, int64_t ldy,
                             int64_t m, int64_t n, int64_t k, void* ws, int64_t ws_bytes, void* stream);
 
-/* The whole W8A8 linear of xdna::linear / linear_cat (torch_xdna/runtime.py:326-355, :402-434: the
- * activation quantize of runtime.py:366-368, the int8 GEMM, the dequantize of :350-353) in ONE launch,
- * for short activations: the launch's first workgroups quantize x [m, k] (x_dtype, row stride ldx
- * elements; the output y has the same dtype) into xq [m, k] (row stride k) and sx [m], exactly as
- * xdna_quant_rows does, and the GEMM's workgroups wait for the rows they use, then compute y as
- * xdna_gemm_i8_dequant does (same results bit for bit). flags: device memory of at least
- * xdna_linear_fq_flag_bytes(m) bytes, zero before its first use (calls only ever write launch-unique
- * nonzero tags into it and leave word 0 zero unless a wait timed out); calls sharing it must be ordered
- * (one stream); each call tags its flags anew, so a call must not be captured into a graph and replayed.
- * Returns XDNA_EUNSUPPORTED, with nothing launched, when the shape or layout has no fused form (m above
- * 1024, k not a multiple of 64 or above 4096, rows not 16-byte aligned, or a tile plan without it): then
- * call xdna_quant_rows and xdna_gemm_i8_dequant. On MI355X the two calls measured faster for every shape
- * this one takes (the in-launch handshake costs more than the separate quantize launch); torch_xdna's
- * route uses them. */
-int64_t xdna_linear_fq_flag_bytes(int64_t m);
-int xdna_linear_fq(const void* x, int x_dtype, int64_t ldx, int8_t* xq, float* sx, const int8_t* w, int64_t ldw,
-                   const float* sw, const float* bias, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
-                   uint32_t* flags, int64_t flag_bytes, void* stream);
-
 /* The bf16 GEMM of precision "bf16": y[m, n] = sum_k a[m, k] * w[n, k] with bf16 operands and float32
  * accumulation (+ bias[n] in float32), converted to y_dtype (XDNA_F32/BF16/F16, round to nearest
  * even). Replaces kernels.mm_bf16 (torch_xdna/kernels.py:167-169) behind runtime._npu_bf16 /

@@ -71,14 +71,6 @@ def test_argument_validation(lib):
     assert lib.xdna_conv3x3_i8(p, 1, 4, 4, 16, p, 8, 0, 0, p, None, None) == -1    # shift 0
     assert "shift" in lib.xdna_last_error().decode()
     assert lib.xdna_conv_quant_nhwc(p, 0, 1, 3, 4, 4, p, 8, p, p, None) == -1     # c_pad % 16
-    # the one-launch linear: bad arguments are XDNA_EINVAL; shapes outside its fused form XDNA_EUNSUPPORTED
-    # (-2) with nothing launched, the caller's cue to use the two calls
-    assert lib.xdna_linear_fq(p, 9, 64, p, p, p, 64, p, None, p, 64, 4, 64, 64, p, 64, None) == -1   # dtype
-    assert lib.xdna_linear_fq(p, 1, 64, None, p, p, 64, p, None, p, 64, 4, 64, 64, p, 64, None) == -1  # null
-    assert lib.xdna_linear_fq(p, 1, 4096, p, p, p, 4096, p, None, p, 64, 2000, 64, 4096, p, 64, None) == -2
-    assert "fused form" in lib.xdna_last_error().decode()
-    assert lib.xdna_linear_fq(p, 1, 1008, p, p, p, 1008, p, None, p, 64, 64, 64, 1008, p, 64, None) == -2
-    assert lib.xdna_linear_fq_flag_bytes(128) == 4 * 129
     # empty work is a no-op success
     assert lib.xdna_gemm_i8_i32(None, 16, None, 16, None, 16, 0, 4, 16, None) == 0
     assert lib.xdna_quant_rows(None, 0, 0, 16, 16, None, 16, 16, None, None) == 0

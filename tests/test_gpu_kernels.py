@@ -162,57 +162,6 @@ def test_gemm_dequant(gpu, out, m, n, k, bias):
     assert not bad.any(), f"{bad.sum()} of {got.size} differ, e.g. {got[bad][:4]} vs {want[bad][:4]}"
 
 
-FQ_SHAPES = [(128, 4096, 1024), (128, 6144, 1024), (128, 1024, 3072), (512, 4096, 1024), (512, 6144, 1024),
-             (512, 1024, 3072), (1024, 4096, 1024), (1024, 6144, 1024), (1024, 1024, 3072),   # C2 at M <= 1024
-             (65, 300, 64), (100, 2048, 1024), (129, 4096, 4096), (300, 520, 3072), (777, 4100, 1024),
-             (1000, 777, 2048)]
-
-
-@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("m,n,k", FQ_SHAPES)
-def test_linear_fq(gpu, dt, m, n, k):
-    """xdna_linear_fq (the activation quantize inside the GEMM launch) against the separate quantize +
-    fused-dequantize GEMM, bit for bit: y, the quantized rows and the row scales, with and without bias,
-    two calls in a row on one flag buffer (the second on other rows), no wait timed out. Ragged row and
-    column counts, every tile the rule picks for rows up to 1024, and the oracle on the smaller shapes."""
-    from torch_xdna import kernels
-
-    x = _rand((m, k), DT[dt], seed=m * 7 + n + k, outliers=1e-3)
-    wt = _rand((n, k), torch.float32, seed=m + n + k + 1, scale=0.02)
-    b = _rand((n,), torch.float32, seed=n + 3, scale=0.01).to(gpu)
-    wq, sw = kernels.quant_rows(wt.to(gpu))
-    for bias in (b, None):
-        for rows in (x, x.flip(0) * 0.5):
-            xg = rows.to(gpu)
-            xq = torch.empty((m, k), dtype=torch.int8, device=gpu)
-            sx = torch.empty((m,), dtype=torch.float32, device=gpu)
-            y = kernels.linear_fq(xg, wq, sw, bias, out=(xq, sx))
-            assert y is not None, kernels.gemm_variant(gpu, m, n, k)
-            xq_r, sx_r = kernels.quant_rows(xg)
-            want = kernels.mm_i8_dequant(xq_r, sx_r, wq, sw, bias, DT[dt])
-            assert torch.equal(xq, xq_r) and torch.equal(sx, sx_r)
-            assert y.dtype == want.dtype and torch.equal(y, want), f"{int((y != want).sum())} of {y.numel()} differ"
-    assert not kernels.fq_timeouts(gpu)
-    q_ref, s_ref = O.quant_rows(_f32(rows))          # the last call's rows against the oracle
-    assert np.array_equal(_np(xq), q_ref) and np.array_equal(_np(sx), s_ref)
-
-
-def test_linear_fq_unsupported(gpu):
-    """Shapes outside the fused form come back as None with nothing launched (the caller's separate path):
-    K above 4096 or not a multiple of 64, more than 1024 rows, and rows the small-M kernels take."""
-    from torch_xdna import kernels
-
-    wq, sw = kernels.quant_rows(torch.randn(300, 64, device=gpu))
-    assert kernels.linear_fq(torch.randn(1, 64, device=gpu), wq, sw, None) is None         # one-row kernel
-    assert kernels.linear_fq(torch.randn(40, 64, device=gpu), wq, sw, None) is None        # small-M kernel
-    wq, sw = kernels.quant_rows(torch.randn(256, 4160, device=gpu))
-    assert kernels.linear_fq(torch.randn(16, 4160, device=gpu), wq, sw, None) is None      # k > 4096
-    wq, sw = kernels.quant_rows(torch.randn(256, 1024, device=gpu))
-    assert kernels.linear_fq(torch.randn(2000, 1024, device=gpu), wq, sw, None) is None    # m > 1024
-    wq, sw = kernels.quant_rows(torch.randn(256, 1008, device=gpu))
-    assert kernels.linear_fq(torch.randn(64, 1008, device=gpu), wq, sw, None) is None      # k % 64 != 0
-
-
 @pytest.mark.parametrize("out", ["f32", "bf16", "f16"])
 def test_gemm_dequant_range(gpu, out):
     """Scales from 1e-45 to 3e38 put the fused epilogue's outputs in every float range (zero,

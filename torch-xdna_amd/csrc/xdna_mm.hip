@@ -80,18 +80,6 @@ struct EpiArgs {
   int32_t* part;        // [tiles * waves][ksplit][the wave's int32 accumulators in register order]
   void* ws;             // host side: the caller's workspace (counters, then partial sums), or null
   int64_t ws_bytes;
-  // Fused activation quantize (FQ kernels): workgroups 0 .. fq_wgs-1 quantize rows of fq_x [M, K] (the
-  // epilogue's output dtype, row stride fq_ldx elements) into the A operand and sx, fq_rows rows each, then
-  // set fq_flags[1 + wg] = fq_epoch; the other workgroups are the GEMM's tiles and wait for the flags of
-  // their rows (fq_flags[0] = 1 marks a wait that timed out)
-  const void* fq_x;
-  int64_t fq_ldx;
-  int8_t* fq_q;
-  float* fq_s;
-  uint32_t* fq_flags;
-  uint32_t fq_epoch;
-  int fq_wgs;
-  int fq_rows;
 };
 
 struct ConvGeom {
@@ -379,97 +367,6 @@ __device__ __forceinline__ void calib_flush(const EpiArgs& e, int calib) {
   }
 }
 
-// ------------------------------------------------------------------------------ fused quantize
-// The activation quantize of a small-M W8A8 linear inside its GEMM launch: the launch's first fq_wgs
-// workgroups quantize fq_rows rows each (one wave per row, the row in registers, the arithmetic of
-// quant_rows_wave_kernel: magnitude-bit max, scale max(amax, 1e-8) / 127, quant_pack) and publish their
-// rows with one flag; every GEMM workgroup waits for the flags of its rows before its first A load.
-// Visibility across the XCDs' L2 caches: the int8 rows and scales go out as agent-scope atomic stores
-// (write-through to the device-coherent level) and the flag after every one of them completed
-// (vmcnt 0, then a workgroup barrier); a GEMM workgroup reads the rows only after their flag, so its
-// caches hold no copy of them from this launch, and the caches' copies from earlier launches are
-// invalidated at the launch's start. Forward progress: the quantize workgroups have the lowest ids, so
-// they are dispatched before any GEMM workgroup that waits for them, and they wait for nothing; each wait
-// is still bounded (about 20 ms), and a wait that times out sets fq_flags[0] and goes on.
-template <int EPI>
-__device__ __forceinline__ void fq_quantize(const EpiArgs& e, int64_t K, int64_t M, int waves) {
-  constexpr int DT = EPI == EPI_DQ_F32 ? XDNA_F32 : EPI == EPI_DQ_BF16 ? XDNA_BF16 : XDNA_F16;
-  using V = Vec16<DT>;
-  constexpr int VEC = V::N;
-  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
-  constexpr int LPG = 16 / VEC;          // 16-byte loads per group of 16 elements
-  constexpr int G = 4;                    // groups of 16 per lane: rows of up to 4096 elements (the host checks)
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int ng = (int)(K / 16);           // K % 16 == 0
-  const int64_t r0 = (int64_t)blockIdx.x * e.fq_rows;
-  const int64_t r1 = min<int64_t>(M, r0 + e.fq_rows);
-  for (int64_t row = r0 + wave; row < r1; row += waves) {
-    const __amdgpu_buffer_rsrc_t rr =
-        make_rsrc(reinterpret_cast<const char*>(e.fq_x) + row * e.fq_ldx * ESZ, (uint32_t)(K * ESZ));
-    V v[G][LPG];
-#pragma unroll
-    for (int j = 0; j < G; ++j)
-#pragma unroll
-      for (int l = 0; l < LPG; ++l)
-        v[j][l].raw = buf_load_u4<false>(rr, (uint32_t)((lane + j * 64) * 16 * ESZ + l * 16));
-    AbsMaxBits<DT> am;
-#pragma unroll
-    for (int j = 0; j < G; ++j)
-#pragma unroll
-      for (int l = 0; l < LPG; ++l) am.add(v[j][l]);
-    const float sc = scale_from_amax(bits_to_abs<DT>(wave_max_i(am.lane_bits())));
-    const float rc = 1.0f / sc;
-    if (lane == 0)
-      __hip_atomic_store(reinterpret_cast<uint32_t*>(e.fq_s) + row, __builtin_bit_cast(uint32_t, sc), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t* qr = reinterpret_cast<uint32_t*>(e.fq_q + row * K);
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-      const int gi = lane + j * 64;
-      if (gi < ng) {
-        float f[16];
-#pragma unroll
-        for (int l = 0; l < LPG; ++l)
-#pragma unroll
-          for (int q = 0; q < VEC; ++q) f[l * VEC + q] = v[j][l].get(q);
-        uint32_t w[4];
-        quant_pack<16>(f, sc, rc, w);
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          __hip_atomic_store(qr + gi * 4 + t, w[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0)
-    __hip_atomic_store(e.fq_flags + 1 + blockIdx.x, e.fq_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// A GEMM workgroup of an FQ launch: wait until the quantize workgroups of rows [m_lo, m_hi) have published
-// them. Lanes of wave 0 poll one flag each (at most 64 chunks: the host checks), so one round trip covers
-// them all; bounded by about 20 ms of the 100 MHz real-time counter.
-__device__ __forceinline__ void fq_wait(const EpiArgs& e, int64_t m_lo, int64_t m_hi) {
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    const int64_t c0 = m_lo / e.fq_rows, c1 = (m_hi - 1) / e.fq_rows;
-    const int64_t c = c0 + lane;
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (true) {
-      const uint32_t f = c <= c1 ? __hip_atomic_load(e.fq_flags + 1 + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                 : e.fq_epoch;
-      if (__builtin_amdgcn_ballot_w64(f != e.fq_epoch) == 0) break;
-      if (__builtin_amdgcn_s_memrealtime() - t0 > 2000000ull) {
-        if (lane == 0) __hip_atomic_store(e.fq_flags, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-  }
-  __syncthreads();
-}
-
 // ------------------------------------------------------------------------------ tile engine
 // XCD-aware order: consecutive workgroup ids go round-robin over the 8 XCDs, so ids are remapped
 // to give each XCD a contiguous run of tiles, and runs are walked GROUP_M tile-rows at a time so
@@ -592,8 +489,7 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-template <int BM, int BN, int WM, int WN, int S, int CONVM, int EPI, bool KFULL, int KG = 1, bool PP = false,
-          bool FQ = false>
+template <int BM, int BN, int WM, int WN, int S, int CONVM, int EPI, bool KFULL, int KG = 1, bool PP = false>
 __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t* __restrict__ a, int64_t lda,
                                                                const int8_t* __restrict__ w, int64_t ldw, int64_t M,
                                                                int64_t N, int64_t K, ConvGeom cg, EpiArgs e) {
@@ -632,19 +528,9 @@ __global__ __launch_bounds__(WM * WN * KG * 64) void mm_tile_kernel(const int8_t
   int8_t* const lds = lds_all + kg * (S * STAGE);
 
   const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  uint32_t pid = blockIdx.x;
-  if constexpr (FQ) {
-    static_assert(CONVM == 0 && epi_dq(EPI) && !PP, "fused quantize: the int8 GEMM with the dequantize");
-    if (blockIdx.x < (uint32_t)e.fq_wgs) {   // workgroup-uniform: a quantize workgroup takes no part below
-      fq_quantize<EPI>(e, K, M, WM * WN * KG);
-      return;
-    }
-    pid = blockIdx.x - (uint32_t)e.fq_wgs;
-  }
   int64_t tm, tn;
-  tile_coords(pid, (uint32_t)tiles_m, (uint32_t)tiles_n, tm, tn);
+  tile_coords(blockIdx.x, (uint32_t)tiles_m, (uint32_t)tiles_n, tm, tn);
   const int64_t m0 = tm * BM, n0 = tn * BN;
-  if constexpr (FQ) fq_wait(e, m0, min<int64_t>(M, m0 + BM));
 
   // The epilogue's per-row and per-column scales do not depend on K: load them now, so they arrive
   // during the K loop. Read-back layout: row rr * 8 + (lane >> 3), columns 4 * (lane & 7) .. +3.
@@ -1847,59 +1733,6 @@ int conv_mode(int tile, int64_t h, int64_t w, int64_t c_pad) {
   return c_pad % (64 * t.kg) == 0 ? 1 : 2;
 }
 
-// The W8A8 linear with its activation quantize in the GEMM launch (FQ kernels), for the tiles the built-in
-// rule and the MI355X table give rows up to FQ_MAX_M: one launch of fq_wgs quantize workgroups (one row per
-// wave) and the tiles. XDNA_EUNSUPPORTED when the shape takes another plan (the caller then quantizes and
-// launches the GEMM separately, with the same results).
-constexpr int64_t FQ_MAX_M = 1024;
-std::atomic<uint32_t> g_fq_epoch{0};
-
-template <int EPI>
-int launch_gemm_fq(const void* x, int64_t ldx, int8_t* xq, float* sx, const int8_t* w, int64_t ldw, int64_t M,
-                   int64_t N, int64_t K, EpiArgs e, uint32_t* flags, int64_t flag_bytes, hipStream_t st) {
-  const int tile = choose_tile(XDNA_KIND_I8, M, N, K, K);
-  if (plan_tiles(XDNA_KIND_I8, M, N, K, K, tile).m1 != 0) return XDNA_EUNSUPPORTED;
-  const bool ok = tile == T_32x32 || tile == T_64x64 || tile == T_32x32K4 || tile == T_32x64K4 || tile == T_64x64K2 ||
-                  tile == T_128x128 || tile == T_256x128W8;
-  if (!ok) return XDNA_EUNSUPPORTED;
-  const TileCfg t = tile_cfg(tile);
-  const int waves = t.waves * t.kg;
-  const int64_t fq_wgs = (M + waves - 1) / waves;
-  if (flag_bytes < 4 * (1 + fq_wgs)) {
-    set_error("linear_fq: the flag buffer holds fewer than 1 + ceil(m / waves) words");
-    return XDNA_EINVAL;
-  }
-  const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
-  uint32_t ep = ++g_fq_epoch;
-  if (ep == 0) ep = ++g_fq_epoch;       // 0 is the flags' initial value
-  e.fq_x = x;
-  e.fq_ldx = ldx;
-  e.fq_q = xq;
-  e.fq_s = sx;
-  e.fq_flags = flags;
-  e.fq_epoch = ep;
-  e.fq_wgs = (int)fq_wgs;
-  e.fq_rows = waves;
-  e.sx = sx;
-  e.ksplit = 1;
-  const dim3 grid((unsigned)(fq_wgs + tiles), 1, 1);
-  const ConvGeom cg{};
-#define XDNA_FQ(BM_, BN_, WM_, WN_, S_, KG_)                                                                   \
-  mm_tile_kernel<BM_, BN_, WM_, WN_, S_, 0, EPI, true, KG_, false, true><<<grid, WM_ * WN_ * KG_ * 64, 0, st>>>( \
-      xq, K, w, ldw, M, N, K, cg, e)
-  switch (tile) {
-    case T_32x32: XDNA_FQ(32, 32, 1, 1, 4, 1); break;
-    case T_64x64: XDNA_FQ(64, 64, 2, 2, 4, 1); break;
-    case T_32x32K4: XDNA_FQ(32, 32, 1, 1, 4, 4); break;
-    case T_32x64K4: XDNA_FQ(32, 64, 1, 2, 4, 4); break;
-    case T_64x64K2: XDNA_FQ(64, 64, 2, 2, 4, 2); break;
-    case T_128x128: XDNA_FQ(128, 128, 2, 2, 3, 1); break;
-    default: XDNA_FQ(256, 128, 4, 2, 4, 1); break;
-  }
-#undef XDNA_FQ
-  return launch_status("linear_fq");
-}
-
 template <int CONVM, int EPI>
 int launch_tiles(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                  ConvGeom cg, const EpiArgs& e, int tile, hipStream_t st) {
@@ -2119,39 +1952,6 @@ int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const in
                          const float* bias, void* y, int y_dtype, int64_t ldy, int64_t m, int64_t n, int64_t k,
                          void* stream) {
   return xdna_gemm_i8_dequant_ws(a, lda, sx, w, ldw, sw, bias, y, y_dtype, ldy, m, n, k, nullptr, 0, stream);
-}
-
-int64_t xdna_linear_fq_flag_bytes(int64_t m) { return m < 0 ? 0 : 4 * (1 + m); }
-
-int xdna_linear_fq(const void* x, int x_dtype, int64_t ldx, int8_t* xq, float* sx, const int8_t* w, int64_t ldw,
-                   const float* sw, const float* bias, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
-                   uint32_t* flags, int64_t flag_bytes, void* stream) {
-  XDNA_REQUIRE(x_dtype == XDNA_F32 || x_dtype == XDNA_BF16 || x_dtype == XDNA_F16, "x_dtype must be F32/BF16/F16");
-  XDNA_REQUIRE(m >= 0 && n >= 0 && k >= 0, "negative size");
-  if (m == 0 || n == 0) return XDNA_OK;
-  XDNA_REQUIRE(x && xq && sx && w && sw && y && flags, "null pointer");
-  XDNA_REQUIRE(ldw >= k && ldw % 16 == 0 && ldy >= n && aligned(w, 16), "bad weight or output layout");
-  const int esz = x_dtype == XDNA_F32 ? 4 : 2;
-  // the fused form: rows of up to 4096 elements in whole 64-byte K slices, 16-byte aligned rows
-  if (m > FQ_MAX_M || k % 64 != 0 || k < 64 || k > 4096 || ldx < k || (ldx * esz) % 16 != 0 || !aligned(x, 16) ||
-      !aligned(xq, 16) || n * ldw >= MAX_BUF) {
-    set_error("linear_fq: shape or layout outside the fused form (call xdna_quant_rows + xdna_gemm_i8_dequant)");
-    return XDNA_EUNSUPPORTED;
-  }
-  EpiArgs e{};
-  e.out = y;
-  e.ldo = ldy;
-  e.sw = sw;
-  e.bias = bias;
-  e.vec_ok = (ldy % 8 == 0) && aligned(y, 16);
-  hipStream_t st = as_stream(stream);
-  int rc;
-  if (x_dtype == XDNA_F32) rc = launch_gemm_fq<EPI_DQ_F32>(x, ldx, xq, sx, w, ldw, m, n, k, e, flags, flag_bytes, st);
-  else if (x_dtype == XDNA_BF16) rc = launch_gemm_fq<EPI_DQ_BF16>(x, ldx, xq, sx, w, ldw, m, n, k, e, flags, flag_bytes, st);
-  else rc = launch_gemm_fq<EPI_DQ_F16>(x, ldx, xq, sx, w, ldw, m, n, k, e, flags, flag_bytes, st);
-  if (rc == XDNA_EUNSUPPORTED)
-    set_error("linear_fq: this shape's tile plan has no fused form (call xdna_quant_rows + xdna_gemm_i8_dequant)");
-  return rc;
 }
 
 int xdna_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const float* bias, void* y, int y_dtype,

@@ -99,8 +99,6 @@ def _declare(L):
         "xdna_gemm_ksplit": ([i64, i64, i64, p, p], i),
         "xdna_gemm_i8_i32_ws": ([p, i64, p, i64, p, i64, i64, i64, i64, p, i64, p], i),
         "xdna_gemm_i8_dequant_ws": ([p, i64, p, p, i64, p, p, p, i, i64, i64, i64, i64, p, i64, p], i),
-        "xdna_linear_fq_flag_bytes": ([i64], i64),
-        "xdna_linear_fq": ([p, i, i64, p, p, p, i64, p, p, p, i64, i64, i64, i64, p, i64, p], i),
         "xdna_gemm_bf16": ([p, i64, p, i64, p, p, i, i64, i64, i64, i64, p], i),
         "xdna_gemm_bf16_silu": ([p, i64, p, i64, p, i64, i64, i64, i64, p], i),
         "xdna_pad_rows_i8": ([p, i64, i64, i64, p, i64, i64, p], i),
@@ -131,7 +129,7 @@ def _declare(L):
 
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
            "xdna_gemm_i8_dequant", "xdna_gemm_ws_bytes", "xdna_gemm_ksplit", "xdna_gemm_i8_i32_ws", "xdna_gemm_i8_dequant_ws",
-           "xdna_linear_fq_flag_bytes", "xdna_linear_fq", "xdna_gemm_bf16", "xdna_gemm_bf16_silu", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc",
+           "xdna_gemm_bf16", "xdna_gemm_bf16_silu", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc",
            "xdna_conv_quant_nhwc_noalloc", "xdna_conv_weight_pack",
            "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv3x3_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8",
            "xdna_nhwc_to_nchw_i8",
@@ -407,50 +405,6 @@ def mm_i8_dequant(a, sx, w, sw, bias, out_dtype):
                                                  _ptr(bias), _ptr(y), _DTYPE_CODE[out_dtype], y.stride(0), M, N, K,
                                                  ws, wsb, _stream(dev)), "gemm_i8_dequant")
     return y
-
-
-_fq_buf = {}     # (device index, stream) -> zero-initialised int32 flag words of xdna_linear_fq
-EUNSUPPORTED = -2
-
-
-def linear_fq(x2d, wq, sw, bias, out=None):
-    """The W8A8 linear y [M, N] = dequant(quant(x2d) . wq^T) (+ bias) in x2d's dtype with the activation
-    quantize inside the GEMM launch (xdna_linear_fq), for short activations; None when the shape or layout
-    has no fused form (the caller then runs quant_rows + mm_i8_dequant, with the same results).
-    `out=(xq, sx)` receives the quantized rows and scales (else they are temporaries)."""
-    dev = _need_gpu(x2d, wq, sw, bias)
-    M, K = x2d.shape
-    N = wq.shape[0]
-    if x2d.dtype not in _DTYPE_CODE or wq.shape[1] != K or x2d.stride(1) != 1 or torch.cuda.is_current_stream_capturing():
-        return None
-    if M == 0 or N == 0:
-        return None
-    xq, sx = out if out is not None else (torch.empty((M, K), dtype=torch.int8, device=dev),
-                                          torch.empty((M,), dtype=torch.float32, device=dev))
-    y = torch.empty((M, N), dtype=x2d.dtype, device=dev)
-    idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    with _on(dev):
-        need = lib().xdna_linear_fq_flag_bytes(M)
-        skey = (idx, torch._C._cuda_getCurrentRawStream(idx))
-        buf = _fq_buf.get(skey)
-        if buf is None or buf.numel() * 4 < need:
-            buf = torch.zeros((need + 3) // 4, dtype=torch.int32, device=dev)
-            _fq_buf[skey] = buf
-        rc = lib().xdna_linear_fq(_ptr(x2d), _DTYPE_CODE[x2d.dtype], x2d.stride(0), _ptr(xq), _ptr(sx), _ptr(wq),
-                                  wq.stride(0), _ptr(sw), _ptr(bias), _ptr(y), y.stride(0), M, N, K, _ptr(buf),
-                                  buf.numel() * 4, _stream(dev))
-    if rc == EUNSUPPORTED:
-        return None
-    _check(rc, "linear_fq")
-    return y
-
-
-def fq_timeouts(dev):
-    """Whether a fused-quantize wait on dev's current stream has timed out since its flags were made
-    (word 0 of the flag buffer; synchronises)."""
-    idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    buf = _fq_buf.get((idx, torch._C._cuda_getCurrentRawStream(idx)))
-    return buf is not None and int(buf[0].item()) != 0
 
 
 def bf16_rows(x2d, k_pad):

@@ -278,9 +278,7 @@ def _check(cfg, key, got, want, exact=True):
 
 
 def _gpu_linear(cfg, x2d, qw, bias, dtype):
-    """y [R, N] = W8A8(x2d) on the GPU: quantize kernel, then the GEMM with the fused dequantize. (The
-    one-launch form with the quantize inside the GEMM, kernels.linear_fq, gives the same bits but measured
-    slower on MI355X for every shape it takes, so the route keeps the two launches.)"""
+    """y [R, N] = W8A8(x2d) on the GPU: quantize kernel, then the GEMM with the fused dequantize."""
     dev = kernels.gpu_device(x2d)
     xg = x2d.to(dev)
     wq, sw = qw.gpu(dev)
