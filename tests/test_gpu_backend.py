@@ -222,17 +222,19 @@ def test_conv(gpu, net_cls, shape, ncalls):
 
 
 def test_conv_silent_wrong(gpu, monkeypatch):
+    """A wrong value from the launch a GPU graph's conv runs (conv, requantize and dequantize in one
+    kernel) is caught by verify="first" on that launch: the layer moves to the CPU."""
     from torch_xdna import kernels
 
-    real = kernels.conv3x3
+    real = kernels.conv3x3_dequant
 
-    def corrupt(xq, wq, shift, relu):
-        q = real(xq, wq, shift, relu)
+    def corrupt(xq, wq, shift, relu, scale, sx, bias, out_dtype):
+        y = real(xq, wq, shift, relu, scale, sx, bias, out_dtype)
         if wq.shape[0] == 32:
-            q[0, 0, 0, 0] += 1
-        return q
+            y[0, 0, 0, 0] += 1
+        return y
 
-    monkeypatch.setattr(kernels, "conv3x3", corrupt)
+    monkeypatch.setattr(kernels, "conv3x3_dequant", corrupt)
     torch.manual_seed(8)
     net = CNN().eval().to(gpu)
     x = torch.randn(1, 64, 32, 64, device=gpu)

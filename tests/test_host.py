@@ -400,6 +400,37 @@ def test_conv_chain_layer_failure_fake(chain_fake, fake):
     assert torch.equal(y, y_cpu)
 
 
+def test_conv_chain_fused_launch_verified_fake(chain_fake, fake):
+    """The chain's last conv runs as one launch with its dequantize; under verify="first" that launch is
+    what the first call compares with the CPU (not the conv alone), so a wrong value from it moves the layer
+    to the CPU and the chain runs as its parts."""
+    from torch_xdna import kernels, runtime
+    from torch_xdna import conv as xconv
+
+    real = kernels.conv3x3_dequant
+
+    def corrupt(xq, wq, shift, relu, scale, sx, bias, out_dtype):
+        y = real(xq, wq, shift, relu, scale, sx, bias, out_dtype)
+        if wq.shape[0] == 40:           # the last conv (64 -> 40)
+            y[0, 0, 0, 0] += 1
+        return y
+
+    fake.setattr(kernels, "conv3x3_dequant", corrupt)
+    torch.manual_seed(5)
+    net = VGGStack().eval()
+    x = torch.randn(1, 3, 16, 16)
+    y, _ = _compile_capture(net, x)
+    s = runtime.stats.as_dict()
+    assert len(s["fallbacks"]) == 1 and "one launch" in s["fallbacks"][0][1], s["fallbacks"]
+    last = [L for _, L in xconv._layers.values() if L.co == 40]
+    assert len(last) == 1 and last[0].device == "cpu"
+    for _, layer in xconv._layers.values():
+        layer.device = "cpu"
+    fake.setattr(kernels, "conv3x3_dequant", real)
+    y_cpu, _ = _compile_capture(net, x)
+    assert torch.equal(y, y_cpu)
+
+
 def test_report_text(fake):
     import torch_xdna
 

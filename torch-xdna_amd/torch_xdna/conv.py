@@ -66,6 +66,10 @@ class ConvLayer:
         self.h, self.w, self.relu = h, w, relu
         self.shift = None
         self.device = None      # "gpu" or "cpu" once the first call has decided
+        # GPU programs of this layer already compared with the CPU route: "int" (the conv writing its
+        # integers) and "fused" (conv, requantize and dequantize in one launch), each checked on its
+        # own first launch under verify="first"
+        self.checked = set()
         self._cpu = None
         self._gpu = {}
         self._scale = {}
@@ -124,6 +128,10 @@ class ConvLayer:
         q = (self._acc(xq.cpu()).to(torch.int32) + (1 << (self.shift - 1))) >> self.shift
         return q.clamp_(0, 255).to(torch.uint8) if self.relu else q.clamp_(-128, 127).to(torch.int8)
 
+    def must_check(self, cfg, program):
+        """Whether this launch of `program` ("int" / "fused") is compared with the CPU route."""
+        return cfg.verify == "always" or (cfg.verify == "first" and program not in self.checked)
+
     def gpu_nhwc(self, xq_nhwc, verify=False, xq_nchw=None):
         """The GPU conv of an NHWC int8 activation -> NHWC int8/uint8 q."""
         wq, _ = self.gpu_weights(xq_nhwc.device)
@@ -137,10 +145,40 @@ class ConvLayer:
             if not torch.equal(got, want):
                 raise GPUResultMismatch(f"GPU {self.name} disagrees with the CPU: "
                                         f"{int((got != want).sum())} of {want.numel()} values differ")
+            self.checked.add("int")
         return q
 
+    def dequant_cpu(self, q, sx, bias, dtype):
+        """conv.py:48-50 on the CPU: q * (scale * sx) (+ bias) as dtype, NCHW."""
+        y = q.float() * (self.scale(torch.device("cpu")).view(1, -1, 1, 1) * sx.cpu().float().view(-1, 1, 1, 1))
+        if bias is not None:
+            y = y + bias.cpu().float().view(1, -1, 1, 1)
+        return y.to(dtype)
+
+    def gpu_fused(self, xq_nhwc, sx, bias, dtype, verify=False, want=None):
+        """The GPU conv with its requantize and the op's dequantize in one launch: NHWC int8 xq and per-image
+        sx -> NCHW y in dtype. verify compares y bit for bit with the CPU route: want() when given (the
+        whole composite from the float input), else the CPU conv of the same integers, dequantized."""
+        dev = xq_nhwc.device
+        wq, _ = self.gpu_weights(dev)
+        y = kernels.conv3x3_dequant(xq_nhwc, wq, self.shift, self.relu, self.scale(dev), sx, bias, dtype)
+        stats.launches += 1
+        if verify:
+            if want is None:
+                ref = self.dequant_cpu(self.cpu(xq_nhwc[..., :self.ci].permute(0, 3, 1, 2)), sx, bias, dtype)
+            else:
+                ref = want()
+            got = y.cpu()
+            bad = (got != ref) & ~(torch.isnan(got) & torch.isnan(ref))
+            if bad.any():
+                raise GPUResultMismatch(f"GPU {self.name} (conv + dequantize in one launch) disagrees with the "
+                                        f"CPU: {int(bad.sum())} of {ref.numel()} values differ")
+            self.checked.add("fused")
+        return y
+
     def gpu(self, xq, verify=False):
-        """xdna::conv3x3's contract on the GPU: NCHW int8 in, NCHW int8/uint8 out."""
+        """xdna::conv3x3's contract on the GPU: NCHW int8 in, NCHW int8/uint8 out (verify: its integers
+        against the CPU route's)."""
         dev = kernels.gpu_device(xq)
         xg = xq.to(dev)
         q = self.gpu_nhwc(kernels.nchw_to_nhwc(xg, self.ci_pad), verify, xq_nchw=xq)
@@ -225,7 +263,7 @@ def conv3x3(cfg, xq, weight, relu):
         q, device = None, "cpu"
         if layer.device == "gpu" and use_gpu:
             try:
-                q, device = layer.gpu(xq, verify=cfg.verify == "always"), "gpu"
+                q, device = layer.gpu(xq, verify=layer.must_check(cfg, "int")), "gpu"
             except Exception as e:
                 _failed(layer, e)
         if q is None:
@@ -237,7 +275,10 @@ def conv3x3(cfg, xq, weight, relu):
 
 def conv3x3_fused(cfg, x, weight, bias, relu):
     """The GPU form of conv3x3_int8: y = dequant(conv3x3(quant(x))) with all three in HIP kernels and
-    the activation kept NHWC int8 in between. Falls back to the reference composite on the CPU."""
+    the activation kept NHWC int8 in between. The conv, its requantize and the dequantize run as one
+    launch, and that launch is what verify checks (bit for bit against the reference composite on the
+    CPU from the same float input: on the layer's first fused launch under "first", on every launch
+    under "always"). Falls back to the reference composite on the CPU."""
     n, ci, h, w = x.shape
     t0 = time.perf_counter()
     on_gpu = x.device.type == "cuda"
@@ -249,36 +290,31 @@ def conv3x3_fused(cfg, x, weight, bias, relu):
                 xq, sx = kernels.conv_quant(x, layer.ci_pad)
                 if layer.shift is None:
                     layer.calibrate_gpu(xq[:1])
-                if layer.device is None:
-                    _first_call(cfg, layer, lambda v: layer.gpu_nhwc(xq, verify=v), None, on_gpu)
-                if layer.device == "gpu":
-                    b = None if bias is None else bias.to(x.device, torch.float32).contiguous()
-                    if cfg.verify == "always":     # the integers are checked, so they go through memory
-                        q = layer.gpu_nhwc(xq, verify=True)
-                        y = kernels.conv_dequant(q, relu, layer.scale(x.device), sx, b, x.dtype)
-                    else:                          # conv, requantize and dequantize in one launch
-                        wq, _ = layer.gpu_weights(x.device)
-                        y = kernels.conv3x3_dequant(xq, wq, layer.shift, relu, layer.scale(x.device), sx, b, x.dtype)
-                        stats.launches += 1
-                    device = "gpu"
+                b = None if bias is None else bias.to(x.device, torch.float32).contiguous()
+                y = layer.gpu_fused(xq, sx, b, x.dtype, verify=layer.must_check(cfg, "fused"),
+                                    want=lambda: _cpu_composite(layer, x, bias))
+                layer.device = "gpu"
+                device = "gpu"
             except Exception as e:
                 _failed(layer, e)
                 y = None
         if y is None:
-            xc = x.cpu()
-            sx = xc.abs().amax(dim=(1, 2, 3), keepdim=True).float().clamp(min=1e-8) / 127
-            xq = torch.round(xc.float() / sx).clamp(-127, 127).to(torch.int8)
-            if layer.shift is None:
-                layer.calibrate_cpu(xq[0])
-            if layer.device is None:
-                layer.device = "cpu"
-            q = layer.cpu(xq)
-            y = q.float() * (layer.scale(torch.device("cpu")).view(1, -1, 1, 1) * sx)
-            if bias is not None:
-                y = y + bias.cpu().float().view(1, -1, 1, 1)
-            y = y.to(x.dtype).to(x.device)
+            y = _cpu_composite(layer, x, bias).to(x.device)
     _account(device, t0, n, layer)
     return y
+
+
+def _cpu_composite(layer, x, bias):
+    """conv3x3_int8's CPU route (conv.py:43-51) for the layer: per-image quantize, exact conv, requantize,
+    dequantize (+ bias), in x's dtype on the CPU; the shift is calibrated here on a first call."""
+    xc = x.cpu()
+    sx = xc.abs().amax(dim=(1, 2, 3), keepdim=True).float().clamp(min=1e-8) / 127
+    xq = torch.round(xc.float() / sx).clamp(-127, 127).to(torch.int8)
+    if layer.shift is None:
+        layer.calibrate_cpu(xq[0])
+    if layer.device is None:
+        layer.device = "cpu"
+    return layer.dequant_cpu(layer.cpu(xq), sx, bias, x.dtype)
 
 
 def _on_gpu(t):
@@ -336,23 +372,18 @@ def _gpu_chain(cfg, x, layers, biases, relu_after, pools):
         for i, L in enumerate(layers):
             if L.shift is None:
                 L.calibrate_gpu(xq[:1])
-            if L.device is None:
-                _first_call(cfg, L, lambda v, L=L, xq=xq: L.gpu_nhwc(xq, verify=v), None, True)
-            if L.device != "gpu":
+            if L.device == "cpu":
                 return None
             b = None if biases[i] is None else biases[i].to(dev, torch.float32).contiguous()
-            if i == last and cfg.verify != "always":   # the last conv with its dequantize in one launch
-                wq, _ = L.gpu_weights(dev)
-                y = kernels.conv3x3_dequant(xq, wq, L.shift, L.relu, L.scale(dev), sx, b, x.dtype)
-                stats.launches += 1
+            if i == last:    # the last conv with its dequantize in one launch, checked as that launch
+                y = L.gpu_fused(xq, sx, b, x.dtype, verify=L.must_check(cfg, "fused"))
+                L.device = "gpu"
                 done += 1
                 continue
-            q = L.gpu_nhwc(xq, verify=cfg.verify == "always")
-            if i < last:
-                xq, sx = kernels.conv_requant_next(q, L.relu, pools[i], L.scale(dev), sx, b, x.dtype,
-                                                   layers[i + 1].ci_pad, relu_y=relu_after[i])
-            else:
-                y = kernels.conv_dequant(q, L.relu, L.scale(dev), sx, b, x.dtype)
+            q = L.gpu_nhwc(xq, verify=L.must_check(cfg, "int"))
+            L.device = "gpu"
+            xq, sx = kernels.conv_requant_next(q, L.relu, pools[i], L.scale(dev), sx, b, x.dtype,
+                                               layers[i + 1].ci_pad, relu_y=relu_after[i])
             done += 1
     except Exception as e:
         _failed(layers[done], e)
