@@ -11,7 +11,9 @@ configs; seed 0), with inputs and device-resident int8 weights already in HBM:
                 The same JSON line carries sub-records, each with its own roofline and CPU
                 baseline: C4's 256-channel conv at 1x256x1536x64 and 8x256x256x256 run as the op
                 (xdna::conv3x3_fused: per-image quantize -> conv with the calibrated shift ->
-                dequantize, ReLU fused), with the conv kernel's back-to-back time beside it, and C2.
+                dequantize, ReLU fused), with the conv kernel's back-to-back time beside it; C2; the
+                decode GEMMs (HBM-bound); the activation quantize alone at bf16 8192 x 14336 and
+                8192 x 4096 (HBM-bound); and the C3 chain end to end.
   c2            Qwen3-0.6B projections as xdna::linear_cat runs them on the GPU: for M in
                 {128, 512, 1024, 3000}, bf16 x -> quantize -> fused GEMM -> bf16, for qkv
                 (N 4096, K 1024), gate/up (N 6144, K 1024) and down (N 1024, K 3072).
@@ -20,7 +22,7 @@ configs; seed 0), with inputs and device-resident int8 weights already in HBM:
   c4            C4's two 256-channel convs as the op (the headline's sub-records alone).
   c5            the headline's main record alone.
   decode        the C5 decode GEMMs (M 1 and 16), HBM-bound: roofline in GB/s of algorithmic bytes.
-  quant         the activation quantize kernel alone, bf16 [8192, 14336].
+  quant         the activation quantize kernel alone, bf16 [8192, 14336] and [8192, 4096].
   bf16          precision "bf16" on the C2 shapes: the bf16 MFMA GEMM (bf16 in / out, float32 sums).
   vgg16         VGG-16 features at batch 8 through torch.compile(backend="xdna"), convs chained.
   stack         xdna::qwen3_stack on OmniVoice's step shapes.
@@ -36,7 +38,9 @@ cost included) is reported beside it. Rank 0 prints one JSON line.
 CPU baseline: the reference's CPU route (oracle/cpu_route.py: torch CPU quantize, torch._int_mm or
 an exact float conv of the integers, dequantize) on the GPU box's host cores, timed by the
 reference's protocol (tools/cpu_baseline.py:14-26: 5 warm-up runs, then 60 timed runs, min / p25 /
-median), with the thread count and the CPU model; each record says what its sample is.
+median) with as many torch threads as the process has CPUs (and at the reference's 16 beside it when
+that differs), with the thread count, os.cpu_count() and the CPU model; each record says what its
+sample is.
 """
 
 import argparse
@@ -73,9 +77,6 @@ def parse():
     ap.add_argument("--operands", default="randn", choices=["randn", "zeros"],
                     help="zeros: all-zero activations and weights on the GEMM workloads (a diagnostic of the power "
                          "limit: the same work with the least switching; never the reported configuration)")
-    ap.add_argument("--fq", default="off", choices=["on", "off"],
-                    help="on: the quantize inside the GEMM launch (xdna_linear_fq) where it applies (rows up to "
-                         "1024); measured slower than the two launches, so off by default")
     ap.add_argument("--tile", default=None,
                     help="force this tile (a kernels.TILES name) on every GEMM shape of the c1/c2/c5/decode "
                          "workloads instead of the built-in rule and the tuned table (results do not depend on it)")
@@ -112,33 +113,16 @@ def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed
     return sets
 
 
-FQ = {"on": False}     # the fused-quantize launch where it applies (--fq on)
-_fq_shapes = {}       # (M, N, K, dtype) -> whether xdna_linear_fq takes the shape
-
-
-def fq_taken(M, N, K, dtype):
-    return bool(FQ["on"] and _fq_shapes.get((M, N, K, dtype)))
-
-
 def run_gemm_step_split(items, ev=None):
     """One step ordered as all activation quantizes, then all fused GEMMs (the same work as
     quantize -> GEMM per shape); ev = three events recorded at the start, between the two groups and
-    at the end, so ev[1] -> ev[2] brackets exactly the step's GEMM launches, back to back. Shapes the
-    fused-quantize launch takes (rows up to 1024) run as that one launch in the GEMM group and have no
-    quantize in the first (a shape's first step finds out which, in the warm-up)."""
+    at the end, so ev[1] -> ev[2] brackets exactly the step's GEMM launches, back to back."""
     if ev:
         ev[0].record()
-    qs = [None if (FQ["on"] and _fq_shapes.get((M, N, K, x.dtype), True)) else kernels.quant_rows(x)
-          for x, wq, sw, b, M, N, K in items]
+    qs = [kernels.quant_rows(x) for x, wq, sw, b, M, N, K in items]
     if ev:
         ev[1].record()
     for (x, wq, sw, b, M, N, K), q in zip(items, qs):
-        if q is None:
-            y = kernels.linear_fq(x, wq, sw, b)
-            _fq_shapes[(M, N, K, x.dtype)] = y is not None
-            if y is not None:
-                continue
-            q = kernels.quant_rows(x)
         kernels.mm_i8_dequant(q[0], q[1], wq, sw, b, x.dtype)
     if ev:
         ev[2].record()
@@ -154,24 +138,45 @@ def quant_bytes(M, K, xbytes):
 
 
 # ------------------------------------------------------------------------------ CPU baseline
-def cpu_model():
-    """The host CPU's model string, reported beside every CPU number."""
+def cpu_host():
+    """The host CPU the baseline ran on: /proc/cpuinfo's model string (with family / model / stepping), the
+    logical CPUs the OS reports (os.cpu_count()) and those this process may run on (its affinity mask)."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k in ("model name", "cpu family", "model", "stepping", "cpu MHz", "cache size") and k not in info:
+                    info[k] = v
+                if not line.strip() and "model name" in info:
+                    break
     except OSError:
         pass
-    import platform
+    if "model name" not in info:
+        import platform
 
-    return platform.processor() or "unknown"
+        info["model name"] = platform.processor() or "unknown"
+    ncpu = os.cpu_count() or 1
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = ncpu
+    return {"cpu_model": info.pop("model name"), "cpuinfo": info, "os_cpu_count": ncpu, "affinity_cpus": aff}
 
 
-def cpu_protocol(step, ops, sample, budget_s=20.0, warmup=5, reps=60):
-    """Times `step` by the reference's protocol (tools/cpu_baseline.py:14-26): `warmup` untimed runs,
-    then `reps` timed runs (fewer when they would exceed budget_s, at least 10), min / p25 / median.
-    value = ops / min time, in TOPS (or TFLOP/s for a float route)."""
+# The reference's CPU baseline ran 16 threads (tools/cpu_baseline.py:11); ours runs as many threads as the
+# process has CPUs (os.cpu_count(), bounded by the affinity mask: more threads than CPUs only oversubscribe),
+# with the 16-thread figure beside it when the two differ.
+REF_THREADS = 16
+
+
+def cpu_threads():
+    h = cpu_host()
+    return max(1, min(h["os_cpu_count"], h["affinity_cpus"]))
+
+
+def _time_protocol(step, warmup, reps, budget_s):
     for _ in range(warmup):
         step()
     ts = []
@@ -181,11 +186,34 @@ def cpu_protocol(step, ops, sample, budget_s=20.0, warmup=5, reps=60):
         step()
         ts.append(time.perf_counter() - t)
     ts.sort()
-    rank = lambda p: ts[int(p * len(ts))]   # noqa: E731  (ts[15] / ts[30] of 60, as the reference)
-    return {"value": round(ops / ts[0] / 1e12, 3), "unit": "TOPS", "cores": torch.get_num_threads(),
-            "kind": "port", "sample": sample, "cpu_model": cpu_model(), "warmup": warmup, "reps": len(ts),
-            "min_ms": round(ts[0] * 1e3, 3), "p25_ms": round(rank(0.25) * 1e3, 3),
-            "median_ms": round(rank(0.5) * 1e3, 3)}
+    return ts
+
+
+def cpu_protocol(step, ops, sample, budget_s=20.0, warmup=5, reps=60, unit="TOPS"):
+    """Times `step` by the reference's protocol (tools/cpu_baseline.py:14-26): `warmup` untimed runs,
+    then `reps` timed runs (fewer when they would exceed budget_s, at least 10), min / p25 / median, with
+    torch's CPU threads set to the process's CPUs (cpu_threads()). value = ops / min time, in TOPS (or
+    TFLOP/s for a float route), or GB/s when unit is "GB/s" (ops then counts bytes). When that thread count
+    is not the reference's 16, the same protocol at 16 threads follows (budget_s / 2), as at_16_threads."""
+    scale = 1e9 if unit == "GB/s" else 1e12
+    saved = torch.get_num_threads()
+    nthr = cpu_threads()
+    rank = lambda ts, p: ts[int(p * len(ts))]   # noqa: E731  (ts[15] / ts[30] of 60, as the reference)
+    try:
+        torch.set_num_threads(nthr)
+        ts = _time_protocol(step, warmup, reps, budget_s)
+        rec = {"value": round(ops / ts[0] / scale, 3), "unit": unit, "cores": nthr, "kind": "port",
+               "sample": sample, **cpu_host(), "threads_set": f"torch.set_num_threads({nthr})",
+               "warmup": warmup, "reps": len(ts), "min_ms": round(ts[0] * 1e3, 3),
+               "p25_ms": round(rank(ts, 0.25) * 1e3, 3), "median_ms": round(rank(ts, 0.5) * 1e3, 3)}
+        if nthr != REF_THREADS:
+            torch.set_num_threads(REF_THREADS)
+            t16 = _time_protocol(step, min(warmup, 2), reps, budget_s / 2)
+            rec["at_16_threads"] = {"value": round(ops / t16[0] / scale, 3), "min_ms": round(t16[0] * 1e3, 3),
+                                    "median_ms": round(rank(t16, 0.5) * 1e3, 3), "reps": len(t16)}
+    finally:
+        torch.set_num_threads(saved)
+    return rec
 
 
 def cpu_baseline_gemm(shapes, x_dtype, bias, label, budget_s=20.0):
@@ -238,7 +266,6 @@ def cpu_baseline_conv(n, c, h, w, layers, sample, relu=True, budget_s=20.0):
 # ------------------------------------------------------------------------------ main
 def main():
     a = parse()
-    FQ["on"] = a.fq == "on"
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}); "
               "run with --gpus 1", file=sys.stderr)
@@ -356,14 +383,6 @@ def per_shape_us(sets, launches=10):
         ncopies = max(len(sets), min(64, -(-(MALL_BYTES + (64 << 20)) // wbytes)))
         launches = max(launches, ncopies)
         weights = [sets[i][j][1] if i < len(sets) else sets[0][j][1].clone() for i in range(ncopies)]
-        x0, _, _, _, M0, N0, K0 = sets[0][j]
-        if fq_taken(M0, N0, K0, x0.dtype):     # the one fused-quantize launch (it reads the float rows)
-            calls = []
-            for i in range(launches):
-                x, wq, sw, b, M, N, K = sets[i % len(sets)][j]
-                calls.append(lambda x=x, w=weights[i % ncopies], sw=sw, b=b: kernels.linear_fq(x, w, sw, b))
-            out.append(back_to_back_us(calls, launches))
-            continue
         for i in range(launches):
             x, wq, sw, b, M, N, K = sets[i % len(sets)][j]
             ops.append((kernels.quant_rows(x), weights[i % ncopies], sw, b, x.dtype))
@@ -432,13 +451,10 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
     xb = x_dtype.itemsize
     nshape = len(shapes)
     g_sec = sum(g_ms) / 1e3                            # GEMM launches of the timed steps
-    fq = [fq_taken(M, N, K, x_dtype) for M, N, K in shapes]
-    # a fused-quantize launch also reads the float rows and writes their int8 copy and scales
-    launch_bytes = [gemm_bytes(M, N, K, xb, yb, bias) + (quant_bytes(M, K, xb) if f else 0)
-                    for (M, N, K), f in zip(shapes, fq)]
+    launch_bytes = [gemm_bytes(M, N, K, xb, yb, bias) for M, N, K in shapes]
     g_bytes = sum(launch_bytes) * reps
-    nq = sum(1 for f in fq if not f)
-    q_bytes = sum(quant_bytes(M, K, xb) for (M, N, K), f in zip(shapes, fq) if not f) * reps
+    nq = nshape
+    q_bytes = sum(quant_bytes(M, K, xb) for M, N, K in shapes) * reps
     q_sec = sum(q_ms) / 1e3
     achieved = ops_step * reps / g_sec / 1e12
     bound_us = sum(roofline_us(2 * M * N * K, nb) for (M, N, K), nb in zip(shapes, launch_bytes))
@@ -449,9 +465,7 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
                      "step's quantizes then its GEMMs with events between; host_ms_per_step: the same "
                      "steps launched without a gate, wall clock",
            "config": {"workload": workload, "shapes_mnk": shapes, "x_dtype": str(x_dtype).replace("torch.", ""),
-                      "bias": bias, "rotating_sets": len(sets),
-                      "quantize": "in the GEMM launch for the shapes listed in fused_quantize_shapes, else a launch of "
-                                  "its own (--fq on)" if FQ["on"] else "a launch of its own"},
+                      "bias": bias, "rotating_sets": len(sets), "quantize": "a launch of its own"},
            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(achieved / PEAK_INT8_TOPS, 4),
                         "traffic": None if a.tile or a.operands != "randn" else traffic(label.lower()),
@@ -463,7 +477,6 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
            "quantize": None if nq == 0 else {"achieved_GBs": round(q_bytes / q_sec / 1e9, 1), "peak": PEAK_HBM_GBS,
                                              "avg_launch_us": round(q_sec / (nq * reps) * 1e6, 2),
                                              "launches": nq * reps},
-           "fused_quantize_shapes": [list(sh) for sh, f in zip(shapes, fq) if f],
            "per_shape": []}
     if bound == "hbm":
         gbs = g_bytes / g_sec / 1e9
@@ -472,9 +485,7 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
     for j, (M, N, K) in enumerate(shapes):
         t = per_shape[j] / 1e6
         b = gemm_bytes(M, N, K, xb, yb, bias)
-        if fq[j]:
-            b += quant_bytes(M, K, xb)
-        tile = kernels.gemm_variant(dev, M, N, kernels.round_up(K, 16)) + ("+fq" if fq[j] else "")
+        tile = kernels.gemm_variant(dev, M, N, kernels.round_up(K, 16))
         out["per_shape"].append({"mnk": [M, N, K], "tile": tile,
                                  "us": round(t * 1e6, 2), "TOPS": round(2 * M * N * K / t / 1e12, 1),
                                  "GBs": round(b / t / 1e9, 1),
@@ -505,10 +516,13 @@ def bench_c5(a, dev):
 
 
 def bench_headline(a, dev):
-    """C5 M=8192 (the largest single-GPU config) as the line, C4's two 256-channel convs (as the op)
-    and C2 as sub-records, each with its own roofline and CPU baseline."""
+    """C5 M=8192 (the largest single-GPU config) as the line; as sub-records, each with its own roofline
+    and CPU baseline: C4's two 256-channel convs (as the op), C2, the decode GEMMs (M 1 and 16, HBM-bound),
+    the activation quantize alone at 8192 x 14336 and 8192 x 4096 (HBM-bound), and the C3 chain."""
     out = bench_c5(a, dev)
-    out["sub"] = bench_c4(a, dev)["sub"] + [dict(bench_c2(a, dev), workload_key="C2")]
+    out["sub"] = (bench_c4(a, dev)["sub"] + [dict(bench_c2(a, dev), workload_key="C2"),
+                                              dict(bench_decode(a, dev), workload_key="decode")]
+                  + bench_quant(a, dev)["sub"] + [dict(bench_c3(a, dev), workload_key="C3")])
     return out
 
 
@@ -570,21 +584,55 @@ def bench_decode(a, dev):
     return out
 
 
-def bench_quant(a, dev):
+def quant_kernel_name(K, dtype):
+    """The activation-quantize kernel xdna_quant_rows launches for rows of K elements of `dtype` (16-byte
+    aligned rows, K % 16 == 0): a wavefront per row up to 2048 elements, else a 256-thread block per row."""
+    return "quant_rows_wave_kernel" if K <= 2048 else "quant_rows_block_kernel"
+
+
+def quant_record(a, dev, M, K, x_dtype=torch.bfloat16):
+    """The activation quantize alone (xdna_quant_rows: per-row amax, scale, int8 rows) on x [M, K]: K
+    launches back to back behind the gate and a pre-heat, between two events, on rotating inputs that
+    together exceed the Infinity Cache. value and roofline: algorithmic bytes (M K in + M K int8 out + 4 M
+    scales) per second of launch time."""
     g = gen(0)
-    M, K = 8192, 14336
-    xs = [torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev) for _ in range(2)]
-    # one launch per step, back to back behind the gate: GPU seconds per step = the launch's duration
-    sec, host = timed_steps(a, lambda i, tm: kernels.quant_rows(xs[i % 2]), None)
-    b = quant_bytes(M, K, 2)
-    gbs = b / sec / 1e9
-    return {"metric": "activation quantize GB/s on 1 MI355X", "unit": "GB/s", "value": round(b / sec / 1e9, 1),
-            "ms_per_step": round(sec * 1e3, 4), "host_ms_per_step": round(host * 1e3, 4), "dtype": "bf16->int8",
-            "config": {"workload": "quantize bf16 [8192, 14336] per row"},
-            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic("quant"),
-                         "kernel": "quant_rows_wave_kernel", "avg_launch_us": round(sec * 1e6, 2),
-                         "alg_bytes_per_launch": b}}
+    xb = x_dtype.itemsize
+    nsets = max(3, -(-(MALL_BYTES + (64 << 20)) // (M * K * (xb + 1))))
+    xs = [torch.randn(M, K, generator=g).to(x_dtype).to(dev) for _ in range(nsets)]
+    outs = [(torch.empty((M, K), dtype=torch.int8, device=dev), torch.empty((M,), dtype=torch.float32, device=dev))
+            for _ in range(nsets)]
+    us = back_to_back_us([lambda x=x, o=o: kernels.quant_rows(x, out=o) for x, o in zip(xs, outs)],
+                         max(3 * nsets, a.steps))
+    b = quant_bytes(M, K, xb)
+    gbs = b / (us * 1e3)
+    rec = {"workload_key": f"quantize {M}x{K}", "metric": "activation quantize GB/s on 1 MI355X", "unit": "GB/s",
+           "value": round(gbs, 1), "ms_per_step": round(us / 1e3, 5), "dtype": f"{str(x_dtype)[6:]}->int8",
+           "config": {"workload": f"per-row activation quantize of {str(x_dtype)[6:]} [{M}, {K}] -> int8 rows + "
+                                  "float32 row scales (xdna_quant_rows)", "rotating_inputs": nsets},
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic(f"quant_{M}x{K}"),
+                        "kernel": quant_kernel_name(K, x_dtype), "avg_launch_us": round(us, 2),
+                        "alg_bytes_per_launch": b,
+                        "timing": "launches back to back behind the gate and a pre-heat, events around them"}}
+    if not a.no_cpu_baseline:
+        rows = max(1, min(M, (64 << 20) // (K * 4)))       # a sample of about 64 MB of float32 work per run
+        xc = torch.randn(rows, K, generator=gen(1)).to(x_dtype)
+        from oracle import cpu_route
+
+        rec["cpu_baseline"] = cpu_protocol(lambda: cpu_route.quant_rows(xc), quant_bytes(rows, K, xb),
+                                           f"{rows} of the {M} rows (bytes scaled as the GPU's): torch CPU quantize "
+                                           "(amax, divide, round, clamp, int8), the reference's expression",
+                                           unit="GB/s")
+    return rec
+
+
+def bench_quant(a, dev):
+    """The activation quantize alone on the bf16 shapes it serves: 8192 x 14336 (the down projection's input
+    at C5's M) and 8192 x 4096 (the headline's own). The first is the line, both are sub-records."""
+    recs = [quant_record(a, dev, 8192, 14336), quant_record(a, dev, 8192, 4096)]
+    out = {k: v for k, v in recs[0].items() if k != "workload_key"}
+    out["sub"] = recs
+    return out
 
 
 def bench_copy(a, dev):
