@@ -106,6 +106,78 @@ def test_find_rejects(as_gpu, monkeypatch):
     assert stack.find(gm, ex) is None
 
 
+def _mutated(gm, edit):
+    """A copy of gm's graph with `edit(node)` applied to every node (edit returns True when it changed one)."""
+    g = stack.copy_module(gm)
+    changed = sum(bool(edit(n)) for n in list(g.graph.nodes))
+    assert changed, "the mutation found nothing to change"
+    g.recompile()
+    return g
+
+
+def _set_kw(target, key, value):
+    def edit(n):
+        if n.op == "call_function" and target in str(n.target):
+            n.kwargs = {**n.kwargs, key: value}
+            return True
+    return edit
+
+
+def _set_float(target, old, new):
+    def edit(n):
+        if n.op == "call_function" and target in str(n.target) and old in n.args:
+            n.args = tuple(new if a == old else a for a in n.args)
+            return True
+    return edit
+
+
+@pytest.mark.parametrize("what,edit", [
+    ("causal attention", _set_kw("scaled_dot_product_attention", "is_causal", True)),
+    ("attention dropout", _set_kw("scaled_dot_product_attention", "dropout_p", 0.1)),
+    ("attention scale", _set_kw("scaled_dot_product_attention", "scale", 0.5)),
+    ("no mask", _set_kw("scaled_dot_product_attention", "attn_mask", None)),
+    ("RMSNorm eps", _set_float("add", 1e-06, 1e-05)),
+    ("RoPE scaling", _set_float("mul", 1.0, 2.0)),
+])
+def test_find_rejects_mutations(as_gpu, what, edit):
+    """One rule broken in an otherwise fusable graph (2 layers + head): the matcher turns it down. The
+    unmutated graph is found, so each case isolates its rule."""
+    torch.manual_seed(2)
+    net = Stack(layers=2, out=24).eval()
+    gm, ex = _graph(net, torch.randn(2, 6, 1024), prefix_mask([6, 3], 6))
+    assert stack.find(gm, ex) is not None
+    assert stack.find(_mutated(gm, edit), ex) is None, what
+
+
+def test_find_rejects_model_variants(as_gpu):
+    """Stacks the op is not built for: biased attention projections, another RMSNorm eps, and a stack whose
+    output has a second user besides the head; a head without bias and one with both are found."""
+    from transformers import Qwen3Config, Qwen3Model
+
+    def qwen(**kw):
+        cfg = dict(hidden_size=1024, intermediate_size=3072, num_hidden_layers=1, num_attention_heads=16,
+                   num_key_value_heads=8, head_dim=128, vocab_size=16, rms_norm_eps=1e-6, attn_implementation="sdpa")
+        cfg.update(kw)
+        return Qwen3Model(Qwen3Config(**cfg))
+
+    class Net(torch.nn.Module):
+        def __init__(self, llm, twice=False, bias=False):
+            super().__init__()
+            self.llm, self.head, self.twice = llm, torch.nn.Linear(1024, 8, bias=bias), twice
+
+        def forward(self, x, mask):
+            h = self.llm(inputs_embeds=x, attention_mask=mask)[0]
+            return self.head(h) + h[..., :8] if self.twice else self.head(h)
+
+    torch.manual_seed(3)
+    x, mask = torch.randn(1, 5, 1024), prefix_mask([5], 5)
+    for net, found in ((Net(qwen()), True), (Net(qwen(), bias=True), True),
+                       (Net(qwen(attention_bias=True)), False), (Net(qwen(rms_norm_eps=1e-5)), False),
+                       (Net(qwen(), twice=True), False)):
+        gm, ex = _graph(net.eval(), x, mask)
+        assert (stack.find(gm, ex) is not None) == found, (net.llm.config.attention_bias, net.twice)
+
+
 def test_backend_keeps_host_stacks_plain():
     """Without a GPU the backend compiles a stack model as a plain graph (its linears on the CPU's
     W8A8 route): no stack op runs, and the output stays within int8 error of the float model."""

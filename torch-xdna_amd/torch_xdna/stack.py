@@ -64,23 +64,6 @@ _SDPA = frozenset({torch._C._nn.scaled_dot_product_attention, F.scaled_dot_produ
 _ADD = frozenset({operator.add, torch.add})
 _MUL = frozenset({operator.mul, torch.mul})
 
-# Module paths below the Qwen3Model, split on ".": a layer's sub-path -> the role of the weight its
-# linear uses, or of the parameter its norm uses; the stack-level paths of the final norm and RoPE.
-_LINEAR_ROLE = {("self_attn", "q_proj"): "q", ("self_attn", "k_proj"): "k", ("self_attn", "v_proj"): "v",
-                ("self_attn", "o_proj"): "o", ("mlp", "gate_proj"): "gate", ("mlp", "up_proj"): "up",
-                ("mlp", "down_proj"): "down"}
-_PARAM_ROLE = {("input_layernorm",): "input_norm", ("post_attention_layernorm",): "post_norm",
-               ("self_attn", "q_norm"): "q_norm", ("self_attn", "k_norm"): "k_norm"}
-_STACK_ROLE = {("norm",): "norm", ("rotary_emb",): "inv_freq"}
-
-
-def _layer_path(rel):
-    """(layer index, the rest of the path) for `layers.<i>.<...>`, else (None, the whole path)."""
-    parts = tuple(rel.split(".")) if rel else ()
-    if len(parts) >= 2 and parts[0] == "layers" and parts[1].isdigit():
-        return int(parts[1]), parts[2:]
-    return None, parts
-
 
 def _class_name(c):
     return c.__name__ if isinstance(c, type) else str(c).rsplit(".", 1)[-1].strip("'>")
@@ -120,146 +103,238 @@ class Plan:
         return per_layer + [self.weights[r] for r in ("norm", "head", "inv_freq")]
 
 
-class _Matcher:
-    """Checks one Qwen3Model region (the nodes that ran inside module path `root`) against the rules
-    in the module docstring and builds its Plan."""
+@dataclass(frozen=True)
+class _Slot:
+    """Where a stack parameter may appear: its role, how it enters the graph ("weight": the weight of a
+    bias-free linear; "operand": an input of any other op) and the shape the op is built for."""
+    role: str
+    use: str
+    shape: tuple
+
+
+# Every parameter a fusable stack holds, keyed by the module path (below the Qwen3Model) of the node that
+# uses it, with a layer's index written as "#". A parameter anywhere else, or used another way, means the
+# region is not a stack the op takes (the rules of the reference's stack.py:111-241).
+_SLOTS = {
+    "layers.#.self_attn.q_proj": _Slot("q", "weight", LAYER_SHAPES["q"]),
+    "layers.#.self_attn.k_proj": _Slot("k", "weight", LAYER_SHAPES["k"]),
+    "layers.#.self_attn.v_proj": _Slot("v", "weight", LAYER_SHAPES["v"]),
+    "layers.#.self_attn.o_proj": _Slot("o", "weight", LAYER_SHAPES["o"]),
+    "layers.#.mlp.gate_proj": _Slot("gate", "weight", LAYER_SHAPES["gate"]),
+    "layers.#.mlp.up_proj": _Slot("up", "weight", LAYER_SHAPES["up"]),
+    "layers.#.mlp.down_proj": _Slot("down", "weight", LAYER_SHAPES["down"]),
+    "layers.#.input_layernorm": _Slot("input_norm", "operand", LAYER_SHAPES["input_norm"]),
+    "layers.#.post_attention_layernorm": _Slot("post_norm", "operand", LAYER_SHAPES["post_norm"]),
+    "layers.#.self_attn.q_norm": _Slot("q_norm", "operand", LAYER_SHAPES["q_norm"]),
+    "layers.#.self_attn.k_norm": _Slot("k_norm", "operand", LAYER_SHAPES["k_norm"]),
+    "norm": _Slot("norm", "operand", (D,)),
+    "rotary_emb": _Slot("inv_freq", "operand", (DH // 2,)),
+}
+_STACK_SLOTS = {k: v for k, v in _SLOTS.items() if not k.startswith("layers.#.")}
+
+
+def _slot_key(rel):
+    """(slot key, layer index) of a module path below the root: "layers.7.mlp.up_proj" -> ("layers.#.mlp.up_proj",
+    7); a path outside the layers keeps its text and has no index."""
+    head, sep, rest = rel.partition(".")
+    idx, sep2, tail = rest.partition(".")
+    if head == "layers" and sep and idx.isdigit():
+        return "layers.#" + (sep2 + tail if sep2 else ""), int(idx)
+    return rel, None
+
+
+_SDPA_ARGS = ("query", "key", "value", "attn_mask", "dropout_p", "is_causal", "scale")
+
+
+@dataclass
+class _Census:
+    """Facts about one Qwen3Model region, gathered in a single pass over its nodes: each linear with the
+    slot of its module, each parameter used as an operand, the attentions' arguments, the float constants
+    of RMSNorm adds and RoPE multiplies, the values that come from outside the region and the region's
+    nodes whose value leaves it."""
+    linears: list = field(default_factory=list)      # (slot key, layer, weight node, bias node, module path)
+    operands: list = field(default_factory=list)     # (slot key, layer, parameter node, module path)
+    attentions: list = field(default_factory=list)   # {argument name: value} of each attention call
+    eps: list = field(default_factory=list)          # float constants added inside RMSNorm modules
+    rope_scale: list = field(default_factory=list)   # float constants multiplied inside the RoPE module
+    inputs: list = field(default_factory=list)       # outside tensors (not parameters, sizes or the mask)
+    exits: list = field(default_factory=list)        # region nodes with a user outside the region
+
+
+class _Candidate:
+    """One Qwen3Model region (the nodes that ran inside module path `root`): its census, then the rules, each
+    a generator of problems; the first problem rejects the region, none gives the Plan."""
 
     def __init__(self, root, nodes, example_of, placeholders):
         self.root, self.nodes, self.inside = root, nodes, set(nodes)
         self.example_of, self.placeholders = example_of, placeholders
+        self.census = self._take_census()
         self.roles = {}
-        self.attention = []
+        self.layers = 0
+        self.mask = None
 
-    def is_param(self, n):
-        return n.op == "placeholder" and (isinstance(self.example_of.get(n), torch.nn.Parameter)
-                                          or "_parameters_" in n.name or "_buffers_" in n.name)
+    # ---- facts
+    def _param(self, n):
+        """Whether node n is a parameter or buffer of the model (a graph input Dynamo lifted from one)."""
+        if not isinstance(n, torch.fx.Node) or n.op != "placeholder":
+            return False
+        return isinstance(self.example_of.get(n), torch.nn.Parameter) or any(
+            tag in n.name for tag in ("_parameters_", "_buffers_"))
 
-    def bind(self, role, node):
+    def _module(self, n):
+        path, cls = list(n.meta["nn_module_stack"].values())[-1]
+        return path[len(self.root) + 1:] if path.startswith(self.root + ".") else "", _class_name(cls)
+
+    def _take_census(self):
+        c = _Census()
+        seen = set()
+        for n in self.nodes:
+            rel, cls = self._module(n)
+            key, layer = _slot_key(rel)
+            fn = n.target if n.op == "call_function" else None
+            skip = None
+            if fn in _LINEAR:
+                _, w, bias = _linear_operands(n)
+                c.linears.append((key, layer, w, bias, rel))
+                skip = w
+            elif fn in _SDPA:
+                call = dict(zip(_SDPA_ARGS, n.args))
+                call.update(n.kwargs)
+                c.attentions.append(call)
+            if fn is not None:
+                consts = [v for v in n.args if isinstance(v, float)]
+                if fn in _ADD and cls.endswith("RMSNorm"):
+                    c.eps += consts
+                if fn in _MUL and rel == "rotary_emb":
+                    c.rope_scale += consts
+            for a in n.all_input_nodes:
+                if a is skip:
+                    continue
+                if self._param(a):
+                    c.operands.append((key, layer, a, rel))
+                elif a not in self.inside and a not in seen:
+                    seen.add(a)
+                    c.inputs.append(a)
+            if any(u not in self.inside for u in n.users):
+                c.exits.append(n)
+        return c
+
+    def _claim(self, role, node):
+        """Binds a role to the tensor behind node; a second, different tensor for one role is a problem."""
         t = self.example_of.get(node)
         if not isinstance(t, torch.Tensor):
-            raise _NoStack(f"{role}: no tensor")
+            return f"no tensor behind {role}"
         if self.roles.setdefault(role, t) is not t:
-            raise _NoStack(f"two tensors for {role}")
+            return f"{role} is bound to two different tensors"
+        return None
 
-    def rel_path(self, n):
-        """Path (below the root) and class of the innermost module node n ran in."""
-        path, cls = list(n.meta["nn_module_stack"].values())[-1]
-        return (path[len(self.root) + 1:] if path != self.root else ""), _class_name(cls)
+    # ---- rules
+    def _parameters(self):
+        """Every linear is a bias-free projection of a parameter at a weight slot; every other parameter sits
+        at an operand slot; each role is one tensor."""
+        for key, layer, w, bias, rel in self.census.linears:
+            slot = _SLOTS.get(key)
+            if slot is None or slot.use != "weight" or bias is not None or not self._param(w):
+                yield f"linear at '{rel or '<root>'}' is not a bias-free projection of a stack parameter"
+                return
+            yield from filter(None, [self._claim((layer, slot.role), w)])
+        for key, layer, a, rel in self.census.operands:
+            slot = _SLOTS.get(key)
+            if slot is None or slot.use != "operand":
+                yield f"parameter {a.name} is used at '{rel or '<root>'}', which holds no stack parameter"
+                return
+            yield from filter(None, [self._claim(slot.role if layer is None else (layer, slot.role), a)])
 
-    def scan(self):
-        for n in self.nodes:
-            rel, cls = self.rel_path(n)
-            layer, sub = _layer_path(rel)
-            weight = None
-            if n.op == "call_function" and n.target in _LINEAR:
-                x, weight, bias = _linear_operands(n)
-                role = _LINEAR_ROLE.get(sub) if layer is not None else None
-                if role is None or bias is not None or not self.is_param(weight):
-                    raise _NoStack(f"a linear in {rel or 'the root'}")
-                self.bind((layer, role), weight)
-            elif n.op == "call_function" and n.target in _SDPA:
-                self.attention.append(n)
-            for a in n.all_input_nodes:
-                if a is weight or not self.is_param(a):
-                    continue
-                if layer is not None and sub in _PARAM_ROLE:
-                    self.bind((layer, _PARAM_ROLE[sub]), a)
-                elif layer is None and sub in _STACK_ROLE:
-                    self.bind(_STACK_ROLE[sub], a)
-                else:
-                    raise _NoStack(f"parameter {a.name} used in {rel or 'the root'}")
-            self.check_constants(n, cls, rel)
-
-    @staticmethod
-    def check_constants(n, cls, rel):
-        """The op has RMSNorm's eps and RoPE without attention scaling built in."""
-        floats = [a for a in n.args if isinstance(a, float)]
-        if n.op != "call_function" or not floats:
+    def _shapes(self):
+        """Layers 0 .. L-1, each with every per-layer role at the op's shape, and the stack-level roles."""
+        self.layers = 1 + max((r[0] for r in self.roles if isinstance(r, tuple)), default=-1)
+        if self.layers == 0:
+            yield "the region holds no layer"
             return
-        if n.target in _ADD and cls.endswith("RMSNorm") and any(abs(c - EPS) > 1e-12 for c in floats):
-            raise _NoStack(f"RMSNorm eps {floats} (the op has {EPS})")
-        if n.target in _MUL and rel == "rotary_emb" and any(c != 1.0 for c in floats):
-            raise _NoStack(f"RoPE attention scaling {floats}")
+        for (i, key) in ((i, k) for i in range(self.layers) for k in LAYER_KEYS):
+            got = self.roles.get((i, key))
+            if got is None or tuple(got.shape) != LAYER_SHAPES[key]:
+                yield f"layer {i}: {key} is {'missing' if got is None else tuple(got.shape)}, the op takes " \
+                      f"{LAYER_SHAPES[key]}"
+                return
+        for slot in _STACK_SLOTS.values():
+            got = self.roles.get(slot.role)
+            if got is None or tuple(got.shape) != slot.shape:
+                yield f"{slot.role} is {'missing' if got is None else tuple(got.shape)}, the op takes {slot.shape}"
+                return
 
-    def layer_count(self):
-        layers = 1 + max((r[0] for r in self.roles if isinstance(r, tuple)), default=-1)
-        if layers < 1:
-            raise _NoStack("no layers")
-        for i in range(layers):
-            for key, shape in LAYER_SHAPES.items():
-                t = self.roles.get((i, key))
-                if t is None or tuple(t.shape) != shape:
-                    raise _NoStack(f"layer {i} {key}: {None if t is None else tuple(t.shape)}, need {shape}")
-        for role, shape in (("norm", (D,)), ("inv_freq", (DH // 2,))):
-            if tuple(getattr(self.roles.get(role), "shape", ())) != shape:
-                raise _NoStack("final norm / RoPE frequencies")
-        return layers
+    def _constants(self):
+        """The op's RMSNorm eps and its RoPE (no attention scaling) are built in."""
+        if any(abs(v - EPS) > 1e-12 for v in self.census.eps):
+            yield f"RMSNorm eps {self.census.eps}, the op's is {EPS}"
+        elif any(v != 1.0 for v in self.census.rope_scale):
+            yield f"RoPE scaled by {self.census.rope_scale}"
 
-    def mask(self, layers):
-        """The one 4-D mask placeholder that every layer's attention uses, bidirectionally at 1/sqrt(128)."""
-        names = ("query", "key", "value", "attn_mask", "dropout_p", "is_causal", "scale")
-        used = set()
-        for n in self.attention:
-            a = dict(zip(names, n.args))
-            a.update(n.kwargs)
-            scale = a.get("scale")
-            if a.get("dropout_p", 0.0) != 0.0 or a.get("is_causal", False) or \
-                    (scale is not None and abs(scale - DH ** -0.5) > 1e-6):
-                raise _NoStack("attention: dropout, causal or another scale")
-            used.add(a.get("attn_mask"))
-        if len(self.attention) != layers or len(used) != 1:
-            raise _NoStack(f"{len(self.attention)} attentions for {layers} layers, {len(used)} masks")
-        (m,) = used
-        t = self.example_of.get(m)
-        if not (isinstance(m, torch.fx.Node) and m.op == "placeholder" and isinstance(t, torch.Tensor)
-                and t.dim() == 4 and (t.dtype == torch.bool or t.is_floating_point())):
-            raise _NoStack("the attention mask is not a 4-D input of the graph")
-        return m
+    def _attention(self):
+        """One bidirectional, dropout-free attention per layer at scale 1/sqrt(head dim), all under one mask
+        that is a 4-D bool or float input of the graph."""
+        calls = self.census.attentions
+        odd = [c for c in calls if c.get("dropout_p", 0.0) != 0.0 or c.get("is_causal", False)
+               or (c.get("scale") is not None and abs(c["scale"] - DH ** -0.5) > 1e-6)]
+        if odd:
+            yield "an attention with dropout, a causal mask or another scale"
+            return
+        masks = {id(c.get("attn_mask")): c.get("attn_mask") for c in calls}
+        if len(calls) != self.layers or len(masks) != 1:
+            yield f"{len(calls)} attention calls under {len(masks)} masks for {self.layers} layers"
+            return
+        (m,) = masks.values()
+        ex = self.example_of.get(m) if isinstance(m, torch.fx.Node) and m.op == "placeholder" else None
+        if not (isinstance(ex, torch.Tensor) and ex.dim() == 4 and (ex.dtype == torch.bool or ex.is_floating_point())):
+            yield "the attention mask is not a 4-D bool / float input of the graph"
+            return
+        self.mask = m
 
-    def hidden_states(self, mask):
-        """The region's one tensor input besides the mask and the weights: GPU hidden states [B, L, 1024]."""
-        outside = []
-        for n in self.nodes:
-            for a in n.all_input_nodes:
-                if a in self.inside or a is mask or self.is_param(a) or a in outside:
-                    continue
-                if a.op == "placeholder" and isinstance(self.example_of.get(a), (int, torch.SymInt)):
-                    continue        # sizes
-                outside.append(a)
-        if len(outside) != 1:
-            raise _NoStack(f"inputs {[a.name for a in outside]}")
-        t = outside[0].meta.get("example_value")
+    def _hidden_states(self):
+        """Besides parameters, the mask and sizes, one tensor enters: GPU hidden states [B, L, 1024]."""
+        ins = [a for a in self.census.inputs if a is not self.mask and not (
+            a.op == "placeholder" and isinstance(self.example_of.get(a), (int, torch.SymInt)))]
+        if len(ins) != 1:
+            yield f"{len(ins)} tensors enter the region ({[a.name for a in ins]}), not just the hidden states"
+            return
+        t = ins[0].meta.get("example_value")
         if not (isinstance(t, torch.Tensor) and t.dim() == 3 and t.shape[-1] == D and t.is_floating_point()):
-            raise _NoStack("hidden states are not [B, L, 1024]")
-        if not _on_gpu(t):
-            raise _NoStack("hidden states are not on the GPU")
-        return outside[0]
+            yield "the hidden states are not a float [B, L, 1024] tensor"
+        elif not _on_gpu(t):
+            yield "the hidden states are host tensors"
+        else:
+            self.x = ins[0]
 
-    def head(self):
-        """The linear [N, 1024] of a parameter that alone consumes the region's one output."""
-        leaving = [n for n in self.nodes if any(u not in self.inside for u in n.users)]
-        if len(leaving) != 1 or len(leaving[0].users) != 1:
-            raise _NoStack("the stack's output has other users than one head")
-        head = next(iter(leaving[0].users))
+    def _head(self):
+        """One value leaves the region, into a linear of a parameter [N, 1024] (bias optional) and nothing else."""
+        ex = self.census.exits
+        users = list(ex[0].users) if len(ex) == 1 else []
+        if len(users) != 1:
+            yield "the stack's result has another user than one head"
+            return
+        head = users[0]
         if not (head.op == "call_function" and head.target in _LINEAR):
-            raise _NoStack(f"the stack's output goes to {head.target}")
+            yield f"the stack's result feeds {head.target}, not a linear head"
+            return
         hx, hw, hb = _linear_operands(head)
-        w = self.example_of.get(hw) if self.is_param(hw) else None
-        b = self.example_of.get(hb) if hb is not None and self.is_param(hb) else None
-        ok = hx is leaving[0] and isinstance(w, torch.Tensor) and w.dim() == 2 and w.shape[1] == D
-        if not ok or (hb is not None and not (isinstance(b, torch.Tensor) and tuple(b.shape) == (w.shape[0],))):
-            raise _NoStack("the head is not a linear of a parameter [N, 1024]")
-        return head, w, b
+        w = self.example_of.get(hw) if self._param(hw) else None
+        b = self.example_of.get(hb) if hb is not None and self._param(hb) else None
+        good_w = hx is ex[0] and isinstance(w, torch.Tensor) and w.dim() == 2 and w.shape[1] == D
+        good_b = hb is None or (isinstance(b, torch.Tensor) and tuple(b.shape) == (w.shape[0],))
+        if not (good_w and good_b):
+            yield "the head is not a linear of a [N, 1024] parameter (with an [N] bias or none)"
+            return
+        self.head_node, self.head_w, self.head_b = head, w, b
+
+    RULES = (_parameters, _shapes, _constants, _attention, _hidden_states, _head)
 
     def plan(self):
-        self.scan()
-        layers = self.layer_count()
-        mask = self.mask(layers)
-        x = self.hidden_states(mask)
-        head, w, b = self.head()
-        weights = dict(self.roles, head=w)
-        return Plan([n.name for n in self.nodes], x.name, mask.name, self.placeholders.index(mask), head.name,
-                    weights, b, layers, int(w.shape[0]), MAX_TOKENS)
+        for rule in self.RULES:
+            for problem in rule(self):
+                raise _NoStack(problem)
+        weights = dict(self.roles, head=self.head_w)
+        return Plan([n.name for n in self.nodes], self.x.name, self.mask.name, self.placeholders.index(self.mask),
+                    self.head_node.name, weights, self.head_b, self.layers, int(self.head_w.shape[0]), MAX_TOKENS)
 
 
 def _linear_operands(node):
@@ -284,7 +359,7 @@ def find(gm, example_inputs):
             regions.setdefault(root, []).append(n)
     for root, nodes in regions.items():
         try:
-            return _Matcher(root, nodes, example_of, placeholders).plan()
+            return _Candidate(root, nodes, example_of, placeholders).plan()
         except _NoStack as e:
             log.info("torch_xdna: %s is not a stack the GPU op takes: %s", root, e)
     return None
