@@ -147,7 +147,8 @@ def to_dtype(y, dtype):
     if dtype == "bf16":
         return to_bf16(y)
     if dtype == "f16":
-        return np.asarray(y, dtype=F32).astype(np.float16).astype(F32)
+        with np.errstate(over="ignore"):      # beyond the float16 range the cast gives inf, as torch's does
+            return np.asarray(y, dtype=F32).astype(np.float16).astype(F32)
     raise ValueError(dtype)
 
 

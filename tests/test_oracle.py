@@ -178,6 +178,37 @@ def test_to_bf16_matches_torch_and_brute_force():
         assert O.to_bf16(np.array([v], np.float32))[0] == pick
 
 
+def test_to_f16_matches_torch_and_brute_force():
+    """to_dtype(y, "f16") (every f16 GPU comparison's expected values) against torch's `.to(torch.float16)`
+    and a brute force over all finite float16 values: the nearest one, ties to the even bit pattern, inf at
+    and beyond 65520 (the largest finite value plus half its spacing), subnormals, signed zeros, NaN."""
+    rng = np.random.default_rng(5)
+    y = np.concatenate([rng.standard_normal(4000).astype(np.float32) * 10,
+                        (rng.standard_normal(2000) * 2.0 ** rng.integers(-30, 18, 2000)).astype(np.float32),
+                        np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, -65520.0, 1e6, 2.0 ** -24, 2.0 ** -25,
+                                  3 * 2.0 ** -26, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, 6e-8, np.nan], np.float32)])
+    got = O.to_dtype(y, "f16")
+    want = torch.from_numpy(y).to(torch.float16).float().numpy()
+    assert np.array_equal(got, want, equal_nan=True)
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    f16 = bits.view(np.float16).astype(np.float64)
+    fin = np.isfinite(f16)
+    vals, vbits = f16[fin], bits[fin]
+    for v in y[np.isfinite(y)][::7]:
+        if abs(float(v)) >= 65520.0:
+            pick = np.inf if v > 0 else -np.inf
+        else:
+            d = np.abs(vals - float(v))
+            cand = np.flatnonzero(d == d.min())
+            if len(cand) > 1:             # a tie: the even bit pattern (of the two neighbours)
+                cand = [c for c in cand if vbits[c] % 2 == 0]
+            pick = vals[cand[0]]
+            if pick == 0.0:
+                pick = np.copysign(0.0, float(v))
+        assert O.to_dtype(np.array([v], np.float32), "f16")[0] == np.float32(pick), v
+        assert np.signbit(O.to_dtype(np.array([v], np.float32), "f16")[0]) == np.signbit(np.float32(pick))
+
+
 def test_linear_composite_matches_cpu_route():
     g = torch.Generator().manual_seed(8)
     x = torch.randn(50, 200, generator=g).to(torch.bfloat16)

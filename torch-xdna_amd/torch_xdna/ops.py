@@ -1,11 +1,12 @@
 """xdna::linear / linear_cat / linear_i8 / conv3x3, the custom ops the backend puts in place of
-offloadable GEMMs and convs, plus xdna::conv3x3_fused, the GPU form of the conv composite.
+offloadable GEMMs and convs; xdna::conv3x3_fused and xdna::conv3x3_chain, the GPU forms of the conv
+composite and of a chain of them; and xdna::qwen3_stack, the fused transformer-stack op (its GPU
+implementation is stack.py).
 
 The schemas, fake (meta) functions and the `cfg_id` indirection are those of the reference
-(torch_xdna/ops.py:14-76 in the reference), so graphs built for it run unchanged. To the rest of
+(torch_xdna/ops.py:14-89 in the reference), so graphs built for it run unchanged. To the rest of
 torch.compile each op is opaque with a shape function; Inductor compiles everything around it and
-calls it as an extern kernel. The reference's xdna::qwen3_stack (a fused transformer-stack op) is
-not part of this build.
+calls it as an extern kernel.
 """
 
 from typing import Optional
