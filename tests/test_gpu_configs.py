@@ -183,12 +183,51 @@ def test_c4_large_conv(gpu, shape):
     assert torch.equal(got, want), f"{int((got != want).sum())} of {want.numel()} differ"
     wq_ref = ref.wq.numpy()
     _sampled_conv_check(xq_r, wq_ref, q.cpu().numpy(), shift, True, 500, seed=1)
-    # the op's fused conv + dequantize (one launch, the tail split included) against the two-launch form
+    # the op's fused conv + dequantize (one launch, the tail split included; above 128 MB of output its
+    # stores are non-temporal) against the reference's CPU dequantize of the CPU route's integers
+    # (cpu_route.conv_dequant, conv.py:48-51) and against the two-launch form
     scale = torch.from_numpy(O.conv_scale(sw.cpu().numpy(), shift)).to(gpu)
     bias = (torch.randn(c, generator=_gen(23)) * 0.1).to(gpu)
-    y2 = kernels.conv_dequant(q, True, scale, sx, bias, torch.float32)
     y1 = kernels.conv3x3_dequant(xq, wq, shift, True, scale, sx, bias, torch.float32)
+    assert torch.equal(scale.cpu(), ref.scale)
+    y_ref = cpu_route.conv_dequant(want, ref.scale, sx.cpu().view(-1, 1, 1, 1), bias.cpu(), torch.float32)
+    y1c = y1.cpu()
+    assert torch.equal(y1c, y_ref), f"{int((y1c != y_ref).sum())} of {y_ref.numel()} differ"
+    del y1c, y_ref
+    y2 = kernels.conv_dequant(q, True, scale, sx, bias, torch.float32)
     assert torch.equal(y1, y2), f"{int((y1 != y2).sum())} of {y2.numel()} differ"
+
+
+@pytest.mark.parametrize("shape", [(1, 256, 1536, 64), (8, 256, 256, 256)])
+def test_c4_op_full_size(gpu, shape):
+    """The op xdna::conv3x3_fused as a GPU graph calls it, at C4's full sizes, twice on one layer: the first
+    call quantizes, calibrates the shift on image 0, runs the fused conv + dequantize launch and compares
+    it with the CPU composite (verify "first"); the second reuses the layer. Both outputs equal the
+    reference composite on the CPU (oracle/cpu_route.py: quantize, exact conv, shift, dequantize), bit for
+    bit, with no fallback."""
+    from oracle import cpu_route
+    from torch_xdna import Config, conv, ops, runtime
+
+    conv._layers.clear()
+    runtime.stats.reset()
+    cid = ops.config_id(Config(policy="gpu", verify="first"))
+    c = shape[1]
+    wt = torch.randn(c, c, 3, 3, generator=_gen(31)) * 0.02
+    ref = cpu_route.ConvLayerCPU(wt, True)
+    wg = wt.to(gpu)
+    for seed in (32, 33):
+        x = torch.randn(*shape, generator=_gen(seed))
+        y = torch.ops.xdna.conv3x3_fused(x.to(gpu), wg, None, True, cid).cpu()
+        xq, sx = cpu_route.conv_quant(x)
+        if ref.shift is None:
+            ref.calibrate(xq[0])
+        want = cpu_route.conv_dequant(ref(xq), ref.scale, sx, None, torch.float32)
+        assert torch.equal(y, want), f"{int((y != want).sum())} of {want.numel()} differ"
+        del x, y, xq, want
+    layer = conv._layer(wg, shape[2], shape[3], True)
+    assert layer.shift == ref.shift and layer.device == "gpu" and layer.checked == {"fused"}
+    s = runtime.stats.as_dict()
+    assert s["calls"] == {"gpu": 2} and not s["fallbacks"], s
 
 
 # VGG16's thirteen 3x3 convs have these nine distinct (Ci, Co, H=W) shapes
