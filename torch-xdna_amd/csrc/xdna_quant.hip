@@ -214,8 +214,12 @@ __global__ __launch_bounds__(256) void quant_rows_wave_kernel(const void* __rest
 // prefetch their next row: with one row per block the registers of a second row are not needed, so more
 // blocks are resident (bf16, G 4: 8192 x 14336 64.2 us against 67.2 us persistent, 8192 x 4096 20.0-21.1
 // against 21.4, 3000 x 3072 8.5 against 8.8; float32 2000 x 8192 16.2 against 16.9, all before the second
-// buffer was dropped). (A wave per row holds such a row in up to 224 registers.)
-template <int DT, int G, bool NT>
+// buffer was dropped). (A wave per row holds such a row in up to 224 registers.) NTS: the int8 rows leave as
+// non-temporal stores, for outputs that do not stay in the caches anyway (at least 16 MB): the kernel then reads
+// and writes HBM like a plain stream of its bytes (bf16 8192 x 4096 measured 16.5 against 20.0 us, 0.76 of
+// 8 TB/s; 8192 x 14336 with non-temporal loads 62.3 against 64.3 us, where a copy-like stream of the same
+// bytes with no arithmetic takes 62.2 us).
+template <int DT, int G, bool NT, bool NTS>
 __global__ __launch_bounds__(256) void quant_rows_block_kernel(const void* __restrict__ x, int64_t k, int64_t ld_x,
                                                                int8_t* __restrict__ q, int64_t ld_q, int64_t k_pad,
                                                                float* __restrict__ s) {
@@ -260,7 +264,9 @@ __global__ __launch_bounds__(256) void quant_rows_block_kernel(const void* __res
         for (int e = 0; e < VEC; ++e) f[l * VEC + e] = v[j][l].get(e);
       uint32_t w[4];
       quant_pack<16>(f, sc, rc, w);
-      *reinterpret_cast<uint4*>(qr + (int64_t)gi * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+      const u32x4 word = {w[0], w[1], w[2], w[3]};
+      if constexpr (NTS) __builtin_nontemporal_store(word, reinterpret_cast<u32x4*>(qr + (int64_t)gi * 16));
+      else *reinterpret_cast<u32x4*>(qr + (int64_t)gi * 16) = word;
     }
   }
   for (int64_t c = k + t; c < k_pad; c += 256) qr[c] = 0;
@@ -389,11 +395,13 @@ int launch_quant_rows(const void* x, int64_t rows, int64_t k, int64_t ld_x, int8
   const bool few = rows < 512;
   if (k % 16 == 0 && gpl > 2 && ngr <= 256 * (DT == XDNA_F32 ? 4 : 8) && rows < (int64_t(1) << 31)) {
     const bool nt = rows * k * ESZ >= (int64_t(128) << 20);   // half the Infinity Cache
+    const bool nts = rows * k_pad >= (int64_t(16) << 20);       // an output well beyond the L2 caches
     const dim3 bg((unsigned)rows);                              // one block per row
 #define XDNA_QB(G_)                                                                                           \
   {                                                                                                           \
-    if (nt) quant_rows_block_kernel<DT, G_, true><<<bg, 256, 0, st>>>(x, k, ld_x, q, ld_q, k_pad, s);         \
-    else quant_rows_block_kernel<DT, G_, false><<<bg, 256, 0, st>>>(x, k, ld_x, q, ld_q, k_pad, s);           \
+    if (nt) quant_rows_block_kernel<DT, G_, true, true><<<bg, 256, 0, st>>>(x, k, ld_x, q, ld_q, k_pad, s);   \
+    else if (nts) quant_rows_block_kernel<DT, G_, false, true><<<bg, 256, 0, st>>>(x, k, ld_x, q, ld_q, k_pad, s); \
+    else quant_rows_block_kernel<DT, G_, false, false><<<bg, 256, 0, st>>>(x, k, ld_x, q, ld_q, k_pad, s);    \
   }
     if (ngr <= 256) {
       XDNA_QB(1)
