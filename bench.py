@@ -13,7 +13,7 @@ configs; seed 0), with inputs and device-resident int8 weights already in HBM:
                 (xdna::conv3x3_fused: per-image quantize -> conv with the calibrated shift ->
                 dequantize, ReLU fused), with the conv kernel's back-to-back time beside it; C2; the
                 decode GEMMs (HBM-bound); the activation quantize alone at bf16 8192 x 14336 and
-                8192 x 4096 (HBM-bound); and the C3 chain end to end.
+                8192 x 4096 (HBM-bound); the C3 chain end to end; and VGG-16's features at batch 8.
   c2            Qwen3-0.6B projections as xdna::linear_cat runs them on the GPU: for M in
                 {128, 512, 1024, 3000}, bf16 x -> quantize -> fused GEMM -> bf16, for qkv
                 (N 4096, K 1024), gate/up (N 6144, K 1024) and down (N 1024, K 3072).
@@ -518,11 +518,13 @@ def bench_c5(a, dev):
 def bench_headline(a, dev):
     """C5 M=8192 (the largest single-GPU config) as the line; as sub-records, each with its own roofline
     and CPU baseline: C4's two 256-channel convs (as the op), C2, the decode GEMMs (M 1 and 16, HBM-bound),
-    the activation quantize alone at 8192 x 14336 and 8192 x 4096 (HBM-bound), and the C3 chain."""
+    the activation quantize alone at 8192 x 14336 and 8192 x 4096 (HBM-bound), the C3 chain, and VGG-16's
+    features at batch 8 through torch.compile(backend="xdna")."""
     out = bench_c5(a, dev)
     out["sub"] = (bench_c4(a, dev)["sub"] + [dict(bench_c2(a, dev), workload_key="C2"),
                                               dict(bench_decode(a, dev), workload_key="decode")]
-                  + bench_quant(a, dev)["sub"] + [dict(bench_c3(a, dev), workload_key="C3")])
+                  + bench_quant(a, dev)["sub"] + [dict(bench_c3(a, dev), workload_key="C3"),
+                                                  dict(bench_vgg16(a, dev), workload_key="VGG-16 b8")])
     return out
 
 
@@ -909,10 +911,46 @@ def bench_vgg16(a, dev):
                         "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None,
                         "kernel": "whole step (13 convs, their quantize / requantize passes, the final pool)"}}
     if not a.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_conv(1, 256, 56, 56, 1, "one VGG-16 conv3 layer 256->256 at 1x256x56x56: "
-                                                "torch CPU quantize + exact float conv2d of the integers + shift + "
-                                                "dequantize")
+        out["cpu_baseline"] = cpu_baseline_vgg16(net, n, hw, ops)
     return out
+
+
+def cpu_baseline_vgg16(net, n, hw, ops):
+    """The reference's CPU route for the whole VGG-16 features at batch n (what its backend runs on the CPU,
+    conv.py:43-51 per conv): per conv, per-image quantize, exact float conv of the integers, shift / round /
+    saturate, dequantize + bias; the graph's ReLUs and 2x2 max-pools in float32 between. Each conv's shift is
+    fixed on the first run (a warm-up run), as the reference fixes it on the first call."""
+    from oracle import cpu_route
+
+    x = torch.randn(n, 3, hw, hw, generator=gen(1))
+    net = net.to("cpu")
+    mods = list(net.features if hasattr(net, "features") else net)
+    layers = []
+    for m in mods:
+        if isinstance(m, torch.nn.Conv2d):
+            layers.append(("conv", cpu_route.ConvLayerCPU(m.weight.detach(), False), m.bias.detach()))
+        elif isinstance(m, torch.nn.MaxPool2d):
+            layers.append(("pool", None, None))
+        else:
+            layers.append(("relu", None, None))
+
+    def step():
+        y = x
+        for kind, L, b in layers:
+            if kind == "conv":
+                xq, sx = cpu_route.conv_quant(y)
+                if L.shift is None:
+                    L.calibrate(xq[0])
+                y = cpu_route.conv_dequant(L(xq), L.scale, sx, b, torch.float32)
+            elif kind == "pool":
+                y = torch.nn.functional.max_pool2d(y, 2, 2)
+            else:
+                y = torch.relu(y)
+        return y
+
+    return cpu_protocol(step, ops, f"the full step: VGG-16 features at {n}x3x{hw}x{hw} through the reference's CPU "
+                        "route (per conv: torch CPU quantize + exact float conv2d of the integers + shift + dequantize "
+                        "+ bias; ReLU and max-pool in float32)", budget_s=25.0, warmup=2)
 
 
 # OmniVoice's backbone step (the reference's results/omnivoice_npu.md:3-12): 28 Qwen3-0.6B layers,

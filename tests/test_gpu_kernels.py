@@ -162,6 +162,22 @@ def test_gemm_dequant(gpu, out, m, n, k, bias):
     assert not bad.any(), f"{bad.sum()} of {got.size} differ, e.g. {got[bad][:4]} vs {want[bad][:4]}"
 
 
+@pytest.mark.parametrize("m,n,out", [(8192, 4096, "f32"), (8192, 8192, "bf16"), (8000, 4100, "f16")])
+def test_gemm_dequant_large_output(gpu, m, n, out):
+    """Fused-dequantize outputs of 128 MB (f32 8192 x 4096, bf16 8192 x 8192) and a ragged f16 one: every
+    output against the oracle's float32 dequantize of the C oracle's sums, with bias."""
+    from torch_xdna import kernels
+
+    k = 256
+    a, w = _i8((m, k), seed=m + 1), _i8((n, k), seed=n + 2)
+    sx, sw, b = torch.rand(m) + 0.01, torch.rand(n) + 0.01, torch.randn(n)
+    y = kernels.mm_i8_dequant(a.to(gpu), sx.to(gpu), w.to(gpu), sw.to(gpu), b.to(gpu), DT[out])
+    want = O.to_dtype(O.dequant(c_oracle.gemm_i32(a.numpy(), w.numpy()), sx.numpy(), sw.numpy(), b.numpy()), out)
+    got = _f32(y)
+    bad = ~((got == want) | (np.isnan(got) & np.isnan(want)))
+    assert not bad.any(), f"{bad.sum()} of {got.size} differ"
+
+
 @pytest.mark.parametrize("out", ["f32", "bf16", "f16"])
 def test_gemm_dequant_range(gpu, out):
     """Scales from 1e-45 to 3e38 put the fused epilogue's outputs in every float range (zero,
