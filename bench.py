@@ -113,24 +113,36 @@ def gemm_sets(shapes, dev, nsets_min=1, x_dtype=torch.bfloat16, bias=False, seed
     return sets
 
 
+def row_fused(x, wq):
+    """Whether the route runs this shape as one launch that quantizes its single row itself
+    (xdna_linear_row: decode, M = 1), as runtime._gpu_linear decides."""
+    return kernels.linear_row_ok(x, wq.shape[1])
+
+
 def run_gemm_step_split(items, ev=None):
     """One step ordered as all activation quantizes, then all fused GEMMs (the same work as
-    quantize -> GEMM per shape); ev = three events recorded at the start, between the two groups and
-    at the end, so ev[1] -> ev[2] brackets exactly the step's GEMM launches, back to back."""
+    quantize -> GEMM per shape; a single row, which the route quantizes inside its GEMM launch, has
+    no quantize launch and runs with the GEMMs); ev = three events recorded at the start, between the
+    two groups and at the end, so ev[1] -> ev[2] brackets exactly the step's GEMM launches, back to back."""
     if ev:
         ev[0].record()
-    qs = [kernels.quant_rows(x) for x, wq, sw, b, M, N, K in items]
+    qs = [None if row_fused(x, wq) else kernels.quant_rows(x) for x, wq, sw, b, M, N, K in items]
     if ev:
         ev[1].record()
     for (x, wq, sw, b, M, N, K), q in zip(items, qs):
-        kernels.mm_i8_dequant(q[0], q[1], wq, sw, b, x.dtype)
+        if q is None:
+            kernels.linear_row(x, wq, sw, b, x.dtype)
+        else:
+            kernels.mm_i8_dequant(q[0], q[1], wq, sw, b, x.dtype)
     if ev:
         ev[2].record()
 
 
-def gemm_bytes(M, N, K, xbytes, ybytes, bias):
-    """Algorithmic HBM bytes of the fused-epilogue GEMM launch: A int8 + W int8 + sx + sw (+ bias) + y."""
-    return M * K + N * K + 4 * M + 4 * N + (4 * N if bias else 0) + M * N * ybytes
+def gemm_bytes(M, N, K, xbytes, ybytes, bias, fused=False):
+    """Algorithmic HBM bytes of the fused-epilogue GEMM launch: A int8 + W int8 + sx + sw (+ bias) + y;
+    fused (a single row quantized inside the launch): the float row instead of A int8 and sx."""
+    a = M * K * xbytes if fused else M * K + 4 * M
+    return a + N * K + 4 * N + (4 * N if bias else 0) + M * N * ybytes
 
 
 def quant_bytes(M, K, xbytes):
@@ -372,7 +384,8 @@ def back_to_back_us(calls, launches):
 
 
 def per_shape_us(sets, launches=10):
-    """Microseconds per launch of each shape's fused GEMM: `launches` back-to-back launches of that
+    """Microseconds per launch of each shape's fused GEMM (for a single row the one launch that also
+    quantizes it): `launches` back-to-back launches of that
     shape behind a gate and a pre-heat, between two events. The launches cycle through enough copies of the weight
     (the sets' own, then clones) that they span more than the 256 MB Infinity Cache, so a weight is
     never read from the cache a previous launch filled."""
@@ -385,8 +398,9 @@ def per_shape_us(sets, launches=10):
         weights = [sets[i][j][1] if i < len(sets) else sets[0][j][1].clone() for i in range(ncopies)]
         for i in range(launches):
             x, wq, sw, b, M, N, K = sets[i % len(sets)][j]
-            ops.append((kernels.quant_rows(x), weights[i % ncopies], sw, b, x.dtype))
-        calls = [lambda o=o: kernels.mm_i8_dequant(o[0][0], o[0][1], o[1], o[2], o[3], o[4]) for o in ops]
+            ops.append((x if row_fused(x, wq) else kernels.quant_rows(x), weights[i % ncopies], sw, b, x.dtype))
+        calls = [lambda o=o: kernels.linear_row(o[0], o[1], o[2], o[3], o[4]) if torch.is_tensor(o[0]) else
+                 kernels.mm_i8_dequant(o[0][0], o[0][1], o[1], o[2], o[3], o[4]) for o in ops]
         out.append(back_to_back_us(calls, launches))
     return out
 
@@ -414,10 +428,18 @@ def traffic(workload):
         return None
 
 
-def gemm_kernels(dev, shapes):
-    """The GEMM kernels the shapes launch (the library's tile choice per shape, tuned table applied)."""
-    tiles = sorted({kernels.gemm_variant(dev, M, N, kernels.round_up(K, 16)) for M, N, K in shapes})
-    kernel_of = {"small": "mm_small_kernel", "gemv": "mm_gemv_kernel", "seg4": "mm_seg4_kernel"}
+def shape_variant(dev, M, N, K, fused):
+    """The kernel variant a shape launches: "rowq" for a single row quantized inside the launch, else the
+    library's tile choice (tuned table applied)."""
+    return "rowq" if fused else kernels.gemm_variant(dev, M, N, kernels.round_up(K, 16))
+
+
+def gemm_kernels(dev, shapes, fused=None):
+    """The GEMM kernels the shapes launch (per shape the variant of shape_variant)."""
+    fused = fused or [False] * len(shapes)
+    tiles = sorted({shape_variant(dev, M, N, K, f) for (M, N, K), f in zip(shapes, fused)})
+    kernel_of = {"small": "mm_small_kernel", "gemv": "mm_gemv_kernel", "seg4": "mm_seg4_kernel",
+                 "rowq": "mm_rowq_kernel"}
     names = sorted({kernel_of.get(t.split("_")[0], "mm_tile_kernel") for t in tiles})
     return f"{' + '.join(names)} (EPI_DQ): {', '.join(tiles)}"
 
@@ -451,10 +473,11 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
     xb = x_dtype.itemsize
     nshape = len(shapes)
     g_sec = sum(g_ms) / 1e3                            # GEMM launches of the timed steps
-    launch_bytes = [gemm_bytes(M, N, K, xb, yb, bias) for M, N, K in shapes]
+    fused = [row_fused(x, wq) for x, wq, sw, b, M, N, K in sets[0]]
+    launch_bytes = [gemm_bytes(M, N, K, xb, yb, bias, f) for (M, N, K), f in zip(shapes, fused)]
     g_bytes = sum(launch_bytes) * reps
-    nq = nshape
-    q_bytes = sum(quant_bytes(M, K, xb) for M, N, K in shapes) * reps
+    nq = nshape - sum(fused)
+    q_bytes = sum(quant_bytes(M, K, xb) for (M, N, K), f in zip(shapes, fused) if not f) * reps
     q_sec = sum(q_ms) / 1e3
     achieved = ops_step * reps / g_sec / 1e12
     bound_us = sum(roofline_us(2 * M * N * K, nb) for (M, N, K), nb in zip(shapes, launch_bytes))
@@ -465,11 +488,14 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
                      "step's quantizes then its GEMMs with events between; host_ms_per_step: the same "
                      "steps launched without a gate, wall clock",
            "config": {"workload": workload, "shapes_mnk": shapes, "x_dtype": str(x_dtype).replace("torch.", ""),
-                      "bias": bias, "rotating_sets": len(sets), "quantize": "a launch of its own"},
+                      "bias": bias, "rotating_sets": len(sets),
+                      "quantize": "a launch of its own" + ("" if not any(fused) else
+                                                           "; single rows (M = 1): inside their GEMM launch "
+                                                           "(xdna_linear_row)")},
            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                         "frac": round(achieved / PEAK_INT8_TOPS, 4),
                         "traffic": None if a.tile or a.operands != "randn" else traffic(label.lower()),
-                        "kernel": gemm_kernels(dev, shapes),
+                        "kernel": gemm_kernels(dev, shapes, fused),
                         "launches": nshape * reps, "avg_launch_us": round(g_sec / (nshape * reps) * 1e6, 2),
                         "alg_bytes_per_launch": round(g_bytes / (nshape * reps)),
                         "hbm_GBs_equiv": round(g_bytes / g_sec / 1e9, 1),
@@ -484,8 +510,8 @@ def gemm_result(a, dev, shapes, x_dtype, bias, workload, label, bound="mfma"):
                                 "frac": round(gbs / PEAK_HBM_GBS, 4), "TOPS": round(achieved, 2)})
     for j, (M, N, K) in enumerate(shapes):
         t = per_shape[j] / 1e6
-        b = gemm_bytes(M, N, K, xb, yb, bias)
-        tile = kernels.gemm_variant(dev, M, N, kernels.round_up(K, 16))
+        b = gemm_bytes(M, N, K, xb, yb, bias, fused[j])
+        tile = shape_variant(dev, M, N, K, fused[j])
         out["per_shape"].append({"mnk": [M, N, K], "tile": tile,
                                  "us": round(t * 1e6, 2), "TOPS": round(2 * M * N * K / t / 1e12, 1),
                                  "GBs": round(b / t / 1e9, 1),

@@ -169,6 +169,21 @@ int xdna_gemm_i8_dequant_ws(const int8_t* a, int64_t lda, const float* sx, const
                             const float* sw, const float* bias, void* y, int y_dtype, int64_t ldy,
                             int64_t m, int64_t n, int64_t k, void* ws, int64_t ws_bytes, void* stream);
 
+/* The W8A8 linear of ONE activation row (decode, M = 1) in one launch: the row's per-row quantize
+ * (xdna_quant_rows' arithmetic, replacing torch_xdna/runtime.py:287 `_quant_rows` in `_gemm` and
+ * :145-148) and the GEMM with the dequantize of xdna_gemm_i8_dequant (runtime.py:288-296 and :350-353,
+ * `linear` / `linear_cat` at one row), so
+ *   y[n] = ((float)sum_k q[k] * w[n, k] * s) * sw[n] (+ bias[n]),  s = max(max_k |x[k]|, 1e-8f) / 127,
+ *   q[k] = clamp(round_half_even(x[k] / s), -127, 127),
+ * bit for bit what xdna_quant_rows followed by xdna_gemm_i8_dequant computes. x: kx elements of
+ * x_dtype (XDNA_F32/BF16/F16), 16-byte aligned, kx * element size a multiple of 16 bytes; the
+ * elements [kx, k) count as zeros. w: [n, k] int8 with row stride ldw (k % 16 == 0,
+ * 16 <= k <= XDNA_LINEAR_ROW_KMAX). y: n elements of y_dtype. sx: NULL, or where the row's scale s
+ * is written (when n > 0). No workspace. */
+#define XDNA_LINEAR_ROW_KMAX 32768
+int xdna_linear_row(const void* x, int x_dtype, int64_t kx, const int8_t* w, int64_t ldw, const float* sw,
+                    const float* bias, void* y, int y_dtype, int64_t n, int64_t k, float* sx, void* stream);
+
 /* The bf16 GEMM of precision "bf16": y[m, n] = sum_k a[m, k] * w[n, k] with bf16 operands and float32
  * accumulation (+ bias[n] in float32), converted to y_dtype (XDNA_F32/BF16/F16, round to nearest
  * even). Replaces kernels.mm_bf16 (torch_xdna/kernels.py:167-169) behind runtime._npu_bf16 /

@@ -47,6 +47,13 @@ def mm_i8_dequant(a, sx, w, sw, bias, out_dtype):
     return _to_torch(O.to_dtype(y, _NP_OF[out_dtype]), out_dtype)
 
 
+def linear_row(x2d, w, sw, bias, out_dtype, sx=None):
+    xq, s = quant_rows(x2d, w.shape[1])
+    if sx is not None:
+        sx[:1].copy_(s)
+    return mm_i8_dequant(xq, s, w, sw, bias, out_dtype)
+
+
 def bf16_rows(x2d, k_pad):
     out = torch.zeros((x2d.shape[0], k_pad), dtype=torch.bfloat16)
     out[:, :x2d.shape[1]] = x2d
@@ -125,7 +132,7 @@ def nhwc_to_nchw(q):
     return q.permute(0, 3, 1, 2).contiguous()
 
 
-LAUNCHERS = ("quant_rows", "pad_k", "mm_i8", "mm_i8_dequant", "bf16_rows", "mm_bf16", "conv_weight_pack", "conv_quant", "conv3x3",
+LAUNCHERS = ("quant_rows", "pad_k", "mm_i8", "mm_i8_dequant", "linear_row", "bf16_rows", "mm_bf16", "conv_weight_pack", "conv_quant", "conv3x3",
              "conv3x3_calibrate", "conv_dequant", "conv3x3_dequant", "conv_requant_next", "nchw_to_nhwc", "nhwc_to_nchw")
 
 

@@ -65,6 +65,21 @@ def test_argument_validation(lib):
     assert lib.xdna_gemm_i8_dequant_ws(p, 16, p, p, 16, p, None, p, 0, 16, 4, 4, 16, p, -1, None) == -1
     assert lib.xdna_gemm_ws_bytes(4, 4, 15) == -1
     assert "bad sizes" in lib.xdna_last_error().decode()
+    # the one-row linear: dtypes, k's range and multiple, kx's bytes, leading dimension, pointers
+    f = lib.xdna_linear_row
+    assert f(p, 9, 16, p, 16, p, None, p, 1, 4, 16, None, None) == -1
+    assert "x_dtype" in lib.xdna_last_error().decode()
+    assert f(p, 1, 16, p, 16, p, None, p, 7, 4, 16, None, None) == -1
+    assert f(p, 1, 16, p, 24, p, None, p, 1, 4, 24, None, None) == -1            # k % 16
+    assert f(p, 1, 16, p, 32784, p, None, p, 1, 4, 32784, None, None) == -1      # k > XDNA_LINEAR_ROW_KMAX
+    assert "XDNA_LINEAR_ROW_KMAX" in lib.xdna_last_error().decode()
+    assert f(p, 1, 12, p, 16, p, None, p, 1, 4, 16, None, None) == -1            # 12 bf16: 24 bytes
+    assert "kx" in lib.xdna_last_error().decode()
+    assert f(p, 0, 20, p, 16, p, None, p, 1, 4, 16, None, None) == -1            # kx > k
+    assert f(p, 1, 16, p, 8, p, None, p, 1, 4, 16, None, None) == -1             # ldw < k
+    assert f(ctypes.c_void_p(24), 1, 16, p, 16, p, None, p, 1, 4, 16, None, None) == -1   # x unaligned
+    assert f(p, 1, 16, p, 16, None, None, p, 1, 4, 16, None, None) == -1         # no weight scales
+    assert f(None, 1, 16, None, 16, None, None, None, 1, 0, 16, None, None) == 0   # n = 0: nothing to do
     assert lib.xdna_quant_rows(p, 9, 4, 16, 16, p, 16, 16, p, None) == -1
     assert lib.xdna_quant_rows(p, 0, 4, 16, 8, p, 16, 16, p, None) == -1          # ld_x < k
     assert lib.xdna_conv3x3_i8(p, 1, 4, 4, 15, p, 8, 3, 0, p, None, None) == -1    # c_pad % 16

@@ -46,6 +46,34 @@ def test_c1_single_linear(gpu):
     assert np.array_equal(y.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("N,K", [(4096, 4096), (14336, 4096), (4096, 14336)])
+def test_c5_decode_one_row_op(gpu, N, K):
+    """xdna::linear and xdna::linear_cat at one row (decode) on C5's weights: the route runs the one launch
+    that quantizes the row itself (xdna_linear_row), verified against the CPU route on every call, and its
+    outputs equal the oracle's bit for bit."""
+    from torch_xdna import runtime
+
+    g = _gen(N + K)
+    x = torch.randn(1, K, generator=g).to(torch.bfloat16)
+    w = torch.randn(N, K, generator=g) * 0.02
+    b = torch.randn(N, generator=g) * 0.01
+    runtime._verified.clear()
+    cid = _cid(policy="gpu", verify="always")
+    y = torch.ops.xdna.linear(x.to(gpu), w.to(gpu), b.to(gpu), False, cid)
+    halves = [w[:N // 2], w[N // 2:]]
+    y2 = torch.ops.xdna.linear_cat(x.to(gpu), [h.to(gpu) for h in halves], [b[:N // 2].to(gpu), b[N // 2:].to(gpu)],
+                                   cid)
+    assert _stats()["calls"] == {"gpu": 2}
+    assert any(k[0] == "row" for k in runtime._verified), "the one-row launch did not run"
+    xq, sx = O.quant_rows(x.float().numpy())
+    wq, sw = O.quant_rows(w.numpy())
+    want = O.to_bf16(O.dequant(c_oracle.gemm_i32(xq, wq), sx, sw, b.numpy()))
+    assert y.dtype == torch.bfloat16 and np.array_equal(y.float().cpu().numpy(), want)
+    wq2, sw2 = O.weight_quant_cat([h.numpy() for h in halves])
+    want2 = O.to_bf16(O.dequant(c_oracle.gemm_i32(xq, wq2), sx, sw2, b.numpy()))
+    assert np.array_equal(y2.float().cpu().numpy(), want2)
+
+
 @pytest.mark.parametrize("M", [128, 512, 1024, 3000])
 def test_c2_linear_cat(gpu, M):
     g = _gen(M)

@@ -213,6 +213,113 @@ def _bf16_bracket(got, want, bound, out):
     assert not bad.any(), f"{bad.sum()} of {got.size} outside the bound, e.g. {got[bad][:3]} vs {want[bad][:3]}"
 
 
+# ------------------------------------------------------------------------------ one row, quantize in the launch
+def _row_oracle(x, wq, sw, b, kp, out):
+    """The oracle's one-row W8A8 linear: quantize the row, pad it to kp, exact sums, dequantize, cast."""
+    xq, sx = O.quant_rows(x.float().numpy())
+    xq = np.pad(xq, ((0, 0), (0, kp - xq.shape[1])))
+    acc = c_oracle.gemm_i32(xq, wq.numpy())
+    return O.to_dtype(O.dequant(acc, sx, sw.numpy(), None if b is None else b.numpy()), out), sx
+
+
+@pytest.mark.parametrize("xd", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("out", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("n,k,kp,bias", [(300, 1000, 1008, True), (4096, 4096, 4096, False), (14337, 4104, 4112, True),
+                                         (7, 8, 16, False)])
+def test_linear_row(gpu, xd, out, n, k, kp, bias):
+    """xdna_linear_row (the row's quantize, the GEMM and the dequantize in one launch) against the oracle:
+    every output and the row's scale bit for bit; x shorter than the weight rows (the padding counts as
+    zeros, the weights there are not zero), K past whole 4 KB rounds, N ragged with 4 columns per wave
+    (14337), 1 column per wave (300, 4096, 7)."""
+    from torch_xdna import kernels
+
+    if xd == "f32" and k % 4 or xd != "f32" and k % 8:
+        pytest.skip("kx elements must fill 16-byte loads")
+    x = _rand((1, k), DT[xd], seed=n + k, outliers=1e-2)
+    wq = _i8((n, kp), seed=n + 1)
+    sw = torch.rand(n) * 1e-3 + 1e-5
+    b = _rand((n,), torch.float32, seed=n + 2) if bias else None
+    sx = torch.full((1,), -1.0, device=gpu)
+    y = kernels.linear_row(x.to(gpu), wq.to(gpu), sw.to(gpu), None if b is None else b.to(gpu), DT[out], sx=sx)
+    want, sx_r = _row_oracle(x, wq, sw, b, kp, out)
+    got = _f32(y)
+    bad = ~((got == want) | (np.isnan(got) & np.isnan(want)))
+    assert not bad.any(), f"{bad.sum()} of {got.size} differ, e.g. {got[bad][:4]} vs {want[bad][:4]}"
+    assert _np(sx).view(np.uint32)[0] == sx_r.view(np.uint32)[0]
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (14336, 4096), (4096, 14336)])
+def test_linear_row_decode_shapes(gpu, n, k):
+    """The C5 decode shapes at one row (bf16 in and out, bias) against the oracle and against the two
+    launches it replaces (quant_rows, then the fused-dequantize GEMM), bit for bit."""
+    from torch_xdna import kernels
+
+    x = _rand((1, k), torch.bfloat16, seed=k, outliers=1e-3)
+    wt = _rand((n, k), torch.float32, seed=n, scale=0.02).to(gpu)
+    wq, sw = kernels.quant_rows(wt)
+    b = _rand((n,), torch.float32, seed=n + k, scale=0.01).to(gpu)
+    y = kernels.linear_row(x.to(gpu), wq, sw, b, torch.bfloat16)
+    xq, sx = kernels.quant_rows(x.to(gpu), k)
+    y2 = kernels.mm_i8_dequant(xq, sx, wq, sw, b, torch.bfloat16)
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    want, _ = _row_oracle(x, wq.cpu(), sw.cpu(), b.cpu(), k, "bf16")
+    assert np.array_equal(_f32(y), want)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_linear_row_special_rows(gpu, dtype):
+    """Rows of zeros, with +inf / -inf / NaN, of subnormals, below the 1e-8 scale floor, with values on
+    half-integers of the scale, and of the dtype's largest values: outputs (NaN where the scale is NaN) and
+    scales against quant_rows + the fused-dequantize GEMM."""
+    from torch_xdna import kernels
+
+    k, n = 1024, 520
+    dt = DT[dtype]
+    base = _rand((1, k), torch.float32, seed=5)
+    rows = {"zeros": torch.zeros(1, k), "tiny": base * 1e-12, "sub": base * 1e-40,
+            "halves": torch.arange(k, dtype=torch.float32).view(1, k) % 255 - 127 + 0.5,
+            "big": torch.full((1, k), float(torch.finfo(dt).max)) * torch.sign(base)}
+    for name, v in (("pinf", float("inf")), ("ninf", float("-inf")), ("nan", float("nan"))):
+        r = base.clone()
+        r[0, 77] = v
+        rows[name] = r
+    wq = _i8((n, k), seed=9).to(gpu)
+    sw = (torch.rand(n) * 1e-2 + 1e-4).to(gpu)
+    for name, r in rows.items():
+        xg = r.to(dt).to(gpu)
+        sx1 = torch.empty(1, device=gpu)
+        y = kernels.linear_row(xg, wq, sw, None, dt, sx=sx1)
+        xq, sx2 = kernels.quant_rows(xg, k)
+        y2 = kernels.mm_i8_dequant(xq, sx2, wq, sw, None, dt)
+        a, b2 = _f32(y), _f32(y2)
+        same = (a == b2) | (np.isnan(a) & np.isnan(b2))
+        assert same.all(), f"{name}: {(~same).sum()} of {a.size} differ"
+        s1, s2 = _np(sx1), _np(sx2)
+        assert (s1.view(np.uint32) == s2.view(np.uint32)).all() or (np.isnan(s1) & np.isnan(s2)).all(), name
+
+
+def test_linear_row_kmax_and_chunks(gpu):
+    """The longest row (XDNA_LINEAR_ROW_KMAX, the most groups per thread) and a weight of more than 1 GB
+    (33000 x 32768: two launches of row chunks, the scale written by the first), against the two
+    launches it replaces."""
+    from torch_xdna import kernels
+
+    k = kernels.LINEAR_ROW_KMAX
+    g = torch.Generator(device=gpu).manual_seed(3)
+    x = torch.randn(1, k, generator=g, device=gpu).to(torch.bfloat16)
+    for n in (600, 33000):
+        wq = torch.randint(-127, 128, (n, k), generator=g, device=gpu, dtype=torch.int8)
+        sw = torch.rand(n, generator=g, device=gpu) * 1e-3
+        b = torch.randn(n, generator=g, device=gpu)
+        sx1 = torch.empty(1, device=gpu)
+        y = kernels.linear_row(x, wq, sw, b, torch.float32, sx=sx1)
+        xq, sx2 = kernels.quant_rows(x, k)
+        y2 = kernels.mm_i8_dequant(xq, sx2, wq, sw, b, torch.float32)
+        assert torch.equal(y, y2), f"n={n}: {int((y != y2).sum())} differ"
+        assert torch.equal(sx1, sx2)
+        del wq
+
+
 @pytest.mark.parametrize("out", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("m,n,k,bias", [(1, 4096, 1024, True), (16, 1000, 520, False), (64, 300, 200, True),
                                         (128, 3072, 1024, True), (300, 520, 1032, False), (700, 1000, 4096, True),

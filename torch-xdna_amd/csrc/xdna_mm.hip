@@ -1426,6 +1426,137 @@ __global__ __launch_bounds__(W * 64) void mm_seg4_kernel(const int8_t* __restric
     }
 }
 
+// ------------------------------------------------------------------------------ one row, quantize in the launch
+// The W8A8 linear of a single activation row (decode, M = 1) as one launch: every workgroup quantizes the
+// whole row itself (max |x|, scale, quant_pack: the arithmetic of the quantize kernels, so the int8 row and
+// its scale are bit for bit theirs), with no flag or wait between workgroups, then streams its weight rows
+// against it as mm_gemv_kernel does. Workgroup of 8 waves:
+//   - each wave issues its first D - 1 weight rounds (4 KB of one row per round, 16 bytes per lane per 1 KB
+//     step), so the weight stream is in flight while the row is reduced;
+//   - the 512 threads load the row (16-byte loads, zeros past its end), agree on its max through LDS, and
+//     write its int8 values to LDS (zeros up to the end of the last 4 KB round);
+//   - each wave takes C consecutive output columns, streaming their weight rows round by round through a
+//     ring of D register sets that runs across its columns; a step's activation is one conflict-free
+//     ds_read_b128 (lane l: bytes 16 l .. +15 of the KB), and one 16x16x64 MFMA puts the step's 16 K
+//     segments on the diagonal, as in mm_gemv_kernel.
+// Every workgroup quantizes the K elements again (about 8 vector instructions each), so C grows with N to
+// keep the number of workgroups near 1.75 per CU. Rows whose scale is NaN quantize their zero padding to
+// -127 rather than 0; their outputs are NaN either way.
+template <int DT, int C, int D, int JM, int EPI>
+__global__ __launch_bounds__(512) void mm_rowq_kernel(const void* __restrict__ x, int64_t kx,
+                                                      const int8_t* __restrict__ w, int64_t ldw, int64_t N, int64_t K,
+                                                      float* __restrict__ sx_out, EpiArgs e) {
+  static_assert(epi_dq(EPI), "the dequantizing epilogues");
+  constexpr int W = 8, KS = 4;
+  using V = Vec16<DT>;
+  constexpr int ESZ = DT == XDNA_F32 ? 4 : 2;
+  constexpr int LPG = 16 / V::N;          // 16-byte loads per group of 16 elements
+  extern __shared__ __attribute__((aligned(16))) int8_t xq[];   // the int8 row, rounds * 4 KB
+  __shared__ int red[W];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int rounds = (int)((K + KS * 1024 - 1) / (KS * 1024));
+  const int items = C * rounds;           // (column, round) pairs of this wave
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(N * ldw));
+  const int64_t ncol0 = ((int64_t)blockIdx.x * W + wave) * C;
+  i32x4 ring[D][KS];
+  int ic = 0, ir = 0;                     // the next item to issue: column ic, round ir
+  auto issue = [&](i32x4 (&dst)[KS]) {
+    const int64_t n = ncol0 + ic;
+    const bool live = ic < C && n < N;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int64_t k = (int64_t)ir * (KS * 1024) + s * 1024 + 16 * lane;
+      dst[s] = buf_load16(rw, live && k < K ? (uint32_t)(n * ldw + k) : OOB);
+    }
+    if (++ir == rounds) {
+      ir = 0;
+      ++ic;
+    }
+  };
+  static_for<0, D - 1>([&](auto d) { issue(ring[decltype(d)::value]); });
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)(kx * ESZ));
+  V v[JM][LPG];
+#pragma unroll
+  for (int j = 0; j < JM; ++j) {
+    const uint32_t g = (uint32_t)(t + j * W * 64);
+#pragma unroll
+    for (int l = 0; l < LPG; ++l) v[j][l].raw = buf_load_u4(rx, g * (16 * ESZ) + l * 16);
+  }
+  AbsMaxBits<DT> am;
+#pragma unroll
+  for (int j = 0; j < JM; ++j)
+#pragma unroll
+    for (int l = 0; l < LPG; ++l) am.add(v[j][l]);
+  const int wmax = wave_max_i(am.lane_bits());
+  if (lane == 0) red[wave] = wmax;
+  __syncthreads();
+  int mb = red[0];
+#pragma unroll
+  for (int u = 1; u < W; ++u) mb = max(mb, red[u]);
+  const float sc = scale_from_amax(bits_to_abs<DT>(mb));
+  const float rc = 1.0f / sc;
+  if (sx_out && blockIdx.x == 0 && t == 0) *sx_out = sc;
+  const int ngr = rounds * KS * 64;       // 16-byte groups of the LDS row
+#pragma unroll
+  for (int j = 0; j < JM; ++j) {
+    const int g = t + j * W * 64;
+    if (g < ngr) {
+      float f[16];
+#pragma unroll
+      for (int l = 0; l < LPG; ++l)
+#pragma unroll
+        for (int q = 0; q < V::N; ++q) f[l * V::N + q] = v[j][l].get(q);
+      uint32_t b[4];
+      quant_pack<16>(f, sc, rc, b);
+      *reinterpret_cast<u32x4*>(xq + g * 16) = u32x4{b[0], b[1], b[2], b[3]};
+    }
+  }
+  __syncthreads();                        // the last barrier: waves past N run on with zero loads
+
+  Epi1Ops<EPI> ops;
+  ops.sx = sc;
+  auto column_ops = [&](int64_t n) {
+    const int64_t nc = min(n, N - 1);
+    ops.sw = e.sw[nc];
+    ops.b = e.bias ? e.bias[nc] : 0.0f;
+  };
+  column_ops(ncol0);
+  int cc = 0, rr = 0;                     // the item being consumed
+  i32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+  for (int i0 = 0; i0 < items; i0 += D) {
+    static_for<0, D>([&](auto dc) {
+      constexpr int d = decltype(dc)::value;
+      if (i0 + d < items) {
+        issue(ring[(d + D - 1) % D]);     // the set item i0 + d - 1 used
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const i32x4 xv = *reinterpret_cast<const i32x4*>(xq + rr * (KS * 1024) + s * 1024 + 16 * lane);
+          if (s & 1) acc1 = mfma16x16x64(ring[d][s], xv, acc1);
+          else acc0 = mfma16x16x64(ring[d][s], xv, acc0);
+        }
+        if (++rr == rounds) {
+          // lane l holds D[4 (l / 16) + j][l % 16] in element j: the diagonal is in lanes with
+          // (l % 16) / 4 == l / 16, element l % 4
+          const i32x4 acc = acc0 + acc1;
+          const int i = lane & 15, j = lane & 3;
+          const int32_t dv = j == 0 ? acc[0] : j == 1 ? acc[1] : j == 2 ? acc[2] : acc[3];
+          int32_t sum = (i >> 2) == (lane >> 4) ? dv : 0;
+#pragma unroll
+          for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+          const int64_t n = ncol0 + cc;
+          if (lane == 0 && n < N) epilogue1<EPI>(e, 0, n, sum, ops);
+          rr = 0;
+          ++cc;
+          acc0 = i32x4{0, 0, 0, 0};
+          acc1 = i32x4{0, 0, 0, 0};
+          if (cc < C) column_ops(ncol0 + cc);
+        }
+      }
+    });
+  }
+}
+
 // ------------------------------------------------------------------------------ dispatch
 struct TileCfg {
   int bm, bn, waves, kg;   // kg: K groups of `waves` waves each
@@ -1862,6 +1993,52 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
   return XDNA_OK;
 }
 
+// xdna_linear_row's launches. Columns per wave: 4 (with a 3-deep ring) once that still leaves 1.75 workgroups
+// per CU, else 1 (2-deep), from a sweep of 1 / 2 / 4 columns with 2- to 4-deep rings over the C5 decode
+// shapes (bf16, rotating weights): 14336 x 4096 12.6 us with 4 columns against 14.6 with 1, 4096 x 14336 and
+// 4096 x 4096 13.0 / 6.4 us with 1 against 16.5 / 7.2 with 4. The weight goes in row chunks one buffer
+// resource can address, each chunk a launch of its own.
+template <int DT, int EPI>
+int launch_rowq(const void* x, int64_t kx, const int8_t* w, int64_t ldw, int64_t N, int64_t K, float* sx,
+                const EpiArgs& e, hipStream_t st) {
+  const int64_t rounds = cdiv(K, 4096);
+  const int jm = (int)cdiv(rounds * 256, 512);   // 16-element groups of the row per thread
+  const size_t lds = (size_t)rounds * 4096;
+  const bool c4 = N >= 32 * (7 * (int64_t)device_cus() / 4);
+  const int64_t cols = c4 ? 32 : 8;              // output columns per workgroup
+  const int64_t nrows = std::max<int64_t>(cols, (MAX_BUF / ldw) / cols * cols);
+  for (int64_t n0 = 0; n0 < N; n0 += nrows) {
+    const int64_t nc = std::min(nrows, N - n0);
+    dim3 grid((unsigned)cdiv(nc, cols), 1, 1);
+    const EpiArgs en = shift_epi(e, out_bytes<EPI>(), 0, n0);
+    const int8_t* wn = w + n0 * ldw;
+    float* s = n0 == 0 ? sx : nullptr;
+#define XDNA_ROWQ(C_, D_, JM_) \
+  mm_rowq_kernel<DT, C_, D_, JM_, EPI><<<grid, 512, lds, st>>>(x, kx, wn, ldw, nc, K, s, en)
+    if (c4) {
+      if (jm <= 1) XDNA_ROWQ(4, 3, 1);
+      else if (jm <= 2) XDNA_ROWQ(4, 3, 2);
+      else XDNA_ROWQ(4, 3, 4);
+    } else {
+      if (jm <= 1) XDNA_ROWQ(1, 2, 1);
+      else if (jm <= 2) XDNA_ROWQ(1, 2, 2);
+      else XDNA_ROWQ(1, 2, 4);
+    }
+#undef XDNA_ROWQ
+    const int rc = launch_status("mm_rowq");
+    if (rc) return rc;
+  }
+  return XDNA_OK;
+}
+
+template <int EPI>
+int launch_rowq_dt(const void* x, int x_dtype, int64_t kx, const int8_t* w, int64_t ldw, int64_t N, int64_t K,
+                   float* sx, const EpiArgs& e, hipStream_t st) {
+  if (x_dtype == XDNA_F32) return launch_rowq<XDNA_F32, EPI>(x, kx, w, ldw, N, K, sx, e, st);
+  if (x_dtype == XDNA_BF16) return launch_rowq<XDNA_BF16, EPI>(x, kx, w, ldw, N, K, sx, e, st);
+  return launch_rowq<XDNA_F16, EPI>(x, kx, w, ldw, N, K, sx, e, st);
+}
+
 template <int EPI>
 int launch_conv(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad, const int8_t* wq, int64_t co,
                 const EpiArgs& e, hipStream_t st) {
@@ -1952,6 +2129,29 @@ int xdna_gemm_i8_dequant(const int8_t* a, int64_t lda, const float* sx, const in
                          const float* bias, void* y, int y_dtype, int64_t ldy, int64_t m, int64_t n, int64_t k,
                          void* stream) {
   return xdna_gemm_i8_dequant_ws(a, lda, sx, w, ldw, sw, bias, y, y_dtype, ldy, m, n, k, nullptr, 0, stream);
+}
+
+int xdna_linear_row(const void* x, int x_dtype, int64_t kx, const int8_t* w, int64_t ldw, const float* sw,
+                    const float* bias, void* y, int y_dtype, int64_t n, int64_t k, float* sx, void* stream) {
+  XDNA_REQUIRE(x_dtype == XDNA_F32 || x_dtype == XDNA_BF16 || x_dtype == XDNA_F16, "x_dtype must be F32/BF16/F16");
+  XDNA_REQUIRE(y_dtype == XDNA_F32 || y_dtype == XDNA_BF16 || y_dtype == XDNA_F16, "y_dtype must be F32/BF16/F16");
+  XDNA_REQUIRE(n >= 0 && k >= 0 && kx >= 0, "negative size");
+  if (n == 0) return XDNA_OK;
+  XDNA_REQUIRE(k % 16 == 0 && k >= 16 && k <= XDNA_LINEAR_ROW_KMAX,
+               "k must be a multiple of 16 in [16, XDNA_LINEAR_ROW_KMAX]");
+  const int64_t esz = x_dtype == XDNA_F32 ? 4 : 2;
+  XDNA_REQUIRE(kx >= 1 && kx <= k && (kx * esz) % 16 == 0, "kx must lie in [1, k] with kx elements a multiple of 16 bytes");
+  XDNA_REQUIRE(ldw >= k && ldw % 16 == 0, "bad leading dimension");
+  XDNA_REQUIRE(x && w && sw && y && aligned(x, 16) && aligned(w, 16), "bad pointers");
+  EpiArgs e{};
+  e.out = y;
+  e.ldo = n;
+  e.sw = sw;
+  e.bias = bias;
+  hipStream_t st = as_stream(stream);
+  if (y_dtype == XDNA_F32) return launch_rowq_dt<EPI_DQ_F32>(x, x_dtype, kx, w, ldw, n, k, sx, e, st);
+  if (y_dtype == XDNA_BF16) return launch_rowq_dt<EPI_DQ_BF16>(x, x_dtype, kx, w, ldw, n, k, sx, e, st);
+  return launch_rowq_dt<EPI_DQ_F16>(x, x_dtype, kx, w, ldw, n, k, sx, e, st);
 }
 
 int xdna_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const float* bias, void* y, int y_dtype,

@@ -99,6 +99,7 @@ def _declare(L):
         "xdna_gemm_ksplit": ([i64, i64, i64, p, p], i),
         "xdna_gemm_i8_i32_ws": ([p, i64, p, i64, p, i64, i64, i64, i64, p, i64, p], i),
         "xdna_gemm_i8_dequant_ws": ([p, i64, p, p, i64, p, p, p, i, i64, i64, i64, i64, p, i64, p], i),
+        "xdna_linear_row": ([p, i, i64, p, i64, p, p, p, i, i64, i64, p, p], i),
         "xdna_gemm_bf16": ([p, i64, p, i64, p, p, i, i64, i64, i64, i64, p], i),
         "xdna_gemm_bf16_silu": ([p, i64, p, i64, p, i64, i64, i64, i64, p], i),
         "xdna_pad_rows_i8": ([p, i64, i64, i64, p, i64, i64, p], i),
@@ -129,6 +130,7 @@ def _declare(L):
 
 EXPORTS = ("xdna_abi_version", "xdna_last_error", "xdna_device_info", "xdna_quant_rows", "xdna_gemm_i8_i32",
            "xdna_gemm_i8_dequant", "xdna_gemm_ws_bytes", "xdna_gemm_ksplit", "xdna_gemm_i8_i32_ws", "xdna_gemm_i8_dequant_ws",
+           "xdna_linear_row",
            "xdna_gemm_bf16", "xdna_gemm_bf16_silu", "xdna_pad_rows_i8", "xdna_conv_quant_nhwc",
            "xdna_conv_quant_nhwc_noalloc", "xdna_conv_weight_pack",
            "xdna_conv3x3_i8", "xdna_conv_dequant", "xdna_conv3x3_dequant", "xdna_conv_requant_next", "xdna_nchw_to_nhwc_i8",
@@ -404,6 +406,40 @@ def mm_i8_dequant(a, sx, w, sw, bias, out_dtype):
             _check(lib().xdna_gemm_i8_dequant_ws(_ptr(a), a.stride(0), _ptr(sx), _ptr(w), w.stride(0), _ptr(sw),
                                                  _ptr(bias), _ptr(y), _DTYPE_CODE[out_dtype], y.stride(0), M, N, K,
                                                  ws, wsb, _stream(dev)), "gemm_i8_dequant")
+    return y
+
+
+# XDNA_LINEAR_ROW_KMAX: the longest weight row (bytes) xdna_linear_row takes (its int8 row sits in LDS)
+LINEAR_ROW_KMAX = 32768
+
+
+def linear_row_ok(x2d, k_pad):
+    """Whether xdna_linear_row takes this activation for weights of k_pad columns: one row of
+    float32 / bfloat16 / float16, contiguous and 16-byte aligned, its bytes a multiple of 16, and
+    k_pad <= LINEAR_ROW_KMAX."""
+    R, K = x2d.shape
+    return (R == 1 and x2d.dtype in _DTYPE_CODE and (x2d.stride(1) == 1 or K == 1) and x2d.data_ptr() % 16 == 0
+            and (K * x2d.element_size()) % 16 == 0 and K <= k_pad <= LINEAR_ROW_KMAX and k_pad % 16 == 0)
+
+
+def linear_row(x2d, w, sw, bias, out_dtype, sx=None):
+    """y [1, N] = the W8A8 linear of the one row x2d [1, K] (linear_row_ok) against w [N, Kp] int8, in
+    one launch: the row's quantize (quant_rows' integers and scale) + the GEMM + the dequantize
+    ((acc * s) * sw (+ bias)) as out_dtype, bit for bit quant_rows followed by mm_i8_dequant. sx: an
+    optional float32 [1] tensor that receives the row's scale."""
+    dev = _need_gpu(x2d, w, sw, bias, sx)
+    K = x2d.shape[1]
+    N, Kp = w.shape
+    if not linear_row_ok(x2d, Kp) or w.stride(1) != 1 or w.stride(0) % 16 != 0:
+        raise ValueError(f"linear_row: unsupported operands {x2d.dtype} {tuple(x2d.shape)}, w {tuple(w.shape)}")
+    if sx is not None and (sx.dtype != torch.float32 or sx.numel() < 1):
+        raise ValueError("linear_row: sx must be a float32 tensor of at least one element")
+    y = torch.empty((1, N), dtype=out_dtype, device=dev)
+    if N:
+        with _on(dev):
+            _check(lib().xdna_linear_row(_ptr(x2d), _DTYPE_CODE[x2d.dtype], K, _ptr(w), w.stride(0), _ptr(sw),
+                                         _ptr(bias), _ptr(y), _DTYPE_CODE[out_dtype], N, Kp, _ptr(sx),
+                                         _stream(dev)), "linear_row")
     return y
 
 

@@ -278,15 +278,21 @@ def _check(cfg, key, got, want, exact=True):
 
 
 def _gpu_linear(cfg, x2d, qw, bias, dtype):
-    """y [R, N] = W8A8(x2d) on the GPU: quantize kernel, then the GEMM with the fused dequantize."""
+    """y [R, N] = W8A8(x2d) on the GPU: quantize kernel, then the GEMM with the fused dequantize; a single
+    row (decode) whose layout allows it as one launch that quantizes the row itself (xdna_linear_row)."""
     dev = kernels.gpu_device(x2d)
     xg = x2d.to(dev)
     wq, sw = qw.gpu(dev)
-    xq, sx = kernels.quant_rows(xg, qw.Kp)
     b = None if bias is None else bias.to(dev, torch.float32).contiguous()
-    y = kernels.mm_i8_dequant(xq, sx, wq, sw, b, dtype)
+    if kernels.linear_row_ok(xg, qw.Kp):
+        y = kernels.linear_row(xg, wq, sw, b, dtype)
+        key = ("row", "rowq", _bucket(1, cfg.row_buckets), qw.N, qw.K, str(dtype))
+    else:
+        xq, sx = kernels.quant_rows(xg, qw.Kp)
+        y = kernels.mm_i8_dequant(xq, sx, wq, sw, b, dtype)
+        key = _program(cfg, "dq", dev, x2d.shape[0], qw, dtype)
     stats.launches += 1
-    _check(cfg, _program(cfg, "dq", dev, x2d.shape[0], qw, dtype), y, lambda: _cpu_linear(x2d, qw, bias, dtype))
+    _check(cfg, key, y, lambda: _cpu_linear(x2d, qw, bias, dtype))
     return y
 
 
