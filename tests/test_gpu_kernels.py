@@ -346,6 +346,33 @@ def _conv_case(n, ci, co, h, w, seed):
     return x, wt
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("n,ch,h,w,c_pad", [(8, 3, 224, 224, 16),    # an RGB batch (VGG-16's input)
+                                            (2, 3, 13, 36, 16), (1, 3, 20, 24, 32), (2, 1, 5, 8, 16),
+                                            (1, 5, 33, 40, 16),      # a partly filled last block
+                                            (3, 17, 9, 16, 32), (2, 40, 8, 8, 48), (1, 64, 56, 56, 64),
+                                            (2, 80, 8, 16, 96), (1, 256, 8, 64, 256), (2, 7, 5, 7, 16)])
+def test_conv_quant(gpu, dtype, n, ch, h, w, c_pad):
+    """Per-image quantize + NCHW -> NHWC of float / bf16 / fp16 images against the oracle, bit for bit:
+    narrow images (c_pad <= 64, the pixel-major kernel), wide ones (the 256-channel tile), pixel counts
+    that are not whole 16-byte loads (the scalar kernel), padding channels past ch zero, and an all-zero
+    image beside ones with a single large value."""
+    from torch_xdna import kernels
+
+    x = _rand((n, ch, h, w), torch.float32, seed=n * 1000 + ch * 10 + h + w, scale=3.0)
+    if n > 1:
+        x[0] = 0.0
+    x.view(n, -1)[-1, (ch * h * w) // 2] = -40.0
+    x = x.to(DT[dtype])
+    xq, sx = kernels.conv_quant(x.to(gpu), c_pad)
+    xq_r, sx_r = O.conv_quant_images(x.float().numpy())
+    got = _np(xq)
+    assert got.shape == (n, h, w, c_pad)
+    assert np.array_equal(got[..., :ch].transpose(0, 3, 1, 2), xq_r), f"{(got[..., :ch].transpose(0, 3, 1, 2) != xq_r).sum()} differ"
+    assert not got[..., ch:].any()
+    assert np.array_equal(_np(sx), sx_r)
+
+
 @pytest.mark.parametrize("n,ci,co,h,w", [(2, 3, 48, 13, 37), (1, 64, 128, 16, 64), (2, 16, 20, 5, 7),
                                          (1, 256, 256, 8, 64), (3, 40, 64, 9, 9),
                                          (1, 32, 256, 64, 256),      # larger tiles (every tile shape:

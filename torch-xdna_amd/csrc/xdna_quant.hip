@@ -570,6 +570,55 @@ __global__ __launch_bounds__(256) void conv_quant_nhwc_vec_kernel(const void* __
   }
 }
 
+// Quantize + NCHW -> NHWC for narrow images (c_pad <= 48: RGB inputs, early layers), pixel-major with no
+// channel tile: lane i of the block owns PPL consecutive pixels, and per group of 16 channels it reads
+// each real channel's PPL pixels with one 16-byte load (channels past ch are not read: they quantize to
+// 0), quantizes each pixel's 16 channels and writes them as one 16-byte store. Lanes read consecutive 16
+// bytes of a channel and write consecutive pixels. Grid (cdiv(hw, 256 PPL), nb); needs hw % PPL == 0 and
+// an image below 2 GB.
+template <int DT, bool NT>
+__global__ __launch_bounds__(256) void conv_quant_nhwc_narrow_kernel(const void* __restrict__ x, int64_t ch,
+                                                                     int64_t hw, const float* __restrict__ parts,
+                                                                     int nparts, int8_t* __restrict__ q,
+                                                                     int64_t c_pad, float* __restrict__ sx) {
+  constexpr int ESZ = (DT == XDNA_F32) ? 4 : 2;
+  constexpr int PPL = 16 / ESZ;
+  __shared__ float red[4];
+  using V = Vec16<DT>;
+  const int64_t b = blockIdx.y;
+  const int64_t p = ((int64_t)blockIdx.x * 256 + threadIdx.x) * PPL;     // the lane's first pixel
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(reinterpret_cast<const char*>(x) + b * ch * hw * ESZ,
+                                             (uint32_t)(ch * hw * ESZ));
+  const int groups = (int)(c_pad / 16);
+  // the first group's loads go out before the image's scale is reduced
+  V v[16];
+  int nc = (int)min<int64_t>(16, ch);
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    v[i].raw = i < nc ? buf_load_u4<NT>(r, (uint32_t)((i * hw + p) * ESZ)) : make_uint4(0, 0, 0, 0);
+  const float sc = scale_from_amax(image_amax(parts, b, nparts, red));
+  const float rc = 1.0f / sc;
+  if (blockIdx.x == 0 && threadIdx.x == 0) sx[b] = sc;
+  int8_t* qp = q + (b * hw + p) * c_pad;
+  for (int g = 0; g < groups; ++g) {
+    if (g > 0) {
+      nc = (int)max<int64_t>(0, min<int64_t>(16, ch - 16 * g));
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        v[i].raw = i < nc ? buf_load_u4<NT>(r, (uint32_t)(((16 * g + i) * hw + p) * ESZ)) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+      float f[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) f[i] = v[i].get(j);
+      uint32_t w[4];
+      quant_pack<16>(f, sc, rc, w);
+      if (p < hw) *reinterpret_cast<uint4*>(qp + j * c_pad + 16 * g) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+}
+
 // Quantize + NCHW -> NHWC: tile of 64 channels x 64 pixels per block (256 threads). Wave w
 // reads channels [w*16, w*16+16) of the tile, lane = pixel, so every global read is 64
 // consecutive pixels of one channel; four channels pack into one LDS word per pixel. The
@@ -1075,10 +1124,16 @@ int xdna_conv_quant_nhwc(const void* x, int x_dtype, int64_t nb, int64_t ch, int
   // the 16-byte path: pixel rows in whole 16-byte loads, an image's bytes addressable by one buffer resource
   const bool vec = hw % (16 / esz) == 0 && aligned(x, 16) && per * esz < (int64_t(1) << 31);
   const dim3 gv((unsigned)cdiv(hw, 16 * (16 / esz)), (unsigned)cdiv(c_pad, 256), (unsigned)nb);
+  // narrow images: the pixel-major kernel reads only the real channels (a 256-channel tile spends most of its
+  // loads past ch: 8x3x448x448 float32 took 114 us, 20 us this way); at c_pad 64 the tile is faster again
+  const bool narrow = vec && c_pad <= 48;
+  const dim3 gn((unsigned)cdiv(hw, 256 * (16 / esz)), (unsigned)nb, 1);
 #define XDNA_CQ(DT)                                                                                        \
   if (nt) image_absmax_kernel<DT, true><<<g1, 1024, 0, st>>>(x, per, amax_ws);                              \
   else image_absmax_kernel<DT, false><<<g1, 1024, 0, st>>>(x, per, amax_ws);                                \
-  if (vec && nt) conv_quant_nhwc_vec_kernel<DT, true><<<gv, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx); \
+  if (narrow && nt) conv_quant_nhwc_narrow_kernel<DT, true><<<gn, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx); \
+  else if (narrow) conv_quant_nhwc_narrow_kernel<DT, false><<<gn, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx); \
+  else if (vec && nt) conv_quant_nhwc_vec_kernel<DT, true><<<gv, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx); \
   else if (vec) conv_quant_nhwc_vec_kernel<DT, false><<<gv, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx); \
   else conv_quant_nhwc_kernel<DT><<<g2, 256, 0, st>>>(x, ch, hw, amax_ws, parts, q, c_pad, sx);
   switch (x_dtype) {
