@@ -440,24 +440,50 @@ def test_conv3x3_dequant_fused(gpu, dtype, n, ci, co, h, w):
 @pytest.mark.parametrize("relu", [False, True])
 @pytest.mark.parametrize("pool", [False, True])
 @pytest.mark.parametrize("x_dtype", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("n,co,h,w,c_pad", [(2, 64, 14, 10, 64), (1, 20, 9, 7, 32), (3, 48, 6, 6, 48)])
+@pytest.mark.parametrize("n,co,h,w,c_pad", [(2, 64, 14, 10, 64), (1, 20, 9, 7, 32), (3, 48, 6, 6, 48),
+                                             # whole 16-channel groups, a power-of-two group count (the wide
+                                             # kernels): odd sizes, empty padding groups, partial tiles, one
+                                             # image larger than 256 tiles (the max pass loops)
+                                             (2, 16, 9, 9, 16), (1, 32, 15, 9, 64), (2, 128, 12, 10, 128),
+                                             (1, 512, 6, 6, 512), (2, 256, 40, 38, 256), (1, 16, 520, 520, 16)])
 def test_conv_requant_next(gpu, relu, pool, x_dtype, n, co, h, w, c_pad):
     """Conv chaining: the previous conv's NHWC q -> the next conv's NHWC int8 input and per-image scale,
-    equal to dequantize -> cast -> [2x2 max-pool] -> per-image quantize through the oracle (bit for
-    bit, padding channels zero)."""
+    equal to dequantize -> cast -> [ReLU] -> [2x2 max-pool] -> per-image quantize through the oracle (bit
+    for bit, padding channels zero)."""
+    _check_requant_next(gpu, relu, pool, x_dtype, n, co, h, w, c_pad,
+                        ((False, False), (True, False), (True, True)))
+
+
+@pytest.mark.parametrize("relu", [False, True])
+@pytest.mark.parametrize("n,co,h,w,c_pad,pool", [(4, 64, 224, 224, 64, False), (3, 16, 1024, 1024, 16, True)])
+def test_conv_requant_next_wide_tiles(gpu, relu, n, co, h, w, c_pad, pool):
+    """The same at sizes with at least two blocks of 1024 items per CU, where the wide kernels give each
+    lane four items (the smaller cases above take one), with bias and the ReLU after it."""
+    _check_requant_next(gpu, relu, pool, "f32", n, co, h, w, c_pad, ((True, True),))
+
+
+def _check_requant_next(gpu, relu, pool, x_dtype, n, co, h, w, c_pad, variants):
+    """variants: (with bias, relu_y) pairs; q in a narrow range with one spike per image (positive or
+    negative) at a seeded place, so each image's scale comes from one item."""
     from torch_xdna import kernels
 
     g = torch.Generator().manual_seed(n * 100 + co + h)
-    q = (torch.randint(0, 256, (n, h, w, co), generator=g, dtype=torch.uint8) if relu
-         else torch.randint(-128, 128, (n, h, w, co), generator=g, dtype=torch.int8))
+    q = (torch.randint(0, 40, (n, h, w, co), generator=g, dtype=torch.uint8) if relu
+         else torch.randint(-40, 40, (n, h, w, co), generator=g, dtype=torch.int8))
+    for i in range(n):
+        yi, xi, ci = (int(torch.randint(0, d, (1,), generator=g)) for d in (h, w, co))
+        q[i, yi, xi, ci] = 250 if relu else (-127 if i % 2 else 126)
     scale = torch.rand(co, generator=g) * 1e-3 + 1e-5
     sx = torch.rand(n, generator=g) + 0.1
     bias = torch.randn(co, generator=g) * 0.1
-    for b in (None, bias):
+    for with_bias, relu_y in variants:
+        b = bias if with_bias else None
         xq, sxn = kernels.conv_requant_next(q.to(gpu), relu, pool, scale.to(gpu), sx.to(gpu),
-                                            None if b is None else b.to(gpu), DT[x_dtype], c_pad)
+                                            None if b is None else b.to(gpu), DT[x_dtype], c_pad, relu_y=relu_y)
         y = O.to_dtype(O.conv_dequant(_np(q).transpose(0, 3, 1, 2), scale.numpy(), sx.numpy(),
                                       None if b is None else b.numpy()), x_dtype)
+        if relu_y:
+            y = np.maximum(y, 0)
         if pool:
             y = O.max_pool2(y)
         xq_r, sx_r = O.conv_quant_images(y)

@@ -892,6 +892,119 @@ __device__ __forceinline__ float chain_value(int q, float f, float bias, bool ha
   return t;
 }
 
+// Chaining for channels in whole 16-byte groups whose group count divides 64 (co % 16 == 0, c_pad_next / 16
+// a power of two <= 64: every VGG-16 and C3 boundary). A block covers U * 256 consecutive items (pixel,
+// channel group) of one image, wave w the U * 64 from w * U * 64, and lane l item k * 64 + l of its wave's
+// range: every load and store instruction covers 64 consecutive items, and a lane keeps one channel group
+// (l % ng), so its factors are read once and its extremes are per channel. A lane's U items are all loaded
+// before any is used. Loads are buffer loads over the image's bytes.
+
+// The source bytes of item pixel pix, channels c0 .. c0+15: the pixel's (1) or its 2x2 window's (4) 16 bytes.
+template <bool POOL>
+__device__ __forceinline__ void chain_load(__amdgpu_buffer_rsrc_t r, const ChainArgs& a, uint32_t pix, uint32_t c0,
+                                           uint4 (&raw)[POOL ? 4 : 1]) {
+  if constexpr (POOL) {
+    const uint32_t y = pix / a.wo, x = pix - y * a.wo;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      raw[d] = buf_load_u4(r, ((2 * y + (d >> 1)) * a.w + 2 * x + (d & 1)) * a.co + c0);
+  } else {
+    raw[0] = buf_load_u4(r, pix * a.co + c0);
+  }
+}
+
+// The (window max of the) 16 integers in raw: uint8 with RELU, else int8.
+template <bool RELU, bool POOL>
+__device__ __forceinline__ void chain_decode(const uint4 (&raw)[POOL ? 4 : 1], int (&qv)[16]) {
+#pragma unroll
+  for (int d = 0; d < (POOL ? 4 : 1); ++d) {
+    const uint32_t words[4] = {raw[d].x, raw[d].y, raw[d].z, raw[d].w};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t byte = (words[e >> 2] >> (8 * (e & 3))) & 0xffu;
+      const int v = RELU ? (int)byte : (int)(int8_t)byte;
+      qv[e] = d == 0 ? v : max(qv[e], v);
+    }
+  }
+}
+
+template <int DT, bool RELU, bool POOL, int PASS, int U>
+__global__ __launch_bounds__(256) void conv_chain_wide_kernel(ChainArgs a, const float* __restrict__ sx,
+                                                              float* __restrict__ parts, int nparts,
+                                                              int8_t* __restrict__ xq, float* __restrict__ sx_next) {
+  constexpr int ND = POOL ? 4 : 1;
+  __shared__ float red[4];
+  const int64_t b = blockIdx.y;
+  const uint32_t items = a.ho * a.wo * a.ng;
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t sh = (uint32_t)__builtin_ctz(a.ng);              // ng is a power of two
+  const uint32_t c0 = (lane & (a.ng - 1)) * 16;
+  const float sxb = sx[b];
+  const bool has_bias = a.bias != nullptr;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(a.q + (uint64_t)b * a.h * a.w * a.co, a.h * a.w * a.co);
+  const uint32_t span = 256u * U;
+  float f[16], bv[16];
+  if constexpr (PASS == 0) {
+    // per-channel integer extremes over the lane's items; an item past the end is replaced by item `lane`
+    // (the same channel group), which exists whenever lane < items
+    int hi[16], lo[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) { hi[e] = -1024; lo[e] = 1024; }
+    for (uint32_t t0 = blockIdx.x * span; t0 < items; t0 += gridDim.x * span) {
+      uint4 raw[U][ND];
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        uint32_t it = t0 + wave * 64u * U + 64u * k + lane;
+        if (it >= items) it = lane;
+        chain_load<POOL>(r, a, it >> sh, c0, raw[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        int qv[16];
+        chain_decode<RELU, POOL>(raw[k], qv);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) { hi[e] = max(hi[e], qv[e]); lo[e] = min(lo[e], qv[e]); }
+      }
+    }
+    float m = 0.0f;
+    if (lane < items && blockIdx.x * span < items) {
+      chain_factors(a, c0, sxb, f, bv);
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (c0 + e < a.co)
+          m = fmaxf(m, fmaxf(fabsf(chain_value<DT>(hi[e], f[e], bv[e], has_bias, a.relu_y)),
+                             fabsf(chain_value<DT>(lo[e], f[e], bv[e], has_bias, a.relu_y))));
+    }
+    m = group_max<256>(m, red);
+    if (threadIdx.x == 0) parts[b * AMAX_PARTS + blockIdx.x] = m;
+  } else {
+    // items past the end are loaded (in bounds or zeros) but never stored; the loads go out before the
+    // image's scale is reduced
+    const uint32_t t0 = blockIdx.x * span + wave * 64u * U + lane;
+    uint4 raw[U][ND];
+#pragma unroll
+    for (int k = 0; k < U; ++k) chain_load<POOL>(r, a, (t0 + 64u * k) >> sh, c0, raw[k]);
+    const float sc = scale_from_amax(image_amax(parts, b, nparts, red));
+    const float rc = 1.0f / sc;
+    if (blockIdx.x == 0 && threadIdx.x == 0) sx_next[b] = sc;
+    chain_factors(a, c0, sxb, f, bv);
+    int8_t* out = xq + (uint64_t)b * items * 16;
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      int qv[16];
+      chain_decode<RELU, POOL>(raw[k], qv);
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        v[e] = c0 + e < a.co ? chain_value<DT>(qv[e], f[e], bv[e], has_bias, a.relu_y) : 0.0f;
+      uint32_t wds[4];
+      quant_pack<16>(v, sc, rc, wds);
+      const uint32_t it = t0 + 64u * k;
+      if (it < items) *reinterpret_cast<uint4*>(out + (uint64_t)it * 16) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+    }
+  }
+}
+
 template <int DT, bool RELU, bool POOL, int PASS>
 __global__ __launch_bounds__(256) void conv_chain_kernel(ChainArgs a, const float* __restrict__ sx,
                                                          float* __restrict__ parts, int nparts,
@@ -1214,14 +1327,28 @@ int xdna_conv_requant_next(const void* q, int relu, int relu_y, int pool, int64_
   const int64_t items = ho * wo * (c_pad_next / 16);
   XDNA_REQUIRE(h * w * co < (1ll << 31) && items * 16 < (1ll << 31), "image too large");
   hipStream_t st = as_stream(stream);
-  const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(items, 256), AMAX_PARTS));
-  dim3 g0((unsigned)parts, (unsigned)nb), g1((unsigned)cdiv(items, 256), (unsigned)nb);
+  // whole 16-byte channel groups, a power-of-two group count <= 64: the wide kernels, 4 items a lane where
+  // that still gives two blocks per CU, else 1 (small boundaries are latency-bound: more blocks)
+  const int64_t ng = c_pad_next / 16;
+  const bool wide = co % 16 == 0 && ng <= 64 && (ng & (ng - 1)) == 0;
+  const int u = wide && cdiv(items, 1024) * nb >= 2 * device_cus() ? 4 : 1;
+  const int64_t per_block = 256 * u;
+  const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(items, per_block), AMAX_PARTS));
+  dim3 g0((unsigned)parts, (unsigned)nb), g1((unsigned)cdiv(items, per_block), (unsigned)nb);
   ChainArgs ca{static_cast<const uint8_t*>(q), (uint32_t)h, (uint32_t)w, (uint32_t)co, (uint32_t)ho, (uint32_t)wo,
-               (uint32_t)(c_pad_next / 16), scale, bias, relu_y ? 1 : 0,
+               (uint32_t)ng, scale, bias, relu_y ? 1 : 0,
                (aligned(scale, 16) && (!bias || aligned(bias, 16))) ? 1 : 0};
 #define XDNA_CH(DT, R, P)                                                                                 \
-  conv_chain_kernel<DT, R, P, 0><<<g0, 256, 0, st>>>(ca, sx, amax_ws, parts, xq_next, sx_next);          \
-  conv_chain_kernel<DT, R, P, 1><<<g1, 256, 0, st>>>(ca, sx, amax_ws, parts, xq_next, sx_next);
+  if (wide && u == 4) {                                                                                   \
+    conv_chain_wide_kernel<DT, R, P, 0, 4><<<g0, 256, 0, st>>>(ca, sx, amax_ws, parts, xq_next, sx_next); \
+    conv_chain_wide_kernel<DT, R, P, 1, 4><<<g1, 256, 0, st>>>(ca, sx, amax_ws, parts, xq_next, sx_next); \
+  } else if (wide) {                                                                                      \
+    conv_chain_wide_kernel<DT, R, P, 0, 1><<<g0, 256, 0, st>>>(ca, sx, amax_ws, parts, xq_next, sx_next); \
+    conv_chain_wide_kernel<DT, R, P, 1, 1><<<g1, 256, 0, st>>>(ca, sx, amax_ws, parts, xq_next, sx_next); \
+  } else {                                                                                                \
+    conv_chain_kernel<DT, R, P, 0><<<g0, 256, 0, st>>>(ca, sx, amax_ws, parts, xq_next, sx_next);        \
+    conv_chain_kernel<DT, R, P, 1><<<g1, 256, 0, st>>>(ca, sx, amax_ws, parts, xq_next, sx_next);        \
+  }
 #define XDNA_CH_RP(DT)                 \
   if (relu && pool) { XDNA_CH(DT, true, true) }        \
   else if (relu) { XDNA_CH(DT, true, false) }          \
