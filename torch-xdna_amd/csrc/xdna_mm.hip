@@ -2039,6 +2039,135 @@ int launch_rowq_dt(const void* x, int x_dtype, int64_t kx, const int8_t* w, int6
   return launch_rowq<XDNA_F16, EPI>(x, kx, w, ldw, N, K, sx, e, st);
 }
 
+// Conv of 16-channel inputs (c_pad == 16: RGB or gray images padded to 16 channels, narrow early layers).
+// With 16-byte pixels a 32-deep K step of the MFMA is exactly two taps x 16 channels: lanes 0-31 carry
+// K chunk 2 s (tap 2 s) and lanes 32-63 chunk 2 s + 1, so a lane's activation operand is one 16-byte load
+// of its pixel's tap-shifted neighbour (a zero load outside the image: the padding) and its weight operand
+// 16 contiguous bytes of wq. No LDS stages and no barriers: K = 9 taps in 5 steps (chunk 9 is zero). Each
+// wave holds the weight fragments of all NB = co / 32 column blocks (loaded once) and takes runs of BPW
+// consecutive 32-pixel blocks, a grid stride of runs apart, every activation load of a run issued before
+// its first MFMA and the next run's loads issued before this run's MFMAs (one run per wave measured best:
+// VGG-16's 8x3x224x224 -> 64 in 14.0 us, 16.3 us with runs of four, 30 us on the tile engine). Lane l
+// holds pixel l % 32 and channels 32 j + 8 g + 4 (l / 32) + t (t < 4) of column
+// block j; the requantized bytes go through a wave-private LDS tile [32 pixels][co] (pitch co + 16: the
+// 4-byte writes of 32 pixels fall on 16 bank groups) and leave as 16-byte stores, consecutive lanes
+// covering consecutive 16-byte pieces of the block's 32 * co contiguous output bytes (4-byte stores
+// straight from the accumulators split every instruction into partial lines of 16 pixel rows).
+// EPI_REQUANT (int8 / uint8 NHWC rows of co bytes) or EPI_CALIB.
+template <int EPI, int NB, int BPW>
+__global__ __launch_bounds__(256) void conv16_kernel(const int8_t* __restrict__ x, uint32_t M, uint32_t h,
+                                                     uint32_t w, const int8_t* __restrict__ wq, EpiArgs e) {
+  static_assert(EPI == EPI_REQUANT || EPI == EPI_CALIB, "requantize or calibrate");
+  constexpr int PITCH = NB * 32 + 16, CPP = NB * 2;       // tile pitch; 16-byte pieces per pixel
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[EPI == EPI_REQUANT ? 4 : 1][EPI == EPI_REQUANT ? 32 * PITCH : 16];
+  const int lane = threadIdx.x & 63;
+  const int hl = lane >> 5, r32 = lane & 31;
+  const uint32_t nwaves = gridDim.x * 4;
+  const uint32_t nrun = (M + 32 * BPW - 1) / (32 * BPW);
+  const uint32_t hw = h * w;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(wq, NB * 32 * 9 * 16);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, M * 16);
+  uint8_t* const tile = tiles[EPI == EPI_REQUANT ? (threadIdx.x >> 6) : 0];
+  i32x4 wf[5][NB];
+#pragma unroll
+  for (int s = 0; s < 5; ++s) {
+    const int tap = 2 * s + hl;
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      wf[s][j] = __builtin_bit_cast(i32x4, buf_load_u4(rw, tap < 9 ? (uint32_t)(((32 * j + r32) * 9 + tap) * 16) : OOB));
+  }
+  const int qlo = e.relu ? 0 : -128, qhi = e.relu ? 255 : 127;
+  int calib = 0;
+  // the 5 activation chunks of each block's pixel for this lane (zeros past M, outside the image, tap 9)
+  auto load_run = [&](uint32_t run, i32x4 (&a)[BPW][5]) {
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) {
+      const uint32_t m = (run * BPW + b) * 32 + r32;
+      const uint32_t img = m / hw, p = m - img * hw, y = p / w, xx = p - y * w;
+#pragma unroll
+      for (int s = 0; s < 5; ++s) {
+        const int tap = 2 * s + hl;
+        const uint32_t yy = y + (uint32_t)(tap / 3) - 1u, xs = xx + (uint32_t)(tap % 3) - 1u;
+        const bool ok = m < M && tap < 9 && yy < h && xs < w;
+        a[b][s] = __builtin_bit_cast(i32x4, buf_load_u4(rx, ok ? (img * hw + yy * w + xs) * 16u : OOB));
+      }
+    }
+  };
+  uint32_t run = (blockIdx.x * 256 + threadIdx.x) >> 6;
+  i32x4 a[BPW][5];
+  load_run(run, a);
+  for (; run < nrun; run += nwaves) {
+    i32x4 an[BPW][5];
+    load_run(run + nwaves, an);
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) {
+      i32x16 acc[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) acc[j] = i32x16{};
+#pragma unroll
+      for (int s = 0; s < 5; ++s)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[j] = mfma32x32x32(wf[s][j], a[b][s], acc[j]);
+      const uint32_t m0 = (run * BPW + b) * 32;
+      if constexpr (EPI == EPI_CALIB) {
+        if (m0 + r32 < M) {
+#pragma unroll
+          for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) calib = max(calib, e.relu ? max(acc[j][r], 0) : abs(acc[j][r]));
+        }
+      } else {
+        const int rnd = 1 << (e.shift - 1);
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            uint32_t packed = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const int q = min(max((acc[j][4 * g + t] + rnd) >> e.shift, qlo), qhi);   // round half up
+              packed |= ((uint32_t)(q & 0xff)) << (8 * t);
+            }
+            *reinterpret_cast<uint32_t*>(tile + r32 * PITCH + 32 * j + 8 * g + 4 * hl) = packed;
+          }
+        uint8_t* const out = reinterpret_cast<uint8_t*>(e.out) + (int64_t)m0 * e.ldo;
+#pragma unroll
+        for (int k = 0; k < CPP / 2; ++k) {
+          const int idx = 64 * k + lane, px = idx / CPP, pc = idx - px * CPP;
+          const uint4 v = *reinterpret_cast<const uint4*>(tile + px * PITCH + pc * 16);
+          if (m0 + px < M) *reinterpret_cast<uint4*>(out + (int64_t)px * e.ldo + pc * 16) = v;
+        }
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < BPW; ++b)
+#pragma unroll
+      for (int s = 0; s < 5; ++s) a[b][s] = an[b][s];
+  }
+  calib_flush<EPI>(e, calib);
+}
+
+// The 16-channel conv's launch, or XDNA_EUNSUPPORTED when the shape is not one it takes (co a multiple
+// of 32 up to 128, no fused dequantize, the launch's bytes addressable in 32 bits).
+template <int EPI>
+int launch_conv16(const int8_t* x, int64_t m, int64_t h, int64_t w, const int8_t* wq, int64_t co, const EpiArgs& e,
+                  hipStream_t st) {
+  if (co % 32 != 0 || co > 128 || m * 16 >= (int64_t(1) << 31) || m * co >= (int64_t(1) << 31)) return XDNA_EUNSUPPORTED;
+  if constexpr (EPI == EPI_REQUANT) {
+    if (e.dq_out) return XDNA_EUNSUPPORTED;
+  }
+  constexpr int BPW = 1;                  // blocks of 32 pixels per run of a wave
+  const int64_t waves = std::min<int64_t>(cdiv(m, 32 * BPW), (int64_t)device_cus() * 12);
+  const dim3 grid((unsigned)cdiv(waves, 4));
+  switch (co / 32) {
+    case 1: conv16_kernel<EPI, 1, BPW><<<grid, 256, 0, st>>>(x, (uint32_t)m, (uint32_t)h, (uint32_t)w, wq, e); break;
+    case 2: conv16_kernel<EPI, 2, BPW><<<grid, 256, 0, st>>>(x, (uint32_t)m, (uint32_t)h, (uint32_t)w, wq, e); break;
+    case 3: conv16_kernel<EPI, 3, BPW><<<grid, 256, 0, st>>>(x, (uint32_t)m, (uint32_t)h, (uint32_t)w, wq, e); break;
+    default: conv16_kernel<EPI, 4, BPW><<<grid, 256, 0, st>>>(x, (uint32_t)m, (uint32_t)h, (uint32_t)w, wq, e);
+  }
+  return launch_status("conv3x3 (16 channels)");
+}
+
 template <int EPI>
 int launch_conv(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad, const int8_t* wq, int64_t co,
                 const EpiArgs& e, hipStream_t st) {
@@ -2057,6 +2186,16 @@ int launch_conv(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad
     if (e.dq_out) eb.px0 = e.px0 + b0 * h * w;   // NCHW output: addressed by global pixel, not by row
     else eb = shift_epi(e, 1, b0 * h * w, 0);
     const int8_t* xb = x + b0 * per_img;
+    // 16-channel inputs: the register-only kernel where it takes the shape
+    if constexpr (EPI == EPI_REQUANT || EPI == EPI_CALIB) {
+      if (c_pad == 16) {
+        const int rc = launch_conv16<EPI>(xb, bc * h * w, h, w, wq, co, eb, st);
+        if (rc != XDNA_EUNSUPPORTED) {
+          if (rc) return rc;
+          continue;
+        }
+      }
+    }
     // the haloed input tile where the tile allows it; the running tap counters of CONVM 1 step by KG
     // slices of 64 channels
     const int mode = conv_mode(tile, h, w, c_pad);
