@@ -513,8 +513,9 @@ def test_conv_layouts(gpu):
 # ------------------------------------------------------------------------------ HIP graph capture
 def test_graph_replay(gpu):
     """The launchers captured into one HIP graph (activation quantize, fused GEMM, conv quantize, conv,
-    conv dequantize): three replays, with new inputs copied in and eager work plus synchronization
-    between them, each bit-identical to the eager result on the same inputs."""
+    conv dequantize; and an RGB chain: narrow-image quantize, 16-channel conv, wide-kernel requantize,
+    conv): three replays, with new inputs copied in and eager work plus synchronization between them,
+    each bit-identical to the eager result on the same inputs."""
     from torch_xdna import kernels
 
     x = _rand((300, 1024), torch.bfloat16, seed=51).to(gpu)
@@ -522,13 +523,21 @@ def test_graph_replay(gpu):
     xc = _rand((2, 64, 20, 24), torch.float32, seed=53).to(gpu)
     cwq, csw = kernels.conv_weight_pack(_rand((64, 64, 3, 3), torch.float32, seed=54, scale=0.05).to(gpu), 64)
     scale = csw * 2.0 ** 9
+    xr = _rand((2, 3, 30, 34), torch.float32, seed=55).to(gpu)
+    rwq, rsw = kernels.conv_weight_pack(_rand((64, 3, 3, 3), torch.float32, seed=56, scale=0.2).to(gpu), 16)
+    rbias = _rand((64,), torch.float32, seed=57, scale=0.1).to(gpu)
 
     def path():
         xq, sx = kernels.quant_rows(x)
         y = kernels.mm_i8_dequant(xq, sx, wq, sw, None, torch.bfloat16)
         cq, csx = kernels.conv_quant(xc, 64)
-        q = kernels.conv3x3(cq, cwq, 9, True)
-        return y, kernels.conv_dequant(q, True, scale, csx, None, torch.float32)
+        q = kernels.conv3x3(cq, cwq, 9, False)
+        yc = kernels.conv_dequant(q, False, scale, csx, None, torch.float32)
+        rq, rsx = kernels.conv_quant(xr, 16)
+        q1 = kernels.conv3x3(rq, rwq, 7, False)
+        nq, nsx = kernels.conv_requant_next(q1, False, True, rsw * 2.0 ** 7, rsx, rbias, torch.float32, 64,
+                                            relu_y=True)
+        return y, yc, kernels.conv3x3(nq, cwq, 9, True), nsx
 
     path()
     torch.cuda.synchronize()
@@ -538,6 +547,7 @@ def test_graph_replay(gpu):
     for rep in range(3):
         x.copy_(_rand((300, 1024), torch.bfloat16, seed=60 + rep).to(gpu))
         xc.copy_(_rand((2, 64, 20, 24), torch.float32, seed=70 + rep).to(gpu))
+        xr.copy_(_rand((2, 3, 30, 34), torch.float32, seed=80 + rep).to(gpu))
         want = path()                       # eager work between the replays
         torch.cuda.synchronize()
         g.replay()
