@@ -381,7 +381,11 @@ def test_conv_quant(gpu, dtype, n, ch, h, w, c_pad):
                                          # register-only kernel): RGB, gray, 5 and 16 channels, ragged
                                          # sizes, pixel counts off the 32-pixel blocks, several images
                                          (2, 3, 64, 13, 37), (1, 16, 32, 7, 5), (3, 1, 128, 9, 11),
-                                         (2, 5, 96, 31, 17), (1, 3, 64, 224, 224), (4, 16, 128, 1, 3)])
+                                         (2, 5, 96, 31, 17), (1, 3, 64, 224, 224), (4, 16, 128, 1, 3),
+                                         # 32-, 48- and 64-channel inputs with co a multiple of 32 up to 128
+                                         # (the resident-weight kernel): odd chunk counts, ragged sizes
+                                         (2, 64, 64, 13, 37), (1, 40, 128, 9, 11), (3, 32, 96, 7, 5),
+                                         (2, 20, 32, 15, 4), (1, 64, 128, 56, 56), (2, 48, 64, 1, 1)])
 @pytest.mark.parametrize("relu", [False, True])
 def test_conv3x3(gpu, n, ci, co, h, w, relu):
     from torch_xdna import kernels
@@ -421,7 +425,8 @@ def test_conv3x3(gpu, n, ci, co, h, w, relu):
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("n,ci,co,h,w", [(2, 3, 48, 13, 37), (3, 40, 64, 9, 9), (2, 16, 20, 5, 7), (5, 16, 36, 1, 3),
                                          (1, 64, 128, 16, 64), (1, 256, 256, 8, 64), (1, 32, 256, 64, 256),
-                                         (2, 3, 64, 13, 37), (3, 16, 128, 9, 11)])   # the 16-channel kernel's integers
+                                         (2, 3, 64, 13, 37), (3, 16, 128, 9, 11),    # the 16-channel kernel's integers
+                                         (2, 64, 64, 13, 37), (1, 40, 128, 9, 11)])  # the resident-weight kernel's
 def test_conv3x3_dequant_fused(gpu, dtype, n, ci, co, h, w):
     """xdna_conv3x3_dequant against xdna_conv3x3_i8 + xdna_conv_dequant, bit for bit, in every output dtype,
     with and without ReLU and bias: images whose pixel counts are not multiples of 4 (runs of four pixels

@@ -2147,6 +2147,142 @@ __global__ __launch_bounds__(256) void conv16_kernel(const int8_t* __restrict__ 
   calib_flush<EPI>(e, calib);
 }
 
+// Conv of 32-, 48- and 64-channel inputs (c_pad = 16 CP) with the weights resident in LDS and the
+// activations loaded straight into registers. Row k of the implicit GEMM is KC = 9 CP chunks of 16 bytes
+// (chunk c: tap c / CP, channels 16 (c % CP) ..), so as in conv16_kernel a lane's activation operand of K
+// step s is one 16-byte load: chunk 2 s + (l / 32) of its pixel's tap-shifted neighbour. The whole weight
+// [co][KC][16] sits in LDS for the workgroup's life (loaded once by its 8 waves; row pitch KC * 16 + 16, so
+// the 16 rows one 16-lane phase of a fragment read touches fall on distinct bank groups; the pad chunk is
+// zero and serves the odd KC's last step), and only those weight fragments are read from LDS: 16 bytes per
+// lane per MFMA, half of what the tile engine's fragment reads of both operands cost for the same MACs.
+// Each wave walks 32-pixel blocks a grid stride apart, all NS activation loads of a block issued before
+// its first MFMA; epilogue as conv16_kernel (requantize into a wave-private LDS tile, 16-byte stores).
+template <int EPI, int NB, int CP>
+__global__ __launch_bounds__(512) void convd_kernel(const int8_t* __restrict__ x, uint32_t M, uint32_t h,
+                                                    uint32_t w, const int8_t* __restrict__ wq, EpiArgs e) {
+  static_assert(EPI == EPI_REQUANT || EPI == EPI_CALIB, "requantize or calibrate");
+  constexpr int KC = 9 * CP, NS = (KC + 1) / 2;
+  constexpr int WP = KC * 16 + 16;                          // weight row pitch (bytes)
+  constexpr int PITCH = NB * 32 + 16, CPP = NB * 2;          // epilogue tile pitch; 16-byte pieces per pixel
+  constexpr int TILE = EPI == EPI_REQUANT ? 32 * PITCH : 0;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[NB * 32 * WP + 8 * TILE];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, r32 = lane & 31;
+  const uint32_t nwaves = gridDim.x * 8;
+  const uint32_t nblk = (M + 31) / 32;
+  const uint32_t hw = h * w;
+  // the weights, chunk i of the flat [co][KC] array to row i / KC, chunk i % KC; the pad chunks zero
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(wq, NB * 32 * KC * 16);
+  for (int i = threadIdx.x; i < NB * 32 * (KC + 1); i += 512) {
+    const int n = i / (KC + 1), c = i - n * (KC + 1);
+    const uint4 v = buf_load_u4(rw, c < KC ? (uint32_t)((n * KC + c) * 16) : OOB);
+    *reinterpret_cast<uint4*>(lds + n * WP + c * 16) = v;
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, M * CP * 16);
+  uint8_t* const tile = lds + NB * 32 * WP + wave * TILE;
+  const int qlo = e.relu ? 0 : -128, qhi = e.relu ? 255 : 127;
+  int calib = 0;
+  for (uint32_t blk = blockIdx.x * 8 + wave; blk < nblk; blk += nwaves) {
+    const uint32_t m = blk * 32 + r32;
+    const uint32_t img = m / hw, p = m - img * hw, y = p / w, xx = p - y * w;
+    i32x4 a[NS];
+    if constexpr (CP % 2 == 0) {
+      // even CP: step s covers chunks 2 s, 2 s + 1 of one tap (s / (CP / 2)), so each tap's bounds and
+      // offset are worked out once and its CP / 2 loads differ by a constant
+      const uint32_t pix = (img * hw + y * w + xx) * (CP * 16) + 16 * hl;
+#pragma unroll
+      for (int tap = 0; tap < 9; ++tap) {
+        const int dy = tap / 3 - 1, dx = tap % 3 - 1;
+        const bool ok = m < M && y + (uint32_t)dy < h && xx + (uint32_t)dx < w;
+        const uint32_t off = pix + (uint32_t)((dy * (int)w + dx) * CP * 16);
+#pragma unroll
+        for (int uu = 0; uu < CP / 2; ++uu)
+          a[tap * (CP / 2) + uu] = __builtin_bit_cast(i32x4, buf_load_u4(rx, ok ? off + 32u * uu : OOB));
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int c = 2 * s + hl, tap = c / CP, u = c - tap * CP;
+        const uint32_t yy = y + (uint32_t)(tap / 3) - 1u, xs = xx + (uint32_t)(tap % 3) - 1u;
+        const bool ok = m < M && c < KC && yy < h && xs < w;
+        a[s] = __builtin_bit_cast(i32x4, buf_load_u4(rx, ok ? ((img * hw + yy * w + xs) * CP + u) * 16u : OOB));
+      }
+    }
+    i32x16 acc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[j] = i32x16{};
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const i32x4 b = *reinterpret_cast<const i32x4*>(lds + (32 * j + r32) * WP + (2 * s + hl) * 16);
+        acc[j] = mfma32x32x32(b, a[s], acc[j]);
+      }
+    const uint32_t m0 = blk * 32;
+    if constexpr (EPI == EPI_CALIB) {
+      if (m < M) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) calib = max(calib, e.relu ? max(acc[j][r], 0) : abs(acc[j][r]));
+      }
+    } else {
+      const int rnd = 1 << (e.shift - 1);
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          uint32_t packed = 0;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int q = min(max((acc[j][4 * g + t] + rnd) >> e.shift, qlo), qhi);   // round half up
+            packed |= ((uint32_t)(q & 0xff)) << (8 * t);
+          }
+          *reinterpret_cast<uint32_t*>(tile + r32 * PITCH + 32 * j + 8 * g + 4 * hl) = packed;
+        }
+      uint8_t* const out = reinterpret_cast<uint8_t*>(e.out) + (int64_t)m0 * e.ldo;
+#pragma unroll
+      for (int k = 0; k < CPP / 2; ++k) {
+        const int idx = 64 * k + lane, px = idx / CPP, pc = idx - px * CPP;
+        const uint4 v = *reinterpret_cast<const uint4*>(tile + px * PITCH + pc * 16);
+        if (m0 + px < M) *reinterpret_cast<uint4*>(out + (int64_t)px * e.ldo + pc * 16) = v;
+      }
+    }
+  }
+  calib_flush<EPI>(e, calib);
+}
+
+// The direct conv's launch (c_pad 32, 48 or 64), XDNA_EUNSUPPORTED for shapes it does not take.
+template <int EPI>
+int launch_convd(const int8_t* x, int64_t m, int64_t h, int64_t w, int64_t c_pad, const int8_t* wq, int64_t co,
+                 const EpiArgs& e, hipStream_t st) {
+  if (co % 32 != 0 || co > 128 || m * c_pad >= (int64_t(1) << 31) || m * co >= (int64_t(1) << 31)) return XDNA_EUNSUPPORTED;
+  if constexpr (EPI == EPI_REQUANT) {
+    if (e.dq_out) return XDNA_EUNSUPPORTED;
+  }
+  const int64_t wgs = std::min<int64_t>(cdiv(cdiv(m, 32), 8), (int64_t)device_cus() * (co <= 64 ? 2 : 1));
+  const dim3 grid((unsigned)wgs);
+  const uint32_t um = (uint32_t)m, uh = (uint32_t)h, uw = (uint32_t)w;
+#define XDNA_CD(NB_, CP_) convd_kernel<EPI, NB_, CP_><<<grid, 512, 0, st>>>(x, um, uh, uw, wq, e)
+#define XDNA_CD_NB(CP_)                      \
+  switch (co / 32) {                         \
+    case 1: XDNA_CD(1, CP_); break;          \
+    case 2: XDNA_CD(2, CP_); break;          \
+    case 3: XDNA_CD(3, CP_); break;          \
+    default: XDNA_CD(4, CP_);                \
+  }
+  switch (c_pad) {
+    case 32: XDNA_CD_NB(2) break;
+    case 48: XDNA_CD_NB(3) break;
+    case 64: XDNA_CD_NB(4) break;
+    default: return XDNA_EUNSUPPORTED;
+  }
+#undef XDNA_CD_NB
+#undef XDNA_CD
+  return launch_status("conv3x3 (resident weights)");
+}
+
 // The 16-channel conv's launch, or XDNA_EUNSUPPORTED when the shape is not one it takes (co a multiple
 // of 32 up to 128, no fused dequantize, the launch's bytes addressable in 32 bits).
 template <int EPI>
@@ -2190,6 +2326,12 @@ int launch_conv(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad
     if constexpr (EPI == EPI_REQUANT || EPI == EPI_CALIB) {
       if (c_pad == 16) {
         const int rc = launch_conv16<EPI>(xb, bc * h * w, h, w, wq, co, eb, st);
+        if (rc != XDNA_EUNSUPPORTED) {
+          if (rc) return rc;
+          continue;
+        }
+      } else if (c_pad <= 64) {
+        const int rc = launch_convd<EPI>(xb, bc * h * w, h, w, c_pad, wq, co, eb, st);
         if (rc != XDNA_EUNSUPPORTED) {
           if (rc) return rc;
           continue;
