@@ -881,6 +881,34 @@ __device__ __forceinline__ void chain_factors(const ChainArgs& a, uint32_t c0, f
   }
 }
 
+// The raw scale and bias of channels c0 .. c0+15 (0 past co), loaded without the image's factor so the
+// loads can go out before anything they would wait for; chain_scale then forms chain_factors' values.
+__device__ __forceinline__ void chain_factors_raw(const ChainArgs& a, uint32_t c0, float (&sr)[16], float (&bv)[16]) {
+  if (a.vec_f && c0 + 16 <= a.co) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 s4 = reinterpret_cast<const float4*>(a.scale + c0)[k];
+      sr[4 * k] = s4.x; sr[4 * k + 1] = s4.y; sr[4 * k + 2] = s4.z; sr[4 * k + 3] = s4.w;
+      float4 b4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (a.bias) b4 = reinterpret_cast<const float4*>(a.bias + c0)[k];
+      bv[4 * k] = b4.x; bv[4 * k + 1] = b4.y; bv[4 * k + 2] = b4.z; bv[4 * k + 3] = b4.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t o = min(c0 + e, a.co - 1);
+      const bool in = c0 + e < a.co;
+      sr[e] = in ? a.scale[o] : 0.0f;
+      bv[e] = (in && a.bias) ? a.bias[o] : 0.0f;
+    }
+  }
+}
+__device__ __forceinline__ void chain_scale(const ChainArgs& a, uint32_t c0, float sxb, const float (&sr)[16],
+                                            float (&f)[16]) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) f[e] = c0 + e < a.co ? sr[e] * sxb : 0.0f;
+}
+
 // The activation value of integer q: q * f (+ bias), ReLU'd with relu_y, cast to DT (as a float).
 template <int DT>
 __device__ __forceinline__ float chain_value(int q, float f, float bias, bool has_bias, int relu_y) {
@@ -943,7 +971,9 @@ __global__ __launch_bounds__(256) void conv_chain_wide_kernel(ChainArgs a, const
   const bool has_bias = a.bias != nullptr;
   const __amdgpu_buffer_rsrc_t r = make_rsrc(a.q + (uint64_t)b * a.h * a.w * a.co, a.h * a.w * a.co);
   const uint32_t span = 256u * U;
-  float f[16], bv[16];
+  // the channel group's scale and bias go out first: nothing they feed waits on them before the end
+  float sr[16], f[16], bv[16];
+  chain_factors_raw(a, c0, sr, bv);
   if constexpr (PASS == 0) {
     // per-channel integer extremes over the lane's items; an item past the end is replaced by item `lane`
     // (the same channel group), which exists whenever lane < items
@@ -968,7 +998,7 @@ __global__ __launch_bounds__(256) void conv_chain_wide_kernel(ChainArgs a, const
     }
     float m = 0.0f;
     if (lane < items && blockIdx.x * span < items) {
-      chain_factors(a, c0, sxb, f, bv);
+      chain_scale(a, c0, sxb, sr, f);
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         if (c0 + e < a.co)
@@ -987,7 +1017,7 @@ __global__ __launch_bounds__(256) void conv_chain_wide_kernel(ChainArgs a, const
     const float sc = scale_from_amax(image_amax(parts, b, nparts, red));
     const float rc = 1.0f / sc;
     if (blockIdx.x == 0 && threadIdx.x == 0) sx_next[b] = sc;
-    chain_factors(a, c0, sxb, f, bv);
+    chain_scale(a, c0, sxb, sr, f);
     int8_t* out = xq + (uint64_t)b * items * 16;
 #pragma unroll
     for (int k = 0; k < U; ++k) {
