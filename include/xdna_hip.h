@@ -85,6 +85,7 @@ extern "C" {
 #define XDNA_TILE_256x128W8 28
 #define XDNA_TILE_256x256PP 29  /* 256 x 256, 8 waves, ping-pong schedule (two groups of four waves) */
 #define XDNA_TILE_256x64 30     /* 256 x 64, 4 waves stacked along M (narrow outputs with many rows) */
+#define XDNA_TILE_DIRECT 31     /* convs only: register-operand kernels for c_pad 16..64, co a multiple of 32 <= 128 */
 
 /* Library version (XDNA_ABI_VERSION). Replaces the import probe of kernels.available()
  * (torch_xdna/kernels.py:43-56): a loader checks it before trusting the other symbols. */

@@ -43,6 +43,16 @@ def test_library_exports_every_declared_symbol(lib):
     assert sorted(kernels.EXPORTS) == declared()
 
 
+def test_tile_ids_match_header():
+    """kernels.TILES lists the tile names by the header's XDNA_TILE_* ids."""
+    from torch_xdna import kernels
+
+    ids = {int(v): n for n, v in re.findall(r"^#define XDNA_TILE_(\w+) (\d+)", open(HEADER).read(), re.M)}
+    assert sorted(ids) == list(range(len(kernels.TILES)))
+    for i, name in ids.items():
+        assert kernels.TILES[i].replace("_", "").lower().lstrip("t") == name.replace("_", "").lower().lstrip("t"), (i, name)
+
+
 def test_abi_version(lib):
     from torch_xdna import kernels
 

@@ -562,6 +562,35 @@ def test_graph_replay(gpu):
 
 
 # ------------------------------------------------------------------------------ every tile shape
+def test_direct_tile(gpu, tile_table):
+    """The direct conv kernels as the tile "direct": the rule's choice for the shapes they take (c_pad 16 to
+    64, co a multiple of 32 up to 128), a forced engine tile overrides it, a forced "direct" on a shape they
+    do not take runs the rule's engine tile, GEMM kinds reject it; results equal the oracle's throughout."""
+    from torch_xdna import kernels
+
+    assert kernels.tile_get(gpu, "conv", 1000, 64, 9 * 16) == "direct"
+    assert kernels.tile_get(gpu, "conv", 1000, 128, 9 * 64) == "direct"
+    assert kernels.tile_get(gpu, "conv", 1000, 48, 9 * 64) != "direct"        # co not a multiple of 32
+    assert kernels.tile_get(gpu, "conv", 1000, 64, 9 * 128) != "direct"       # c_pad 128
+    assert kernels.tile_plan(gpu, "conv", 1000, 64, 9 * 16) == ("direct", 0, "auto")
+    with pytest.raises(RuntimeError, match="only convs"):
+        kernels.tile_set("i8", 1000, 64, 144, "direct")
+    for n, ci, co, h, w_, tile in [(2, 64, 96, 16, 20, "t64x64"), (2, 3, 64, 13, 37, "t256x64"),
+                                   (1, 48, 40, 13, 37, "direct"), (1, 128, 64, 8, 12, "direct")]:
+        c_pad = -(-ci // 16) * 16
+        kernels.tile_set("conv", n * h * w_, co, 9 * c_pad, tile)
+        want_tile = tile if tile != "direct" else kernels.tile_plan(gpu, "conv", n * h * w_, co, 9 * c_pad)[0]
+        assert want_tile != "direct" or (co % 32 == 0 and co <= 128 and c_pad <= 64)
+        xq = _i8((n, ci, h, w_), seed=ci + h)
+        wq = _i8((co, ci, 3, 3), seed=co + w_)
+        packed = torch.zeros(co, 9, c_pad, dtype=torch.int8)
+        packed[:, :, :ci] = wq.permute(0, 2, 3, 1).reshape(co, 9, ci)
+        q = kernels.conv3x3(kernels.nchw_to_nhwc(xq.to(gpu), c_pad), packed.to(gpu), 9, False)
+        acc = c_oracle.conv3x3_acc(xq.numpy(), wq.numpy())
+        assert np.array_equal(_np(q).transpose(0, 3, 1, 2), O.requant(acc, 9, False)), (n, ci, co, h, w_, tile)
+
+
+
 @pytest.fixture
 def tile_table():
     """The library's tile table, emptied before and after the test."""
@@ -932,7 +961,7 @@ def test_sweep_tool(gpu, tile_table, tmp_path):
     sweep.main(["--kind", "i8", "--rows", "16", "300", "--shapes", "520x256", "--out", out])   # resumed: no-op
     recs = [json.loads(line) for line in open(out)]
     want = len(sweep.candidates("i8", 16)) + len(sweep.candidates("i8", 300)) + \
-        len(sweep.candidates("bf16", 300)) + len(sweep.candidates("conv", 2 * 13 * 37))
+        len(sweep.candidates("bf16", 300)) + len(sweep.candidates("conv", 2 * 13 * 37, 40, 9 * 48))
     assert len(recs) == n_lines == want
     assert all(r["status"] == "ok" and r["exact"] and r["gpu_us"] > 0 for r in recs), recs
     assert {r["checked_against"] for r in recs} == {"cpu"}

@@ -92,6 +92,9 @@ def test_sweep_candidates():
     assert sweep.candidates("i8", 1) == sweep.ENGINE_TILES + sweep.SMALL_TILES + sweep.GEMV_TILES + sweep.SEG4_TILES
     assert sweep.candidates("bf16", 1) == sweep.candidates("i8", 1)
     assert sweep.candidates("i8", 3000) == sweep.ENGINE_TILES
-    assert sweep.candidates("conv", 1) == sweep.ENGINE_TILES
-    assert set(sweep.ENGINE_TILES + sweep.SMALL_TILES + sweep.GEMV_TILES + sweep.SEG4_TILES) == \
+    assert sweep.candidates("conv", 1) == sweep.ENGINE_TILES + ["direct"]
+    assert sweep.candidates("conv", 1000, 64, 9 * 16) == sweep.ENGINE_TILES + ["direct"]
+    assert sweep.candidates("conv", 1000, 40, 9 * 48) == sweep.ENGINE_TILES            # co not a multiple of 32
+    assert sweep.candidates("conv", 1000, 64, 9 * 128) == sweep.ENGINE_TILES           # c_pad 128
+    assert set(sweep.ENGINE_TILES + sweep.SMALL_TILES + sweep.GEMV_TILES + sweep.SEG4_TILES + sweep.DIRECT_TILES) == \
         set(kernels.TILES) - {"auto"}

@@ -1568,7 +1568,7 @@ constexpr int T_AUTO = 0, T_256x256W8 = 1, T_256x256W4 = 2, T_256x128 = 3, T_128
               T_192x256 = 12, T_256x192 = 13, T_64x32 = 14, T_32x64 = 15, T_32x32 = 16, T_GEMV4 = 17,
               T_GEMV2 = 18, T_GEMV8 = 19, T_SEG4R2 = 20, T_SEG4R4 = 21, T_64x64K2 = 22, T_64x64K4 = 23,
               T_32x64K4 = 24, T_32x32K4 = 25, T_128x128K2 = 26, T_128x256W8 = 27, T_256x128W8 = 28,
-              T_256x256PP = 29, T_256x64 = 30, T_COUNT = 31;
+              T_256x256PP = 29, T_256x64 = 30, T_DIRECT = 31, T_COUNT = 32;
 
 static_assert(T_SMALL2 == T_SMALL1 + 1 && T_SMALL4 == T_SMALL1 + 2 && T_SMALL8 == T_SMALL1 + 3 &&
                   T_SMALL16 == T_SMALL1 + 4,
@@ -1578,6 +1578,12 @@ inline int small_waves(int t) { return 1 << (t - T_SMALL1); }
 inline bool is_gemv(int t) { return t >= T_GEMV4 && t <= T_GEMV8; }
 inline int gemv_waves(int t) { return t == T_GEMV2 ? 2 : t == T_GEMV8 ? 8 : 4; }
 inline bool is_seg4(int t) { return t == T_SEG4R2 || t == T_SEG4R4; }
+// T_DIRECT: the conv kernels with register operands (conv16_kernel for c_pad 16, convd_kernel for c_pad 32,
+// 48, 64), for co a multiple of 32 up to 128; a conv of K = 9 c_pad, N = co they take
+inline bool direct_ok(int64_t n, int64_t k) {
+  const int64_t c_pad = k / 9;
+  return k % 9 == 0 && (c_pad == 16 || c_pad == 32 || c_pad == 48 || c_pad == 64) && n % 32 == 0 && n <= 128;
+}
 
 inline TileCfg tile_cfg(int t) {
   switch (t) {
@@ -1672,8 +1678,11 @@ int rule_tile(int64_t M, int64_t N, int64_t kbytes, bool small_ok) {
 
 // kind / (m, n, k): the table key; kbytes: K as the engine counts it (bytes of an operand row).
 int choose_tile(int kind, int64_t m, int64_t n, int64_t k, int64_t kbytes) {
-  const int t = tile_lookup(kind, m, n, k);
-  return t != T_AUTO ? t : rule_tile(m, n, kbytes, kind != XDNA_KIND_CONV);
+  int t = tile_lookup(kind, m, n, k);
+  if (t == T_DIRECT && !(kind == XDNA_KIND_CONV && direct_ok(n, k))) t = T_AUTO;   // not a shape it takes
+  if (t != T_AUTO) return t;
+  if (kind == XDNA_KIND_CONV && direct_ok(n, k)) return T_DIRECT;
+  return rule_tile(m, n, kbytes, kind != XDNA_KIND_CONV);
 }
 
 // Buffer resources address at most 2 GB; larger operands are processed in row chunks.
@@ -1827,7 +1836,7 @@ struct TilePlan {
 // ktab: K as the table keys it (bf16 elements for the bf16 GEMM).
 TilePlan plan_tiles(int kind, int64_t M, int64_t N, int64_t kbytes, int64_t ktab, int tile) {
   const TilePlan one{tile, 0, T_AUTO};
-  if (is_small(tile) || is_gemv(tile) || is_seg4(tile)) return one;
+  if (is_small(tile) || is_gemv(tile) || is_seg4(tile) || tile == T_DIRECT) return one;
   const TileCfg t = tile_cfg(tile);
   const bool one_per_cu = t.kg == 1 && t.bm >= 128 && t.bn >= 128 && !(t.bm == 128 && t.bn == 128);
   if (!one_per_cu) return one;
@@ -1841,7 +1850,7 @@ TilePlan plan_tiles(int kind, int64_t M, int64_t N, int64_t kbytes, int64_t ktab
   // 256 x 256 tiles the 8-wave 128 x 256 tile, else the rule. C4 (1 x 256 x 1536 x 64) measured 79.8 us
   // unsplit, 72.7 us with a 128 x 128 tail (the rule's) and 69.4 us with the 128 x 256 one.
   int tail = tile_lookup(kind, M - m1, N, ktab);
-  if (is_small(tail) || is_gemv(tail) || is_seg4(tail)) tail = T_AUTO;
+  if (is_small(tail) || is_gemv(tail) || is_seg4(tail) || tail == T_DIRECT) tail = T_AUTO;
   if (tail == T_AUTO)
     tail = (tile == T_256x256W8 || tile == T_256x256PP) ? T_128x256W8 : rule_tile(M - m1, N, kbytes, false);
   // only when the leftover rows fit one round of the tail's tiles (8192 x 3072 in 256 x 256 tiles leaves
@@ -2322,28 +2331,26 @@ int launch_conv(const int8_t* x, int64_t nb, int64_t h, int64_t w, int64_t c_pad
     if (e.dq_out) eb.px0 = e.px0 + b0 * h * w;   // NCHW output: addressed by global pixel, not by row
     else eb = shift_epi(e, 1, b0 * h * w, 0);
     const int8_t* xb = x + b0 * per_img;
-    // 16-channel inputs: the register-only kernel where it takes the shape
-    if constexpr (EPI == EPI_REQUANT || EPI == EPI_CALIB) {
-      if (c_pad == 16) {
-        const int rc = launch_conv16<EPI>(xb, bc * h * w, h, w, wq, co, eb, st);
-        if (rc != XDNA_EUNSUPPORTED) {
-          if (rc) return rc;
-          continue;
-        }
-      } else if (c_pad <= 64) {
-        const int rc = launch_convd<EPI>(xb, bc * h * w, h, w, c_pad, wq, co, eb, st);
-        if (rc != XDNA_EUNSUPPORTED) {
-          if (rc) return rc;
-          continue;
-        }
+    // the direct kernels (register operands) for the shapes and epilogues they take, else the tile engine
+    // with the rule's tile (the fused dequantize, launches past their 32-bit sizes)
+    if (tile == T_DIRECT) {
+      int rc = XDNA_EUNSUPPORTED;
+      if constexpr (EPI == EPI_REQUANT || EPI == EPI_CALIB) {
+        rc = c_pad == 16 ? launch_conv16<EPI>(xb, bc * h * w, h, w, wq, co, eb, st)
+                         : launch_convd<EPI>(xb, bc * h * w, h, w, c_pad, wq, co, eb, st);
+      }
+      if (rc != XDNA_EUNSUPPORTED) {
+        if (rc) return rc;
+        continue;
       }
     }
+    const int etile = tile == T_DIRECT ? rule_tile(nb * h * w, co, K, false) : tile;
     // the haloed input tile where the tile allows it; the running tap counters of CONVM 1 step by KG
     // slices of 64 channels
-    const int mode = conv_mode(tile, h, w, c_pad);
-    int rc = mode == 3   ? launch_tiles<3, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st)
-             : mode == 1 ? launch_tiles<1, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st)
-                         : launch_tiles<2, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, tile, st);
+    const int mode = conv_mode(etile, h, w, c_pad);
+    int rc = mode == 3   ? launch_tiles<3, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, etile, st)
+             : mode == 1 ? launch_tiles<1, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, etile, st)
+                         : launch_tiles<2, EPI>(xb, c_pad, wq, K, bc * h * w, co, K, cg, eb, etile, st);
     if (rc) return rc;
   }
   return XDNA_OK;
@@ -2532,6 +2539,7 @@ int xdna_tile_set(int kind, int64_t m, int64_t n, int64_t k, int tile) {
   XDNA_REQUIRE(tile >= T_AUTO && tile < T_COUNT, "unknown tile id");
   XDNA_REQUIRE(!(kind == XDNA_KIND_CONV && (is_small(tile) || is_gemv(tile) || is_seg4(tile))),
                "the small-M, one-row and few-row kernels do not run convs");
+  XDNA_REQUIRE(!(kind != XDNA_KIND_CONV && tile == T_DIRECT), "the direct conv kernels run only convs");
   std::lock_guard<std::mutex> lock(g_tile_mu);
   const TileKey key{kind, m, n, k};
   if (tile == T_AUTO) g_tiles.erase(key);

@@ -196,12 +196,18 @@ def num_cus(dev) -> int:
 KIND_I8, KIND_BF16, KIND_CONV = 0, 1, 2          # XDNA_KIND_*
 KINDS = {"i8": KIND_I8, "bf16": KIND_BF16, "conv": KIND_CONV}
 # XDNA_TILE_* by id: the tile engine's workgroup tiles, the small-M kernel by waves, the one-row kernel,
-# the few-row kernel, tile-engine tiles with 2 or 4 K groups per workgroup
+# the few-row kernel, tile-engine tiles with 2 or 4 K groups per workgroup, and the direct conv kernels
 TILES = ("auto", "t256x256w8", "t256x256w4", "t256x128", "t128x256", "t128x128", "t64x64",
          "small_w1", "small_w2", "small_w4", "small_w8", "small_w16", "t192x256", "t256x192", "t64x32", "t32x64",
          "t32x32", "gemv_w4", "gemv_w2", "gemv_w8", "seg4_r2", "seg4_r4", "t64x64k2", "t64x64k4", "t32x64k4",
-         "t32x32k4", "t128x128k2", "t128x256w8", "t256x128w8", "t256x256pp", "t256x64")
+         "t32x32k4", "t128x128k2", "t128x256w8", "t256x128w8", "t256x256pp", "t256x64", "direct")
 TILE_ID = {name: i for i, name in enumerate(TILES)}
+
+
+def direct_ok(N, K) -> bool:
+    """Whether the direct conv kernels (tile "direct") take a conv of N = co, K = 9 c_pad: c_pad 16, 32, 48
+    or 64 and co a multiple of 32 up to 128, as the library's rule decides (xdna_mm.hip direct_ok)."""
+    return K % 9 == 0 and K // 9 in (16, 32, 48, 64) and N % 32 == 0 and N <= 128
 
 
 def tile_set(kind, M, N, K, tile):

@@ -44,12 +44,16 @@ ENGINE_TILES = [t for t in kernels.TILES if t.startswith("t")]
 SMALL_TILES = [t for t in kernels.TILES if t.startswith("small")]
 GEMV_TILES = [t for t in kernels.TILES if t.startswith("gemv")]
 SEG4_TILES = [t for t in kernels.TILES if t.startswith("seg4")]
+DIRECT_TILES = ["direct"]
 
 
-def candidates(kind, M):
-    """Tiles to try: every tile-engine shape; the small-M kernel's widths for up to 256 rows; the one-row
-    kernel's widths for one row; the few-row kernel's widths for up to 16 rows."""
-    if kind == "conv" or M > 256:
+def candidates(kind, M, N=None, K=None):
+    """Tiles to try: every tile-engine shape (and, for convs of N = co, K = 9 c_pad, the direct kernels
+    where they take the shape: kernels.direct_ok); the small-M kernel's widths for up to 256 rows; the
+    one-row kernel's widths for one row; the few-row kernel's widths for up to 16 rows."""
+    if kind == "conv":
+        return ENGINE_TILES + (DIRECT_TILES if N is None or kernels.direct_ok(N, K) else [])
+    if M > 256:
         return list(ENGINE_TILES)
     return ENGINE_TILES + SMALL_TILES + (GEMV_TILES if M == 1 else []) + (SEG4_TILES if M <= 16 else [])
 
@@ -168,7 +172,7 @@ def sweep_shape(kind, M, N, K, dev, case, done, out, tiles=None):
     ref_kind = "cpu"
     if want is None:               # too large for the CPU: the rule's tile is the reference
         want, ref_kind = exact(), "rule"
-    for tile in candidates(kind, M):
+    for tile in candidates(kind, M, N, K):
         if (kind, M, N, K, tile) in done or (tiles is not None and tile not in tiles):
             continue
         rec = {"kind": kind, "M": M, "N": N, "K": K, "tiling": tile, "rule": rule, "rule_plan": list(rule_plan),
