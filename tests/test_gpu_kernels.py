@@ -373,6 +373,31 @@ def test_conv_quant(gpu, dtype, n, ch, h, w, c_pad):
     assert np.array_equal(_np(sx), sx_r)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("ch,c_pad", [(3, 16), (40, 48)])
+def test_conv_quant_special(gpu, dtype, ch, c_pad):
+    """Non-finite images: an image with +inf (its scale inf), one with -inf, one with a NaN (its scale NaN,
+    as torch.amax propagates it) and a normal one. The reference's int8 cast of a NaN quotient is not defined
+    (numpy and torch's CPU cast give what the platform gives), so the narrow-image kernel is held to the
+    256-channel tile kernel on the same images bit for bit (scales NaN where NaN), and the normal image to
+    the oracle."""
+    from torch_xdna import kernels
+
+    x = _rand((4, ch, 8, 12), torch.float32, seed=ch, scale=2.0)
+    x[0, ch // 2, 3, 5] = float("inf")
+    x[1, 0, 7, 11] = float("-inf")
+    x[2, ch - 1, 0, 0] = float("nan")
+    x = x.to(DT[dtype]).to(gpu)
+    xq, sx = kernels.conv_quant(x, c_pad)              # the narrow-image kernel
+    xq_t, sx_t = kernels.conv_quant(x, 256)            # the 256-channel tile kernel
+    assert np.array_equal(_np(xq)[..., :ch], _np(xq_t)[..., :ch]) and not _np(xq)[..., ch:].any()
+    s1, s2 = _np(sx), _np(sx_t)
+    assert ((s1.view(np.uint32) == s2.view(np.uint32)) | (np.isnan(s1) & np.isnan(s2))).all()
+    assert np.isinf(s1[:2]).all() and np.isnan(s1[2])
+    xq_r, sx_r = O.conv_quant_images(x[3:].float().cpu().numpy())
+    assert np.array_equal(_np(xq)[3:, ..., :ch].transpose(0, 3, 1, 2), xq_r) and np.array_equal(s1[3:], sx_r)
+
+
 @pytest.mark.parametrize("n,ci,co,h,w", [(2, 3, 48, 13, 37), (1, 64, 128, 16, 64), (2, 16, 20, 5, 7),
                                          (1, 256, 256, 8, 64), (3, 40, 64, 9, 9),
                                          (1, 32, 256, 64, 256),      # larger tiles (every tile shape:
@@ -471,6 +496,35 @@ def test_conv_requant_next_wide_tiles(gpu, relu, n, co, h, w, c_pad, pool):
     """The same at sizes with at least two blocks of 1024 items per CU, where the wide kernels give each
     lane four items (the smaller cases above take one), with bias and the ReLU after it."""
     _check_requant_next(gpu, relu, pool, "f32", n, co, h, w, c_pad, ((True, True),))
+
+
+@pytest.mark.parametrize("relu_y", [False, True])
+@pytest.mark.parametrize("co,c_pad", [(64, 64), (20, 32)])
+def test_conv_requant_next_nan_image(gpu, relu_y, co, c_pad):
+    """An image whose input scale is NaN (a NaN somewhere in the layer's float input): its next scale is NaN,
+    as the reference's dequantize, ReLU (torch.relu keeps NaN) and amax give; the other images are unaffected
+    and equal the oracle. The integers of the NaN image are not compared: the reference's int8 cast of a NaN
+    quotient is not defined."""
+    from torch_xdna import kernels
+
+    g = torch.Generator().manual_seed(co)
+    q = torch.randint(-40, 40, (3, 9, 10, co), generator=g, dtype=torch.int8)
+    scale = torch.rand(co, generator=g) * 1e-3 + 1e-5
+    sx = torch.tensor([0.7, float("nan"), 0.3])
+    bias = torch.randn(co, generator=g) * 0.1
+    for pool in (False, True):
+        xq, sxn = kernels.conv_requant_next(q.to(gpu), False, pool, scale.to(gpu), sx.to(gpu), bias.to(gpu),
+                                            torch.float32, c_pad, relu_y=relu_y)
+        got_s = _np(sxn)
+        assert np.isnan(got_s[1]) and np.isfinite(got_s[[0, 2]]).all()
+        for i in (0, 2):
+            y = O.conv_dequant(_np(q[i:i + 1]).transpose(0, 3, 1, 2), scale.numpy(), sx[i:i + 1].numpy(), bias.numpy())
+            if relu_y:
+                y = np.maximum(y, 0)
+            if pool:
+                y = O.max_pool2(y)
+            xq_r, sx_r = O.conv_quant_images(y)
+            assert np.array_equal(_np(xq)[i:i + 1, ..., :co].transpose(0, 3, 1, 2), xq_r) and got_s[i] == sx_r[0]
 
 
 def _check_requant_next(gpu, relu, pool, x_dtype, n, co, h, w, c_pad, variants):

@@ -46,9 +46,26 @@ int launch_status(const char* where) {
 }
 
 // ------------------------------------------------------------------------------ quant_rows
+// The larger of two magnitudes (values with the sign bit clear: |x|, or maxima of them) as their bit
+// patterns order: a NaN (above +inf) wins, so it propagates as torch.amax propagates it (fmaxf would drop it).
+__device__ __forceinline__ float mag_max(float a, float b) {
+  return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
+}
+
+// Masks that keep the first `valid` bytes of a packed 16-byte group (0..16): padding channels read as 0.0 quantize
+// to 0 only while the scale is finite (0 * (1 / NaN) would give -127), so their bytes are cleared instead.
+__device__ __forceinline__ void valid_masks(int valid, uint32_t (&m)[4]) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int k = valid - 4 * g;
+    m[g] = k >= 4 ? 0xffffffffu : k <= 0 ? 0u : (0xffffffffu >> (32 - 8 * k));
+  }
+}
+
+// Max of the magnitudes v over the group's TPR threads (one wave, or the whole block through LDS); NaN wins.
 template <int TPR>
 __device__ __forceinline__ float group_max(float v, float* red) {
-  v = wave_max(v);
+  v = __int_as_float(wave_max_i(__float_as_int(v)));      // magnitudes order as their (non-negative) bits
   if constexpr (TPR == 64) {
     return v;
   } else {
@@ -59,7 +76,7 @@ __device__ __forceinline__ float group_max(float v, float* red) {
     __syncthreads();
     float m = red[0];
 #pragma unroll
-    for (int i = 1; i < W; ++i) m = fmaxf(m, red[i]);
+    for (int i = 1; i < W; ++i) m = mag_max(m, red[i]);
     return m;
   }
 }
@@ -348,7 +365,7 @@ __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(const void* __re
   const int64_t row = blockIdx.x;
   const int64_t base = row * ld_x;
   float amax = 0.0f;
-  for (int64_t i = threadIdx.x; i < k; i += 256) amax = fmaxf(amax, fabsf(load_as_f32<DT>(x, base + i)));
+  for (int64_t i = threadIdx.x; i < k; i += 256) amax = mag_max(amax, fabsf(load_as_f32<DT>(x, base + i)));
   amax = group_max<256>(amax, red);
   const float sc = scale_from_amax(amax);
   const float rc = 1.0f / sc;
@@ -505,7 +522,7 @@ __global__ __launch_bounds__(1024) void image_absmax_kernel(const void* __restri
     m = bits_to_abs<DT>(am.lane_bits());
   } else {
     for (int64_t i = (int64_t)blockIdx.x * 1024 + t; i < per; i += (int64_t)gridDim.x * 1024)
-      m = fmaxf(m, fabsf(load_as_f32<DT>(xb, i)));
+      m = mag_max(m, fabsf(load_as_f32<DT>(xb, i)));
   }
   m = group_max<1024>(m, red);
   if (t == 0) parts[b * AMAX_PARTS + blockIdx.x] = m;
@@ -549,6 +566,8 @@ __global__ __launch_bounds__(256) void conv_quant_nhwc_vec_kernel(const void* __
   const float sc = scale_from_amax(image_amax(parts, b, nparts, red));
   const float rc = 1.0f / sc;
   if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) sx[b] = sc;
+  uint32_t keep[4];
+  valid_masks((int)max<int64_t>(0, min<int64_t>(16, ch - (c0 + cl))), keep);
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
     float f[16];
@@ -556,7 +575,8 @@ __global__ __launch_bounds__(256) void conv_quant_nhwc_vec_kernel(const void* __
     for (int i = 0; i < 16; ++i) f[i] = v[i].get(j);
     uint32_t w[4];
     quant_pack<16>(f, sc, rc, w);
-    *reinterpret_cast<uint4*>(&tile[(pl + j) * 256 + (((cl >> 4) ^ (lane & 15)) << 4)]) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4*>(&tile[(pl + j) * 256 + (((cl >> 4) ^ (lane & 15)) << 4)]) =
+        make_uint4(w[0] & keep[0], w[1] & keep[1], w[2] & keep[2], w[3] & keep[3]);
   }
   __syncthreads();
 #pragma unroll
@@ -607,6 +627,8 @@ __global__ __launch_bounds__(256) void conv_quant_nhwc_narrow_kernel(const void*
       for (int i = 0; i < 16; ++i)
         v[i].raw = i < nc ? buf_load_u4<NT>(r, (uint32_t)(((16 * g + i) * hw + p) * ESZ)) : make_uint4(0, 0, 0, 0);
     }
+    uint32_t keep[4];
+    valid_masks(nc, keep);
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
       float f[16];
@@ -614,7 +636,9 @@ __global__ __launch_bounds__(256) void conv_quant_nhwc_narrow_kernel(const void*
       for (int i = 0; i < 16; ++i) f[i] = v[i].get(j);
       uint32_t w[4];
       quant_pack<16>(f, sc, rc, w);
-      if (p < hw) *reinterpret_cast<uint4*>(qp + j * c_pad + 16 * g) = make_uint4(w[0], w[1], w[2], w[3]);
+      if (p < hw)
+        *reinterpret_cast<uint4*>(qp + j * c_pad + 16 * g) =
+            make_uint4(w[0] & keep[0], w[1] & keep[1], w[2] & keep[2], w[3] & keep[3]);
     }
   }
 }
@@ -673,7 +697,7 @@ __global__ __launch_bounds__(256) void conv_weight_pack_kernel(const void* __res
   const int64_t per = ci * 9;
   const int64_t base = o * per;
   float m = 0.0f;
-  for (int64_t i = threadIdx.x; i < per; i += 256) m = fmaxf(m, fabsf(load_as_f32<DT>(w, base + i)));
+  for (int64_t i = threadIdx.x; i < per; i += 256) m = mag_max(m, fabsf(load_as_f32<DT>(w, base + i)));
   m = group_max<256>(m, red);
   const float sc = scale_from_amax(m);
   const float rc = 1.0f / sc;
@@ -914,7 +938,7 @@ template <int DT>
 __device__ __forceinline__ float chain_value(int q, float f, float bias, bool has_bias, int relu_y) {
   float t = (float)q * f;
   if (has_bias) t = t + bias;
-  if (relu_y) t = fmaxf(t, 0.0f);
+  if (relu_y) t = __builtin_elementwise_maximum(t, 0.0f);   // IEEE maximum: a NaN stays NaN, as torch.relu keeps it
   if constexpr (DT == XDNA_BF16) t = bf16_bits_to_f32(f32_to_bf16_bits(t));
   if constexpr (DT == XDNA_F16) t = f16_bits_to_f32(f32_to_f16_bits(t));
   return t;
@@ -1002,7 +1026,7 @@ __global__ __launch_bounds__(256) void conv_chain_wide_kernel(ChainArgs a, const
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         if (c0 + e < a.co)
-          m = fmaxf(m, fmaxf(fabsf(chain_value<DT>(hi[e], f[e], bv[e], has_bias, a.relu_y)),
+          m = mag_max(m, mag_max(fabsf(chain_value<DT>(hi[e], f[e], bv[e], has_bias, a.relu_y)),
                              fabsf(chain_value<DT>(lo[e], f[e], bv[e], has_bias, a.relu_y))));
     }
     m = group_max<256>(m, red);
@@ -1018,6 +1042,8 @@ __global__ __launch_bounds__(256) void conv_chain_wide_kernel(ChainArgs a, const
     const float rc = 1.0f / sc;
     if (blockIdx.x == 0 && threadIdx.x == 0) sx_next[b] = sc;
     chain_scale(a, c0, sxb, sr, f);
+    uint32_t keep[4];
+    valid_masks((int)min<uint32_t>(16u, a.co > c0 ? a.co - c0 : 0u), keep);
     int8_t* out = xq + (uint64_t)b * items * 16;
 #pragma unroll
     for (int k = 0; k < U; ++k) {
@@ -1030,7 +1056,9 @@ __global__ __launch_bounds__(256) void conv_chain_wide_kernel(ChainArgs a, const
       uint32_t wds[4];
       quant_pack<16>(v, sc, rc, wds);
       const uint32_t it = t0 + 64u * k;
-      if (it < items) *reinterpret_cast<uint4*>(out + (uint64_t)it * 16) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+      if (it < items)
+        *reinterpret_cast<uint4*>(out + (uint64_t)it * 16) =
+            make_uint4(wds[0] & keep[0], wds[1] & keep[1], wds[2] & keep[2], wds[3] & keep[3]);
     }
   }
 }
@@ -1066,7 +1094,7 @@ __global__ __launch_bounds__(256) void conv_chain_kernel(ChainArgs a, const floa
 #pragma unroll
         for (int e = 0; e < 16; ++e)
           if (c0 + e < a.co)
-            m = fmaxf(m, fmaxf(fabsf(chain_value<DT>(hi[e], f[e], bv[e], has_bias, a.relu_y)),
+            m = mag_max(m, mag_max(fabsf(chain_value<DT>(hi[e], f[e], bv[e], has_bias, a.relu_y)),
                                fabsf(chain_value<DT>(lo[e], f[e], bv[e], has_bias, a.relu_y))));
       }
     } else {
@@ -1076,7 +1104,7 @@ __global__ __launch_bounds__(256) void conv_chain_kernel(ChainArgs a, const floa
         chain_factors(a, c0, sxb, f, bv);
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          if (c0 + e < a.co) m = fmaxf(m, fabsf(chain_value<DT>(qv[e], f[e], bv[e], has_bias, a.relu_y)));
+          if (c0 + e < a.co) m = mag_max(m, fabsf(chain_value<DT>(qv[e], f[e], bv[e], has_bias, a.relu_y)));
       }
     }
     m = group_max<256>(m, red);
@@ -1094,10 +1122,11 @@ __global__ __launch_bounds__(256) void conv_chain_kernel(ChainArgs a, const floa
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         v[e] = c0 + e < a.co ? chain_value<DT>(qv[e], f[e], bv[e], has_bias, a.relu_y) : 0.0f;
-      uint32_t wds[4];
+      uint32_t wds[4], keep[4];
       quant_pack<16>(v, sc, rc, wds);
+      valid_masks((int)min<uint32_t>(16u, a.co > c0 ? a.co - c0 : 0u), keep);
       *reinterpret_cast<uint4*>(xq + (uint64_t)b * items * 16 + (uint64_t)item * 16) =
-          make_uint4(wds[0], wds[1], wds[2], wds[3]);
+          make_uint4(wds[0] & keep[0], wds[1] & keep[1], wds[2] & keep[2], wds[3] & keep[3]);
     }
   }
 }
