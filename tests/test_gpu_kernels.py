@@ -1010,12 +1010,15 @@ def test_sweep_tool(gpu, tile_table, tmp_path):
     out = str(tmp_path / "sweep.jsonl")
     sweep.main(["--kind", "i8", "--rows", "16", "300", "--shapes", "520x256", "--out", out])
     sweep.main(["--kind", "bf16", "--rows", "300", "--shapes", "520x256", "--out", out])
-    sweep.main(["--kind", "conv", "--convs", "2x48x40x13x37", "--out", out])
+    sweep.main(["--kind", "conv", "--convs", "2x48x40x13x37", "1x16x64x9x11", "--out", out])
     n_lines = sum(1 for _ in open(out))
     sweep.main(["--kind", "i8", "--rows", "16", "300", "--shapes", "520x256", "--out", out])   # resumed: no-op
     recs = [json.loads(line) for line in open(out)]
     want = len(sweep.candidates("i8", 16)) + len(sweep.candidates("i8", 300)) + \
-        len(sweep.candidates("bf16", 300)) + len(sweep.candidates("conv", 2 * 13 * 37, 40, 9 * 48))
+        len(sweep.candidates("bf16", 300)) + len(sweep.candidates("conv", 2 * 13 * 37, 40, 9 * 48)) + \
+        len(sweep.candidates("conv", 9 * 11, 64, 9 * 16))
+    assert any(r["tiling"] == "direct" and r["plan"][0] == "direct" for r in
+               (json.loads(line) for line in open(out)))       # the direct kernels swept where they run
     assert len(recs) == n_lines == want
     assert all(r["status"] == "ok" and r["exact"] and r["gpu_us"] > 0 for r in recs), recs
     assert {r["checked_against"] for r in recs} == {"cpu"}
