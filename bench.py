@@ -818,34 +818,37 @@ def bench_c3(a, dev):
     scales = [sw * 2.0 ** s for (wq, sw, _), s in zip(layers, shifts)]
 
     def step_parts(i, ct=None):
-        """Each layer as conv3x3_int8 alone: quantize, conv, dequantize to float32."""
+        """Each layer as conv3x3_int8 alone, the launches of the GPU op xdna::conv3x3_fused: quantize, then
+        the conv with its requantize and dequantize to float32 in one launch."""
         y = x
         for (wq, sw, _), s, sc in zip(layers, shifts, scales):
             xq, sx = kernels.conv_quant(y, c_pad)
-            q = ct(kernels.conv3x3, xq, wq, s, True) if ct else kernels.conv3x3(xq, wq, s, True)
-            y = kernels.conv_dequant(q, True, sc, sx, None, torch.float32)
+            y = kernels.conv3x3_dequant(xq, wq, s, True, sc, sx, None, torch.float32)
         return y
 
     def step(i, ct=None):
-        """The chained layers (xdna::conv3x3_chain): the activation stays NHWC int8 between convs."""
+        """The chained layers, the launches of xdna::conv3x3_chain on the GPU: the activation stays NHWC
+        int8 between convs, and the last conv dequantizes in its own launch."""
         xq, sx = kernels.conv_quant(x, c_pad)
         for j, ((wq, sw, _), s, sc) in enumerate(zip(layers, shifts, scales)):
+            if j == L - 1:
+                return kernels.conv3x3_dequant(xq, wq, s, True, sc, sx, None, torch.float32)
             q = ct(kernels.conv3x3, xq, wq, s, True) if ct else kernels.conv3x3(xq, wq, s, True)
-            if j < L - 1:
-                xq, sx = kernels.conv_requant_next(q, True, False, sc, sx, None, torch.float32, c_pad)
-            else:
-                y = kernels.conv_dequant(q, True, sc, sx, None, torch.float32)
-        return y
+            xq, sx = kernels.conv_requant_next(q, True, False, sc, sx, None, torch.float32, c_pad)
 
     if not torch.equal(step(0), step_parts(0)):
         raise SystemExit("chained and per-layer C3 outputs differ")
     sec_parts, _ = timed_steps(a, step_parts, None)
     sec, host = timed_steps(a, step, None)
-    # the dominant kernel alone: the step's four conv launches on their chained inputs, back to back
+    # the dominant kernel alone: the step's four conv launches on their chained inputs, back to back, as the
+    # step runs them (the last with its dequantize)
     convs, xq, sx = [], *kernels.conv_quant(x, c_pad)
     for j, ((wq, sw, _), s, sc) in enumerate(zip(layers, shifts, scales)):
-        convs.append(lambda xq=xq, wq=wq, s=s: kernels.conv3x3(xq, wq, s, True))
-        if j < L - 1:
+        if j == L - 1:
+            convs.append(lambda xq=xq, wq=wq, s=s, sc=sc, sx=sx: kernels.conv3x3_dequant(xq, wq, s, True, sc, sx,
+                                                                                          None, torch.float32))
+        else:
+            convs.append(lambda xq=xq, wq=wq, s=s: kernels.conv3x3(xq, wq, s, True))
             xq, sx = kernels.conv_requant_next(kernels.conv3x3(xq, wq, s, True), True, False, sc, sx, None,
                                                torch.float32, c_pad)
     conv_us = back_to_back_us(convs, L * a.steps)
